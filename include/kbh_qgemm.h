@@ -1,0 +1,73 @@
+/*
+ * kbh_qgemm.h — C ABI of the MI355X (gfx950) quantized-GEMM operator library.
+ *
+ * Every entry point enqueues work on the caller's HIP stream and returns a status code; none
+ * allocates or frees device memory and none synchronises the host. Pointers are device
+ * pointers to contiguous row-major buffers. `stream` is a hipStream_t passed as void* so that
+ * this header needs no HIP include (NULL = the default stream).
+ *
+ * dtype codes: KBH_F16 = 0 (IEEE binary16), KBH_BF16 = 1 (bfloat16).
+ *
+ * The reference "interface" each entry point replaces is the PyTorch Model.forward of the
+ * kernelbench-harbor task family named in its comment (path relative to the reference checkout).
+ */
+#ifndef KBH_QGEMM_H
+#define KBH_QGEMM_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define KBH_ABI_VERSION 1
+
+enum kbh_dtype { KBH_F16 = 0, KBH_BF16 = 1 };
+
+enum kbh_status {
+  KBH_OK = 0,
+  KBH_ERR_NULL = 1,          /* a required pointer is NULL */
+  KBH_ERR_SHAPE = 2,         /* shape not supported (divisibility / range) */
+  KBH_ERR_DTYPE = 3,         /* dtype code not supported */
+  KBH_ERR_WORKSPACE = 4,     /* workspace NULL or smaller than *_workspace_bytes() */
+  KBH_ERR_ALIGN = 5,         /* pointer not aligned as the kernel requires (16 B) */
+  KBH_ERR_LAUNCH = 6         /* the HIP runtime refused the launch (see kbh_last_hip_error) */
+};
+
+/* Library version of this ABI (KBH_ABI_VERSION). */
+int kbh_abi_version(void);
+
+/* Human-readable text for a kbh_status value. */
+const char* kbh_status_string(int status);
+
+/* hipError_t of the most recent failed launch in this process (0 if none). */
+int kbh_last_hip_error(void);
+
+/* ---------------------------------------------------------------------------------------
+ * W4A16 packed-asymmetric group-quantized GEMM.
+ * Replaces tasks/quant_w4a16_pa/quant_w4a16_pa__llama3_8b_down__g128__fp16/environment/
+ * reference.py:10-17 (Model.forward(x, qweight, scales, zeros)); template generate_tasks.py:45-74.
+ *
+ *   x       [M, K]    dtype
+ *   qweight [K, N/8]  int32, nibble i (bits 4i..4i+3) of word [k, j] is column 8j+i
+ *   scales  [K/group, N] dtype
+ *   zeros   [K/group, N] dtype (integer values 0..15)
+ *   y       [M, N]    dtype,  y = x @ ((unpack(qweight) - zeros) * scales)
+ *
+ * Requirements: M >= 1, N % 128 == 0, group in {32, 64, 128, 256}, K % group == 0,
+ * x/qweight/scales/zeros/y 16-byte aligned.
+ * workspace: >= kbh_w4a16_workspace_bytes(M, N, K, group) bytes, zero-filled before its first
+ * use; every call leaves it zero-filled again. Calls that share a workspace must be ordered
+ * (same stream); concurrent calls on one workspace race.
+ */
+size_t kbh_w4a16_workspace_bytes(int M, int N, int K, int group);
+int kbh_w4a16_gemm(const void* x, const int32_t* qweight, const void* scales, const void* zeros,
+                   void* y, void* workspace, size_t workspace_bytes,
+                   int M, int N, int K, int group, int dtype, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* KBH_QGEMM_H */

@@ -1,0 +1,9 @@
+"""MI355X (gfx950) quantized-GEMM operators behind the kernelbench-harbor task interface.
+
+The compute lives in hand-written HIP kernels compiled into ``lib/libkbh_qgemm.so`` (C ABI in
+``include/kbh_qgemm.h``); this package holds the ctypes binding, host-side validation and the
+drop-in ``nn.Module`` classes.
+"""
+from .modules import W4A16Model  # noqa: F401
+
+__all__ = ["W4A16Model"]

@@ -1,0 +1,89 @@
+// Shared device/host helpers for the gfx950 (CDNA4) quantized-GEMM kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "kbh_qgemm.h"
+
+typedef _Float16 kbh_f16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 kbh_bf16x8 __attribute__((ext_vector_type(8)));
+typedef float kbh_f32x4 __attribute__((ext_vector_type(4)));
+typedef float kbh_f32x16 __attribute__((ext_vector_type(16)));
+typedef int kbh_i32x4 __attribute__((ext_vector_type(4)));
+typedef int kbh_i32x8 __attribute__((ext_vector_type(8)));
+typedef int kbh_i32x16 __attribute__((ext_vector_type(16)));
+typedef uint32_t kbh_u32x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t kbh_u32x4 __attribute__((ext_vector_type(4)));
+
+namespace kbh {
+
+// Records the HIP error of the last failed launch (read back through kbh_last_hip_error).
+void set_last_hip_error(int e);
+
+// Translates hipGetLastError() after a launch into a kbh_status.
+int launch_status();
+
+inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+inline size_t round_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
+
+// ---- device helpers -------------------------------------------------------------------
+
+// Workgroups of one launch are dealt to the 8 XCDs round-robin (linear id % 8). Remapping the
+// linear id so that each XCD receives one contiguous range of logical ids keeps the tiles that
+// share cache lines, or that reduce into the same output tile, inside one XCD's L2.
+__device__ inline int xcd_remap(int bid, int nblocks) {
+  if ((nblocks & 7) != 0) return bid;
+  return (bid & 7) * (nblocks >> 3) + (bid >> 3);
+}
+
+// 16x16x32 MFMA, fp16 or bf16 operands (8 values per lane, packed in 4 dwords), fp32 accumulate.
+// Lane l holds A[row l%16][k 8(l/16)..+8] and B[k 8(l/16)..+8][col l%16]; C lane l holds
+// C[4(l/16)+i][l%16], i = 0..3.
+template <bool BF16>
+__device__ inline kbh_f32x4 mfma16x16x32(kbh_u32x4 a, kbh_u32x4 b, kbh_f32x4 c) {
+  if constexpr (BF16) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(kbh_bf16x8, a),
+                                                   __builtin_bit_cast(kbh_bf16x8, b), c, 0, 0, 0);
+  } else {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(kbh_f16x8, a),
+                                                  __builtin_bit_cast(kbh_f16x8, b), c, 0, 0, 0);
+  }
+}
+
+// 32x32x16 MFMA (fp16/bf16). Lane l holds A[row l%32][k 8(l/32)..+8], B[k 8(l/32)..+8][col l%32];
+// C lane l holds C[8(i/4) + 4(l/32) + i%4][l%32], i = 0..15.
+template <bool BF16>
+__device__ inline kbh_f32x16 mfma32x32x16(kbh_u32x4 a, kbh_u32x4 b, kbh_f32x16 c) {
+  if constexpr (BF16) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(kbh_bf16x8, a),
+                                                   __builtin_bit_cast(kbh_bf16x8, b), c, 0, 0, 0);
+  } else {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(kbh_f16x8, a),
+                                                  __builtin_bit_cast(kbh_f16x8, b), c, 0, 0, 0);
+  }
+}
+
+// fp16 / bf16 bit patterns <-> fp32.
+__device__ inline float f16_bits_to_f32(uint16_t h) { return (float)__builtin_bit_cast(_Float16, h); }
+__device__ inline float bf16_bits_to_f32(uint16_t h) { return __builtin_bit_cast(float, (uint32_t)h << 16); }
+template <bool BF16>
+__device__ inline float half_bits_to_f32(uint16_t h) {
+  if constexpr (BF16) return bf16_bits_to_f32(h); else return f16_bits_to_f32(h);
+}
+
+// fp32 -> fp16 / bf16 with round-to-nearest-even (NaN is kept quiet).
+__device__ inline uint16_t f32_to_f16_bits(float f) { return __builtin_bit_cast(uint16_t, (_Float16)f); }
+__device__ inline uint16_t f32_to_bf16_bits(float f) {
+  uint32_t u = __builtin_bit_cast(uint32_t, f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+template <bool BF16>
+__device__ inline uint16_t f32_to_half_bits(float f) {
+  if constexpr (BF16) return f32_to_bf16_bits(f); else return f32_to_f16_bits(f);
+}
+
+}  // namespace kbh

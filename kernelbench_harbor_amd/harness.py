@@ -1,0 +1,151 @@
+"""Grading and timing protocol for the drop-in modules.
+
+Restates the reference grader common/kb_verifier.py:
+  * correctness: the candidate's output, compared as fp32 against an fp32 ground truth over
+    several input draws (kb_verifier.py:192-205), with the reference's allclose(atol=rtol=2e-2)
+    (kb_verifier.py:148-149,177) reported next to the benchmark gate max|err| <= 2e-2*max|gt|
+    and relative Frobenius error <= 5e-3. The ground truth is always compared as fp32
+    (kb_verifier.py:177 compares fp32 against the W8A8 reference's fp16 output and raises);
+  * timing: median of `iters` event-timed calls after `warmup` calls (kb_verifier.py:132-143),
+    with an optional rotation over several input sets so that weights are not cache-resident;
+  * static check (kb_verifier.py:71-120): the same banned torch ops, with "has @triton.jit"
+    replaced by "calls into the HIP library" (this package bans Triton).
+The ground-truth callable is supplied by the caller: this module never computes one.
+"""
+from __future__ import annotations
+
+import ast
+import math
+from dataclasses import dataclass, field
+
+import torch
+
+MAX_ABS_FRAC = 2e-2
+REL_FRO = 5e-3
+REF_ATOL = 2e-2
+REF_RTOL = 2e-2
+
+# kb_verifier.py:47-54
+BANNED_ATTRS = {"matmul", "mm", "bmm", "addmm", "einsum", "softmax", "linear",
+                "scaled_dot_product_attention", "sdpa", "conv1d", "conv2d", "conv3d"}
+BANNED_NAMES = {"scaled_dot_product_attention", "sdpa"}
+BANNED_IMPORTS = {"flash_attn", "xformers", "triton"}
+
+
+@dataclass
+class Comparison:
+    max_abs_err: float
+    max_abs_ref: float
+    max_abs_frac: float
+    rel_fro: float
+    allclose_ref: bool
+    finite: bool
+
+    @property
+    def ok(self) -> bool:
+        return self.finite and self.max_abs_frac <= MAX_ABS_FRAC and self.rel_fro <= REL_FRO
+
+    def as_dict(self) -> dict:
+        return {"max_abs_err": self.max_abs_err, "max_abs_frac": self.max_abs_frac,
+                "rel_fro": self.rel_fro, "allclose_2e-2": self.allclose_ref, "ok": self.ok}
+
+
+def compare(y, gt) -> Comparison:
+    """Compares an output (any float dtype, any device) against an fp32 ground truth."""
+    y = torch.as_tensor(y).detach().float().cpu()
+    gt = torch.as_tensor(gt).detach().float().cpu()
+    if y.shape != gt.shape:
+        raise ValueError(f"shape mismatch {tuple(y.shape)} vs {tuple(gt.shape)}")
+    finite = bool(torch.isfinite(y).all())
+    d = (y.double() - gt.double())
+    max_err = float(d.abs().max()) if d.numel() else 0.0
+    max_ref = float(gt.abs().max()) if gt.numel() else 0.0
+    fro_ref = float(gt.double().norm())
+    rel = float(d.norm()) / fro_ref if fro_ref > 0 else float(d.norm())
+    frac = max_err / max_ref if max_ref > 0 else max_err
+    allc = bool(torch.allclose(y, gt, atol=REF_ATOL, rtol=REF_RTOL))
+    return Comparison(max_err, max_ref, frac, rel, allc, finite)
+
+
+def static_check(src: str) -> tuple[bool, str]:
+    """kb_verifier.py:71-120 with the Triton requirement replaced: the module must call into
+    this package (the HIP library) and must not offload the core compute to torch."""
+    tree = ast.parse(src)
+    uses_lib = False
+    for node in ast.walk(tree):
+        if isinstance(node, ast.Import):
+            for a in node.names:
+                root = a.name.split(".")[0]
+                if root in BANNED_IMPORTS:
+                    return False, f"banned import: {a.name}"
+                uses_lib |= root == "kernelbench_harbor_amd"
+        elif isinstance(node, ast.ImportFrom):
+            root = (node.module or "").split(".")[0]
+            if root in BANNED_IMPORTS:
+                return False, f"banned import: {node.module}"
+            uses_lib |= root == "kernelbench_harbor_amd" or (node.level > 0)
+        elif isinstance(node, ast.Attribute) and node.attr in BANNED_ATTRS:
+            return False, f"banned op (offloads core compute): .{node.attr}"
+        elif isinstance(node, ast.Name) and node.id in BANNED_NAMES:
+            return False, f"banned op (offloads core compute): {node.id}"
+    if not uses_lib:
+        return False, "does not call into the HIP library"
+    return True, "ok"
+
+
+def bench(fn, warmup: int = 25, iters: int = 100, rotate: int = 1) -> list[float]:
+    """Event-timed calls on the current stream (kb_verifier.py:132-143): returns the sorted
+    per-call times in ms. fn(i) receives the call index so callers can rotate input sets."""
+    for i in range(warmup):
+        fn(i % rotate)
+    torch.cuda.synchronize()
+    s = torch.cuda.Event(enable_timing=True)
+    e = torch.cuda.Event(enable_timing=True)
+    ts = []
+    for i in range(iters):
+        s.record()
+        fn(i % rotate)
+        e.record()
+        torch.cuda.synchronize()
+        ts.append(s.elapsed_time(e))
+    return sorted(ts)
+
+
+def median(ts: list[float]) -> float:
+    return ts[len(ts) // 2]
+
+
+@dataclass
+class GradeResult:
+    correct: bool = False
+    draws: list = field(default_factory=list)
+    error: str | None = None
+
+
+def grade(module, get_inputs, ground_truth, draws: int = 5) -> GradeResult:
+    """Correctness over `draws` input draws (kb_verifier.py:192-205). get_inputs(i) returns the
+    device inputs of draw i; ground_truth(inputs) returns the fp32 ground truth."""
+    out = GradeResult()
+    try:
+        ok = True
+        for i in range(draws):
+            inputs = get_inputs(i)
+            y = module(*inputs)
+            gt = ground_truth(inputs)
+            cmp = compare(y, gt)
+            out.draws.append(cmp.as_dict())
+            ok &= cmp.ok
+        out.correct = ok
+    except Exception as exc:  # recorded like kb_verifier.py:223-225, then returned
+        out.error = f"{type(exc).__name__}: {exc}"
+        out.correct = False
+    return out
+
+
+def roofline_frac(seconds: float, bytes_: float, flops: float, hbm_bps: float,
+                  peak_flops: float) -> tuple[str, float]:
+    """(bound, floor/time) with floor = max(bytes/BW, flops/peak)."""
+    t_mem = bytes_ / hbm_bps
+    t_cmp = flops / peak_flops
+    bound = "hbm" if t_mem >= t_cmp else "mfma"
+    return bound, (max(t_mem, t_cmp) / seconds) if seconds > 0 else math.nan

@@ -1,0 +1,99 @@
+"""Host side of the quantized-GEMM ops: argument validation, workspace management and the call
+into the C ABI on torch's current HIP stream.
+
+Each function mirrors the math of one reference ``Model.forward`` (cited per function); the
+arithmetic itself always runs in the HIP library — there is no CPU or torch fallback.
+"""
+from __future__ import annotations
+
+import threading
+
+import torch
+
+from . import _lib
+
+_DT_CODE = {torch.float16: _lib.KBH_F16, torch.bfloat16: _lib.KBH_BF16}
+
+
+class _WorkspacePool:
+    """Zero-filled device scratch per (device, stream), grown on demand.
+
+    The kernels leave the workspace zero-filled after every call, so one buffer serves every
+    call that is ordered on the same stream.
+    """
+
+    def __init__(self):
+        self._bufs: dict[tuple[int, int], torch.Tensor] = {}
+        self._lock = threading.Lock()
+
+    def get(self, nbytes: int, device: torch.device) -> torch.Tensor:
+        stream = torch.cuda.current_stream(device).cuda_stream
+        key = (device.index if device.index is not None else torch.cuda.current_device(), stream)
+        with self._lock:
+            buf = self._bufs.get(key)
+            if buf is None or buf.numel() < nbytes:
+                buf = torch.zeros(max(nbytes, 256), dtype=torch.uint8, device=device)
+                self._bufs[key] = buf
+            return buf
+
+
+workspaces = _WorkspacePool()
+
+
+def _require(cond: bool, msg: str) -> None:
+    if not cond:
+        raise ValueError(msg)
+
+
+def _stream_ptr(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def _check_device(*tensors: torch.Tensor) -> torch.device:
+    dev = tensors[0].device
+    _require(dev.type == "cuda", f"tensors must be on a HIP device, got {dev}")
+    for t in tensors[1:]:
+        _require(t.device == dev, f"all tensors must be on {dev}, got {t.device}")
+    return dev
+
+
+def w4a16_gemm(x: torch.Tensor, qweight: torch.Tensor, scales: torch.Tensor,
+               zeros: torch.Tensor) -> torch.Tensor:
+    """y = x @ ((unpack(qweight) - zeros) * scales), the packed-asymmetric W4A16 linear.
+
+    Follows tasks/quant_w4a16_pa/quant_w4a16_pa__llama3_8b_down__g128__fp16/environment/
+    reference.py:10-17: qweight [K, N/8] int32 with nibble i of word [k, j] = column 8j+i,
+    scales/zeros [K/G, N] in x.dtype; the group size G is K / scales.shape[0].
+    """
+    _require(x.dtype in _DT_CODE, f"x must be float16 or bfloat16, got {x.dtype}")
+    _require(qweight.dtype == torch.int32, f"qweight must be int32, got {qweight.dtype}")
+    _require(qweight.dim() == 2 and scales.dim() == 2 and zeros.dim() == 2,
+             "qweight, scales and zeros must be 2-D")
+    K, NP = qweight.shape
+    N = NP * 8
+    _require(x.shape[-1] == K, f"x last dim {x.shape[-1]} != qweight rows {K}")
+    _require(scales.shape[1] == N and zeros.shape == scales.shape,
+             f"scales/zeros must be [K/G, {N}], got {tuple(scales.shape)} / {tuple(zeros.shape)}")
+    _require(scales.shape[0] > 0 and K % scales.shape[0] == 0,
+             f"K={K} not divisible by scales rows {scales.shape[0]}")
+    group = K // scales.shape[0]
+    _require(scales.dtype == x.dtype and zeros.dtype == x.dtype,
+             "scales and zeros must have x's dtype")
+    dev = _check_device(x, qweight, scales, zeros)
+    lead = x.shape[:-1]
+    x2 = x.reshape(-1, K).contiguous()
+    M = x2.shape[0]
+    y = torch.empty((M, N), dtype=x.dtype, device=dev)
+    if M == 0:
+        return y.reshape(*lead, N)
+    qweight = qweight.contiguous()
+    scales = scales.contiguous()
+    zeros = zeros.contiguous()
+    lib = _lib.load()
+    nbytes = lib.kbh_w4a16_workspace_bytes(M, N, K, group)
+    ws = workspaces.get(nbytes, dev)
+    st = lib.kbh_w4a16_gemm(x2.data_ptr(), qweight.data_ptr(), scales.data_ptr(),
+                            zeros.data_ptr(), y.data_ptr(), ws.data_ptr(), ws.numel(),
+                            M, N, K, group, _DT_CODE[x.dtype], _stream_ptr(dev))
+    _lib.check(st, "kbh_w4a16_gemm")
+    return y.reshape(*lead, N)
