@@ -1,0 +1,53 @@
+"""Summarises a ``rocprofv3 --kernel-trace -f csv`` trace per (kernel, grid, workgroup size).
+
+    python -m kernelbench_harbor_amd.rocprof_summary <prefix>_kernel_trace.csv [--match SUBSTR]
+
+Launches of one kernel symbol with different grids (for example the W4A16 kernel at several
+M) are reported separately, so the average duration of one configuration can be compared with
+the HIP-event figure bench.py reports for it.
+"""
+from __future__ import annotations
+
+import argparse
+import csv
+import statistics
+
+
+def summarize(path: str, match: str | None = None) -> list[dict]:
+    groups: dict[tuple, list[float]] = {}
+    with open(path, newline="") as f:
+        for r in csv.DictReader(f):
+            name = r["Kernel_Name"]
+            if match and match not in name:
+                continue
+            key = (name, int(r["Grid_Size_X"]), int(r.get("Grid_Size_Y") or 1),
+                   int(r["Workgroup_Size_X"]))
+            dur_us = (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1000.0
+            groups.setdefault(key, []).append(dur_us)
+    out = []
+    for (name, gx, gy, wg), ds in groups.items():
+        ds.sort()
+        out.append({"kernel": name, "grid_threads": (gx, gy), "workgroup": wg, "calls": len(ds),
+                    "avg_us": statistics.fmean(ds), "median_us": ds[len(ds) // 2],
+                    "min_us": ds[0], "max_us": ds[-1]})
+    return out
+
+
+def main() -> None:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("trace")
+    ap.add_argument("--match", default=None)
+    a = ap.parse_args()
+    rows = summarize(a.trace, a.match)
+    print("| kernel | grid (threads x,y) | wg | calls | avg us | median us | min us | max us |")
+    print("|---|---|---|---|---|---|---|---|")
+    for r in rows:
+        short = r["kernel"].replace("(anonymous namespace)::", "").replace("void ", "")
+        short = short.split("(")[0]
+        print(f"| `{short}` | {r['grid_threads'][0]}x{r['grid_threads'][1]} | {r['workgroup']} | "
+              f"{r['calls']} | {r['avg_us']:.2f} | {r['median_us']:.2f} | {r['min_us']:.2f} | "
+              f"{r['max_us']:.2f} |")
+
+
+if __name__ == "__main__":
+    main()

@@ -31,6 +31,13 @@ CASES = [
     (16, 2048, 512, 128, torch.bfloat16, "baseline"),
     (5, 1024, 384, 64, torch.bfloat16, "reference"),
     (40, 1024, 256, 128, torch.bfloat16, "baseline"),
+    # tiled (large-M) path
+    (128, 1024, 128, 32, torch.float16, "baseline"),
+    (256, 2048, 512, 128, torch.float16, "baseline"),
+    (300, 1024, 384, 64, torch.bfloat16, "reference"),
+    (513, 4096, 256, 128, torch.float16, "reference"),
+    # K not a multiple of 64 -> split-K path even for large M
+    (96, 1056, 256, 32, torch.float16, "baseline"),
 ]
 
 
@@ -54,22 +61,35 @@ def test_w4a16_full_size_decode(dev, M):
     assert cmp.ok, cmp
 
 
+@pytest.mark.parametrize("M", [16, 64])
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
-def test_w4a16_unpack_bit_exact(dev, dtype):
-    """One-hot activations with scale 1 and zero z select single weight rows: y[m, :] equals
-    unpack(qweight)[k_m, :] - z exactly (integers <= 15 are exact in fp16/bf16/fp32)."""
-    M, K, N, G = 16, 4096, 512, 128
-    g = torch.Generator().manual_seed(7)
+def test_w4a16_dequant_bit_exact(dev, dtype, M):
+    """One-hot activations select single weight rows, so y[m, :] is the dequantized row
+    k_m rounded once to the output dtype: it must equal the reference's own dequantization
+    (unpack, subtract zero, multiply by scale, one rounding) bit for bit. M=16 exercises the
+    split-K decode kernel, M=64 the tiled kernel."""
+    K, N, G = 4096, 512, 128
+    g = torch.Generator().manual_seed(7 + M)
     qw = inputs.random_packed_int4(K, N, g)
     ks = torch.randperm(K, generator=g)[:M]
     x = torch.zeros(M, K, dtype=dtype)
     x[torch.arange(M), ks] = 1.0
-    s = torch.ones(K // G, N, dtype=dtype)
+    s = (torch.randn(K // G, N, generator=g) * 0.01).to(dtype)
     z = torch.randint(0, 16, (K // G, N), generator=g).to(dtype)
     y = ops.w4a16_gemm(x.to(dev), qw.to(dev), s.to(dev), z.to(dev)).float().cpu().numpy()
-    nib = ow.unpack_int4_along_n(qw.numpy()).astype(np.float32)
-    want = nib[ks.numpy()] - z.float().numpy()[ks.numpy() // G]
-    assert np.array_equal(y, want)
+    dt = "f16" if dtype == torch.float16 else "bf16"
+    W = ow.dequant(qw.numpy(), s.float().numpy(), z.float().numpy(), dt)
+    want = W[ks.numpy()]
+    assert np.array_equal(y, want), np.abs(y - want).max()
+
+
+def test_w4a16_full_size_prefill(dev):
+    """BASELINE config 1 largest point: M=2048, K=14336, N=4096."""
+    print("[w4a16 full] M=2048", flush=True)
+    x, qw, s, z = inputs.w4a16(2048, 14336, 4096, 128, torch.float16, seed=5)
+    y = W4A16Model()(x.to(dev), qw.to(dev), s.to(dev), z.to(dev))
+    cmp = compare(y, _gt(x, qw, s, z))
+    assert cmp.ok, cmp
 
 
 def test_w4a16_workspace_left_clean_and_repeatable(dev):
