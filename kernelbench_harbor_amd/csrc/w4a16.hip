@@ -26,8 +26,9 @@
 //    on one XCD.
 //
 // w4a16_tiled_kernel (larger M; MFMA-bound)
-//  * 256x128 output tile per 256-thread workgroup, K in 64-row slabs, two LDS stages. x rows are
-//    staged in LDS as is; packed weights are dequantized on the way into LDS with the exact
+//  * 256x128 output tile per 256-thread workgroup, K in 32-row slabs held in a register ring
+//    three slabs ahead of the MFMAs, two LDS stages, one barrier per slab. x rows are staged in
+//    LDS as is; packed weights are dequantized on the way into LDS with the exact
 //    reference arithmetic ((q - z) in the input dtype, times s, one rounding), stored k-major
 //    per column so that both MFMA operands are 16-byte LDS reads. 2x2 waves, each 128x64 with
 //    32x32x16 MFMAs. XCD remapping gives each XCD whole rows of tiles (shared x rows in L2).
@@ -64,7 +65,10 @@ __device__ inline uint32_t pair_bytes_rt(uint32_t wa, uint32_t wb, int j) {
 constexpr int kDecodeMaxWaves = 8;
 constexpr int kCsStride = 260;  // LDS floats per MFMA column set per wave (4*64 + pad)
 
-template <int NW, int SPW, bool BF16>
+// SPG = K steps per quantization group when a group is shorter than a wave's K range
+// (SPG < SPW), otherwise SPG == SPW (each wave lies inside one group). The fold schedule is thus
+// static, and the scales/zeros of every group a wave touches are loaded with its weights.
+template <int NW, int SPW, int SPG, bool BF16>
 __global__ __launch_bounds__(kDecodeMaxWaves * 64) void w4a16_decode_kernel(
     const uint16_t* __restrict__ x, const uint32_t* __restrict__ qw,
     const uint16_t* __restrict__ scales, const uint16_t* __restrict__ zeros,
@@ -115,6 +119,18 @@ __global__ __launch_bounds__(kDecodeMaxWaves * 64) void w4a16_decode_kernel(
     const kbh_u32x4 v = *reinterpret_cast<const kbh_u32x4*>(xb + u * 32);
     af[u] = xok ? v : kbh_u32x4{0u, 0u, 0u, 0u};
   }
+  constexpr int NG = SPW / SPG;  // quantization groups touched by this wave
+  kbh_u32x4 sv[NG][NW], zv[NG][NW];
+#pragma unroll
+  for (int gq = 0; gq < NG; ++gq) {
+    const int gi = ((st0 + gq * SPG) << 5) / group;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) {
+      const size_t off = (size_t)gi * N + n0 + 8 * (c * NW + w);
+      sv[gq][w] = *reinterpret_cast<const kbh_u32x4*>(scales + off);
+      zv[gq][w] = *reinterpret_cast<const kbh_u32x4*>(zeros + off);
+    }
+  }
 
   const uint32_t one = BF16 ? kOneBF16 : kOneF16;
   const kbh_u32x4 ones = {one, one, one, one};
@@ -124,7 +140,6 @@ __global__ __launch_bounds__(kDecodeMaxWaves * 64) void w4a16_decode_kernel(
     tot[cs] = kbh_f32x4{0.f, 0.f, 0.f, 0.f};
     part[cs] = tot[cs];
   }
-  const int spg = group >> 5;
 #pragma unroll
   for (int u = 0; u < SPW; ++u) {
     xs = mfma16x16x32<BF16>(af[u], ones, xs);
@@ -143,19 +158,16 @@ __global__ __launch_bounds__(kDecodeMaxWaves * 64) void w4a16_decode_kernel(
         part[w * 8 + 2 * j + 1] = mfma16x16x32<BF16>(af[u], bhi, part[w * 8 + 2 * j + 1]);
       }
     }
-    const int st = st0 + u;
-    // Fold at the end of a quantization group or of this wave's K range.
-    if (((st + 1) % spg) == 0 || u == SPW - 1) {
-      const int gi = (st << 5) / group;
+    // Fold at the end of each quantization group (static schedule).
+    if ((u + 1) % SPG == 0) {
+      const int gq = u / SPG;
 #pragma unroll
       for (int w = 0; w < NW; ++w) {
-        const size_t off = (size_t)gi * N + n0 + 8 * (c * NW + w);
-        const kbh_u32x4 sv = *reinterpret_cast<const kbh_u32x4*>(scales + off);
-        const kbh_u32x4 zv = *reinterpret_cast<const kbh_u32x4*>(zeros + off);
 #pragma unroll
         for (int nib = 0; nib < 8; ++nib) {
-          const uint16_t sh = (uint16_t)((nib & 1) ? (sv[nib >> 1] >> 16) : (sv[nib >> 1] & 0xffffu));
-          const uint16_t zh = (uint16_t)((nib & 1) ? (zv[nib >> 1] >> 16) : (zv[nib >> 1] & 0xffffu));
+          const uint32_t sw = sv[gq][w][nib >> 1], zw = zv[gq][w][nib >> 1];
+          const uint16_t sh = (uint16_t)((nib & 1) ? (sw >> 16) : (sw & 0xffffu));
+          const uint16_t zh = (uint16_t)((nib & 1) ? (zw >> 16) : (zw & 0xffffu));
           const float s = half_bits_to_f32<BF16>(sh);
           const float z = half_bits_to_f32<BF16>(zh);
           const float a = (!BF16 && (nib & 1)) ? 0.0625f : 1.0f;
@@ -229,17 +241,21 @@ __global__ __launch_bounds__(kDecodeMaxWaves * 64) void w4a16_decode_kernel(
 }
 
 struct DecodePlan {
-  int nw, spw, waves, ntiles, splits, mblocks;
+  int nw, spw, spg, waves, ntiles, splits, mblocks;
 };
 
 // Chooses column width (NW), K steps per wave (SPW) and waves per workgroup so that the K steps
 // divide evenly and the grid is close to one workgroup per CU (256).
-bool plan_decode(int M, int N, int K, DecodePlan* p) {
+bool plan_decode(int M, int N, int K, int group_steps_, DecodePlan* p) {
   const int nsteps = K / 32;
   p->nw = (N % 256 == 0) ? 2 : 1;
   p->ntiles = N / (128 * p->nw);
   p->mblocks = (M + 15) / 16;
   p->spw = (nsteps % 4 == 0) ? 4 : (nsteps % 2 == 0 ? 2 : 1);
+  // Wave ranges start at multiples of SPW steps, so they stay inside one group when the group
+  // spans a multiple of SPW steps; otherwise the group (1 or 2 steps) divides SPW.
+  const int gsteps = group_steps_;
+  p->spg = (gsteps % p->spw == 0) ? p->spw : gsteps;
   const int units = nsteps / p->spw;  // wave-sized K units per column tile
   int best_w = -1, best_score = 1 << 30;
   for (int w = kDecodeMaxWaves; w >= 1; --w) {
@@ -255,12 +271,12 @@ bool plan_decode(int M, int N, int K, DecodePlan* p) {
   return true;
 }
 
-template <int NW, int SPW, bool BF16>
+template <int NW, int SPW, int SPG, bool BF16>
 void launch_decode(const DecodePlan& p, const void* x, const int32_t* qw, const void* s,
                    const void* z, void* y, float* acc, int* counters, int M, int N, int K,
                    int group, hipStream_t stream) {
   dim3 grid(p.ntiles * p.splits, p.mblocks);
-  hipLaunchKernelGGL((w4a16_decode_kernel<NW, SPW, BF16>), grid, dim3(p.waves * 64), 0, stream,
+  hipLaunchKernelGGL((w4a16_decode_kernel<NW, SPW, SPG, BF16>), grid, dim3(p.waves * 64), 0, stream,
                      (const uint16_t*)x, (const uint32_t*)qw, (const uint16_t*)s,
                      (const uint16_t*)z, (uint16_t*)y, acc, counters, M, N, K, group, p.splits);
 }
@@ -269,62 +285,64 @@ template <bool BF16>
 void dispatch_decode(const DecodePlan& p, const void* x, const int32_t* qw, const void* s,
                      const void* z, void* y, float* acc, int* counters, int M, int N, int K,
                      int group, hipStream_t st) {
-#define KBH_DEC(NW_, SPW_)                                                                       \
-  if (p.nw == NW_ && p.spw == SPW_)                                                              \
-    return launch_decode<NW_, SPW_, BF16>(p, x, qw, s, z, y, acc, counters, M, N, K, group, st);
-  KBH_DEC(2, 4) KBH_DEC(2, 2) KBH_DEC(2, 1) KBH_DEC(1, 4) KBH_DEC(1, 2) KBH_DEC(1, 1)
+#define KBH_DEC(NW_, SPW_, SPG_)                                                                 \
+  if (p.nw == NW_ && p.spw == SPW_ && p.spg == SPG_)                                             \
+    return launch_decode<NW_, SPW_, SPG_, BF16>(p, x, qw, s, z, y, acc, counters, M, N, K, group, st);
+  KBH_DEC(2, 4, 4) KBH_DEC(2, 4, 2) KBH_DEC(2, 4, 1) KBH_DEC(2, 2, 2) KBH_DEC(2, 2, 1)
+  KBH_DEC(2, 1, 1) KBH_DEC(1, 4, 4) KBH_DEC(1, 4, 2) KBH_DEC(1, 4, 1) KBH_DEC(1, 2, 2)
+  KBH_DEC(1, 2, 1) KBH_DEC(1, 1, 1)
 #undef KBH_DEC
 }
 
 // ======================================================================================
 // Tiled kernel
 // ======================================================================================
-constexpr int TBM = 256, TBN = 128, TBK = 64;
-constexpr int TLD = TBK + 8;  // LDS row stride in 16-bit elements (144 B: conflict-free b128)
+constexpr int TBM = 256, TBN = 128, TBK = 32;
+constexpr int TLD = TBK + 8;  // LDS row stride in 16-bit elements (80 B: conflict-free b128)
+constexpr int TDEPTH = 4;     // K slabs in flight in registers ahead of the MFMAs
 
-// Dequantizes one thread's 4 rows x 8 columns and stores them k-major per column.
-// w[4] are the packed words of rows k..k+3 (same word column); result column c (0..7) gets
-// halves for k..k+3 as two dwords.
+// Dequantizes one thread's 2 rows (k, k+1) x 8 columns: result column c is the dword holding
+// the two 16-bit values (k, k+1). The arithmetic is the reference's: (q - z) in the input dtype
+// (exact: small integers), times s with one rounding.
 template <bool BF16>
-__device__ inline void dequant_4x8(const uint32_t w[4], kbh_u32x4 sv, kbh_u32x4 zv,
-                                   uint32_t out[8][2]) {
+__device__ inline void dequant_2x8(uint32_t w0, uint32_t w1, kbh_u32x4 sv, kbh_u32x4 zv,
+                                   uint32_t out[8]) {
   constexpr uint32_t MAGIC = BF16 ? kMagicBF16 : kMagicF16;
 #pragma unroll
-  for (int pr = 0; pr < 2; ++pr) {
+  for (int j = 0; j < 4; ++j) {
+    const uint32_t P = pair_bytes_rt(w0, w1, j);
+    const uint32_t hl = (P & 0x000F000Fu) | MAGIC;          // column 2j   at rows (k, k+1)
+    const uint32_t hh = ((P >> 4) & 0x000F000Fu) | MAGIC;   // column 2j+1 at rows (k, k+1)
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const uint32_t P = pair_bytes_rt(w[2 * pr], w[2 * pr + 1], j);
-      const uint32_t hl = (P & 0x000F000Fu) | MAGIC;          // column 2j   at rows (k, k+1)
-      const uint32_t hh = ((P >> 4) & 0x000F000Fu) | MAGIC;   // column 2j+1 at rows (k, k+1)
-#pragma unroll
-      for (int hsel = 0; hsel < 2; ++hsel) {
-        const int col = 2 * j + hsel;
-        const uint32_t h = hsel ? hh : hl;
-        const uint16_t sb = (uint16_t)((col & 1) ? (sv[col >> 1] >> 16) : (sv[col >> 1] & 0xffffu));
-        const uint16_t zb = (uint16_t)((col & 1) ? (zv[col >> 1] >> 16) : (zv[col >> 1] & 0xffffu));
-        uint32_t r;
-        if constexpr (BF16) {
-          // (B+q) - (B+z) is exact in fp32; times s is exact in fp32 (8+5 bit significands);
-          // one rounding to bf16.
-          const float s = bf16_bits_to_f32(sb);
-          const float bz = 128.0f + bf16_bits_to_f32(zb);
-          const float lo = (bf16_bits_to_f32((uint16_t)(h & 0xffffu)) - bz) * s;
-          const float hi = (bf16_bits_to_f32((uint16_t)(h >> 16)) - bz) * s;
-          r = (uint32_t)f32_to_bf16_bits(lo) | ((uint32_t)f32_to_bf16_bits(hi) << 16);
-        } else {
-          typedef _Float16 h2 __attribute__((ext_vector_type(2)));
-          const _Float16 s = __builtin_bit_cast(_Float16, sb);
-          const _Float16 bz = (_Float16)1024.0f + __builtin_bit_cast(_Float16, zb);
-          const h2 hv = __builtin_bit_cast(h2, h);
-          const h2 d = hv - h2{bz, bz};  // q - z, exact
-          const h2 wv = d * h2{s, s};     // one rounding, as the reference's fp16 multiply
-          r = __builtin_bit_cast(uint32_t, wv);
-        }
-        out[col][pr] = r;
+    for (int hsel = 0; hsel < 2; ++hsel) {
+      const int col = 2 * j + hsel;
+      const uint32_t h = hsel ? hh : hl;
+      const uint16_t sb = (uint16_t)((col & 1) ? (sv[col >> 1] >> 16) : (sv[col >> 1] & 0xffffu));
+      const uint16_t zb = (uint16_t)((col & 1) ? (zv[col >> 1] >> 16) : (zv[col >> 1] & 0xffffu));
+      if constexpr (BF16) {
+        // (128+q) - (128+z) is exact in fp32, times s is exact in fp32; one rounding to bf16.
+        const float s = bf16_bits_to_f32(sb);
+        const float bz = 128.0f + bf16_bits_to_f32(zb);
+        const float lo = (bf16_bits_to_f32((uint16_t)(h & 0xffffu)) - bz) * s;
+        const float hi = (bf16_bits_to_f32((uint16_t)(h >> 16)) - bz) * s;
+        out[col] = (uint32_t)f32_to_bf16_bits(lo) | ((uint32_t)f32_to_bf16_bits(hi) << 16);
+      } else {
+        typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+        const _Float16 sc = __builtin_bit_cast(_Float16, sb);
+        const _Float16 bz = (_Float16)1024.0f + __builtin_bit_cast(_Float16, zb);
+        const h2 d = __builtin_bit_cast(h2, h) - h2{bz, bz};  // q - z, exact
+        out[col] = __builtin_bit_cast(uint32_t, d * h2{sc, sc});
       }
     }
   }
 }
+
+// One K slab of one thread, held in registers between its global load and its LDS store.
+struct TiledSlab {
+  kbh_u32x4 a[4];   // x: rows t/4 + 64i, 16-byte chunk t%4 of the slab
+  uint32_t b[2];    // qweight rows 2*(t%16), +1 of the slab, word column t/16
+  kbh_u32x4 s, z;   // scales / zeros of columns 8*(t/16) .. +7 for the slab's group
+};
 
 template <bool BF16>
 __global__ __launch_bounds__(256) void w4a16_tiled_kernel(
@@ -342,43 +360,45 @@ __global__ __launch_bounds__(256) void w4a16_tiled_kernel(
   const int mb = id / ntn, nb = id - mb * ntn;
   const int m0 = mb * TBM, n0 = nb * TBN;
   const int NP = N >> 3;
+  const int KT = K / TBK;
 
-  // global -> register mapping
-  // A: rows t/8 + 32i (i < 8), 16-byte chunk t%8 of the 64-column slab.
-  const int a_row = t >> 3, a_ch = t & 7;
-  // B: rows 4*(t%16) .. +3 of the slab, packed word column t/16 (columns 8*(t/16) .. +7).
-  const int b_kq = t & 15, b_wc = t >> 4;
+  const int a_ch = t & 3, a_row = t >> 2;
+  const int b_kp = t & 15, b_wc = t >> 4;
+  const uint16_t* xrow[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int r = m0 + a_row + 64 * i;
+    xrow[i] = x + (size_t)(r < M ? r : M - 1) * K + a_ch * 8;  // rows >= M are never stored
+  }
+  const uint32_t* qcol = qw + (size_t)(2 * b_kp) * NP + (n0 >> 3) + b_wc;
+  const size_t scol = (size_t)n0 + 8 * b_wc;
 
-  kbh_u32x4 ar[8];
-  uint32_t br[4];
-  kbh_u32x4 sv, zv;
-
-  auto load_tile = [&](int kt) {
+  auto load = [&](TiledSlab& sl, int kt) {
     const int k0 = kt * TBK;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int r = m0 + a_row + 32 * i;
-      const bool ok = r < M;
-      const kbh_u32x4 v = *reinterpret_cast<const kbh_u32x4*>(x + (size_t)(ok ? r : 0) * K + k0 + a_ch * 8);
-      ar[i] = ok ? v : kbh_u32x4{0u, 0u, 0u, 0u};
-    }
-    const uint32_t* qp = qw + (size_t)(k0 + 4 * b_kq) * NP + (n0 >> 3) + b_wc;
-#pragma unroll
-    for (int r = 0; r < 4; ++r) br[r] = qp[(size_t)r * NP];
-    const int gi = (k0 + 4 * b_kq) / group;
-    const size_t off = (size_t)gi * N + n0 + 8 * b_wc;
-    sv = *reinterpret_cast<const kbh_u32x4*>(scales + off);
-    zv = *reinterpret_cast<const kbh_u32x4*>(zeros + off);
+    for (int i = 0; i < 4; ++i) sl.a[i] = *reinterpret_cast<const kbh_u32x4*>(xrow[i] + k0);
+    const uint32_t* q = qcol + (size_t)k0 * NP;
+    sl.b[0] = __builtin_nontemporal_load(q);
+    sl.b[1] = __builtin_nontemporal_load(q + NP);
+    const size_t off = (size_t)(k0 / group) * N + scol;
+    sl.s = *reinterpret_cast<const kbh_u32x4*>(scales + off);
+    sl.z = *reinterpret_cast<const kbh_u32x4*>(zeros + off);
   };
-  auto store_tile = [&](int buf) {
+  auto store_a = [&](const TiledSlab& sl, int buf) {
 #pragma unroll
-    for (int i = 0; i < 8; ++i)
-      *reinterpret_cast<kbh_u32x4*>(&As[buf][(a_row + 32 * i) * TLD + a_ch * 8]) = ar[i];
-    uint32_t dq[8][2];
-    dequant_4x8<BF16>(br, sv, zv, dq);
+    for (int i = 0; i < 4; ++i)
+      *reinterpret_cast<kbh_u32x4*>(&As[buf][(a_row + 64 * i) * TLD + a_ch * 8]) = sl.a[i];
+  };
+  auto store_b = [&](const TiledSlab& sl, int buf) {
+    uint32_t dq[8];
+    dequant_2x8<BF16>(sl.b[0], sl.b[1], sl.s, sl.z, dq);
 #pragma unroll
     for (int c = 0; c < 8; ++c)
-      *reinterpret_cast<kbh_u32x2*>(&Bs[buf][(b_wc * 8 + c) * TLD + 4 * b_kq]) = kbh_u32x2{dq[c][0], dq[c][1]};
+      *reinterpret_cast<uint32_t*>(&Bs[buf][(b_wc * 8 + c) * TLD + 2 * b_kp]) = dq[c];
+  };
+  auto store = [&](const TiledSlab& sl, int buf) {
+    store_a(sl, buf);
+    store_b(sl, buf);
   };
 
   kbh_f32x16 accv[4][2];
@@ -389,30 +409,46 @@ __global__ __launch_bounds__(256) void w4a16_tiled_kernel(
 #pragma unroll
       for (int e = 0; e < 16; ++e) accv[i][j][e] = 0.f;
 
-  const int KT = K / TBK;
-  load_tile(0);
-  store_tile(0);
-  __syncthreads();
   const int fr = lane & 31, fk = (lane >> 5) * 8;
-  for (int kt = 0; kt < KT; ++kt) {
-    const int buf = kt & 1;
-    if (kt + 1 < KT) load_tile(kt + 1);
-    const uint16_t* Ab = &As[buf][(wm * 128 + fr) * TLD + fk];
-    const uint16_t* Bb = &Bs[buf][(wn * 64 + fr) * TLD + fk];
+  // One 16-wide K step of the wave's 128x64 tile: 6 LDS fragment reads, 8 MFMAs.
+  auto mma_k16 = [&](int buf, int kk) {
+    const uint16_t* Ab = &As[buf][(wm * 128 + fr) * TLD + fk + kk * 16];
+    const uint16_t* Bb = &Bs[buf][(wn * 64 + fr) * TLD + fk + kk * 16];
+    kbh_u32x4 a[4], b[2];
 #pragma unroll
-    for (int kk = 0; kk < TBK / 16; ++kk) {
-      kbh_u32x4 a[4], b[2];
+    for (int i = 0; i < 4; ++i) a[i] = *reinterpret_cast<const kbh_u32x4*>(Ab + i * 32 * TLD);
 #pragma unroll
-      for (int i = 0; i < 4; ++i) a[i] = *reinterpret_cast<const kbh_u32x4*>(Ab + i * 32 * TLD + kk * 16);
+    for (int j = 0; j < 2; ++j) b[j] = *reinterpret_cast<const kbh_u32x4*>(Bb + j * 32 * TLD);
 #pragma unroll
-      for (int j = 0; j < 2; ++j) b[j] = *reinterpret_cast<const kbh_u32x4*>(Bb + j * 32 * TLD + kk * 16);
+    for (int i = 0; i < 4; ++i)
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
+      for (int j = 0; j < 2; ++j) accv[i][j] = mfma32x32x16<BF16>(a[i], b[j], accv[i][j]);
+  };
+
+  // Register ring: slab j lives in stage j % TDEPTH from its load until its LDS store. KT is a
+  // multiple of TDEPTH and loads past the last slab re-read it, so the steady-state loop has no
+  // branches (a conditional load would make the compiler wait for every load in flight).
+  TiledSlab ring[TDEPTH];
 #pragma unroll
-        for (int j = 0; j < 2; ++j) accv[i][j] = mfma32x32x16<BF16>(a[i], b[j], accv[i][j]);
+  for (int d = 0; d < TDEPTH; ++d) load(ring[d], d);
+  store(ring[0], 0);
+  load(ring[0], min(TDEPTH, KT - 1));
+  __syncthreads();
+
+  for (int kt0 = 0; kt0 < KT; kt0 += TDEPTH) {
+#pragma unroll
+    for (int d = 0; d < TDEPTH; ++d) {
+      const int kt = kt0 + d;
+      const int nxt = (d + 1) % TDEPTH;      // stage of slab kt+1
+      // The MFMAs of slab kt run asynchronously while the wave stages slab kt+1 (x copy,
+      // dequantization) into the other LDS buffer; after the last slab that buffer is unused.
+      mma_k16(kt & 1, 0);
+      store_a(ring[nxt], (kt + 1) & 1);
+      mma_k16(kt & 1, 1);
+      store_b(ring[nxt], (kt + 1) & 1);
+      load(ring[nxt], min(kt + 1 + TDEPTH, KT - 1));
+      __syncthreads();
     }
-    if (kt + 1 < KT) store_tile(buf ^ 1);
-    __syncthreads();
   }
 
   // epilogue: accumulator element e of tile (i, j) is row 8(e/4) + 4(l/32) + e%4, column l%32
@@ -458,7 +494,7 @@ extern "C" int kbh_w4a16_gemm(const void* x, const int32_t* qweight, const void*
   const bool bf = dtype == KBH_BF16;
   hipStream_t st = (hipStream_t)stream;
 
-  if (M >= kTiledMinM && K % TBK == 0) {
+  if (M >= kTiledMinM && K % (TBK * TDEPTH) == 0) {
     const int tiles = ((M + TBM - 1) / TBM) * (N / TBN);
     if (bf)
       hipLaunchKernelGGL(w4a16_tiled_kernel<true>, dim3(tiles), dim3(256), 0, st,
@@ -476,7 +512,7 @@ extern "C" int kbh_w4a16_gemm(const void* x, const int32_t* qweight, const void*
   float* acc = (float*)workspace;
   int* counters = (int*)((char*)workspace + round_up((size_t)M * (size_t)N * 4u, 256));
   DecodePlan p;
-  if (!plan_decode(M, N, K, &p)) return KBH_ERR_SHAPE;
+  if (!plan_decode(M, N, K, group / 32, &p)) return KBH_ERR_SHAPE;
   if (bf) dispatch_decode<true>(p, x, qweight, scales, zeros, y, acc, counters, M, N, K, group, st);
   else dispatch_decode<false>(p, x, qweight, scales, zeros, y, acc, counters, M, N, K, group, st);
   return launch_status();
