@@ -66,6 +66,28 @@ int kbh_w4a16_gemm(const void* x, const int32_t* qweight, const void* scales, co
                    void* y, void* workspace, size_t workspace_bytes,
                    int M, int N, int K, int group, int dtype, void* stream);
 
+/* ---------------------------------------------------------------------------------------
+ * W8A8 SmoothQuant int8 GEMM.
+ * Replaces tasks/w8a8_smoothquant/w8a8_smoothquant__llama3_8b_down__M16/environment/
+ * reference.py:7-9 (Model.forward(x_int8, w_int8, x_scale, w_scale)); template
+ * generate_tasks.py:198-215.
+ *
+ *   x_int8  [M, K] int8        x_scale [M] fp16 (per token)
+ *   w_int8  [K, N] int8        w_scale [N] fp16 (per output channel)
+ *   y       [M, N] fp16,  y = fp16((fp32(x_int8 @ w_int8) * x_scale[m]) * w_scale[n])
+ * The int8 x int8 products are accumulated exactly in int32.
+ * Requirements: M >= 1, N % 128 == 0, K % 64 == 0, x/w/y 16-byte aligned.
+ * workspace: as for kbh_w4a16_gemm, with kbh_w8a8_workspace_bytes().
+ */
+size_t kbh_w8a8_workspace_bytes(int M, int N, int K);
+int kbh_w8a8_gemm(const int8_t* x_int8, const int8_t* w_int8, const void* x_scale,
+                  const void* w_scale, void* y, void* workspace, size_t workspace_bytes,
+                  int M, int N, int K, void* stream);
+/* Same GEMM returning the raw int32 accumulators acc_out [M, N] (no scale epilogue); exposes
+ * the integer stage of the reference (reference.py:8) for bit-exact checks. */
+int kbh_w8a8_gemm_i32(const int8_t* x_int8, const int8_t* w_int8, int32_t* acc_out,
+                      void* workspace, size_t workspace_bytes, int M, int N, int K, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

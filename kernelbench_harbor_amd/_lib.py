@@ -38,6 +38,9 @@ SIGNATURES = {
     "kbh_last_hip_error": (_i, []),
     "kbh_w4a16_workspace_bytes": (_sz, [_i, _i, _i, _i]),
     "kbh_w4a16_gemm": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _sz, _i, _i, _i, _i, _i, _vp]),
+    "kbh_w8a8_workspace_bytes": (_sz, [_i, _i, _i]),
+    "kbh_w8a8_gemm": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _sz, _i, _i, _i, _vp]),
+    "kbh_w8a8_gemm_i32": (_i, [_vp, _vp, _vp, _vp, _sz, _i, _i, _i, _vp]),
 }
 
 

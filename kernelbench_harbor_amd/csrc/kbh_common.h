@@ -73,6 +73,14 @@ __device__ inline float half_bits_to_f32(uint16_t h) {
   if constexpr (BF16) return bf16_bits_to_f32(h); else return f16_bits_to_f32(h);
 }
 
+// Materialises v as an fp32 register value. Used where the reference rounds an intermediate to
+// fp32 before a narrower conversion: without it the compiler may fuse a multiply with the
+// conversion (v_fma_mix*), which rounds once and can differ from the reference in a tie.
+__device__ inline float keep_f32(float v) {
+  asm volatile("" : "+v"(v));
+  return v;
+}
+
 // fp32 -> fp16 / bf16 with round-to-nearest-even (NaN is kept quiet).
 __device__ inline uint16_t f32_to_f16_bits(float f) { return __builtin_bit_cast(uint16_t, (_Float16)f); }
 __device__ inline uint16_t f32_to_bf16_bits(float f) {

@@ -40,3 +40,34 @@ def w4a16(M: int, K: int = 14336, N: int = 4096, group: int = 128,
         raise ValueError(dist)
     zeros = torch.randint(0, 16, (K // group, N), generator=g).to(dtype)
     return [x, qweight, scales, zeros]
+
+
+def w8a8(M: int, K: int = 14336, N: int = 4096, seed: int = 0, dist: str = "baseline"):
+    """[x_int8, w_int8, x_scale, w_scale] in the layout of reference.py:7 (W8A8 task).
+
+    "reference": uniform int8 in [-127, 127] and scales U[0.001, 0.011] (reference.py:11-17).
+    "baseline":  SmoothQuant synthesis — x ~ N(0,1) fp16 with a fixed 1% of input channels
+                 scaled x20, W ~ N(0,1)*0.02 fp16; smoothing s_k = max|x_k|^0.5 / max|W_k|^0.5,
+                 x' = x/s, W' = W*s; symmetric absmax int8 per token (x) and per output
+                 channel (W) with fp16 scales."""
+    g = _gen(seed)
+    if dist == "reference":
+        x_int8 = torch.randint(-127, 128, (M, K), generator=g, dtype=torch.int8)
+        w_int8 = torch.randint(-127, 128, (K, N), generator=g, dtype=torch.int8)
+        x_scale = (torch.rand(M, 1, generator=g) * 0.01 + 0.001).to(torch.float16)
+        w_scale = (torch.rand(1, N, generator=g) * 0.01 + 0.001).to(torch.float16)
+        return [x_int8, w_int8, x_scale, w_scale]
+    if dist != "baseline":
+        raise ValueError(dist)
+    x = torch.randn(M, K, generator=g).to(torch.float16).float()
+    outliers = torch.randperm(K, generator=torch.Generator().manual_seed(1234))[: max(1, K // 100)]
+    x[:, outliers] *= 20.0
+    W = (torch.randn(K, N, generator=g) * 0.02).to(torch.float16).float()
+    s = (x.abs().amax(dim=0).clamp(min=1e-5) ** 0.5) / (W.abs().amax(dim=1).clamp(min=1e-5) ** 0.5)
+    xs_ = x / s
+    Ws_ = W * s[:, None]
+    x_scale = (xs_.abs().amax(dim=1, keepdim=True) / 127.0).to(torch.float16)
+    w_scale = (Ws_.abs().amax(dim=0, keepdim=True) / 127.0).to(torch.float16)
+    x_int8 = torch.round(xs_ / x_scale.float()).clamp(-127, 127).to(torch.int8)
+    w_int8 = torch.round(Ws_ / w_scale.float()).clamp(-127, 127).to(torch.int8)
+    return [x_int8, w_int8, x_scale, w_scale]

@@ -21,3 +21,14 @@ class W4A16Model(nn.Module):
 
     def forward(self, x, qweight, scales, zeros):
         return ops.w4a16_gemm(x, qweight, scales, zeros)
+
+
+class W8A8Model(nn.Module):
+    """W8A8 SmoothQuant linear.
+
+    Reference: tasks/w8a8_smoothquant/*/environment/reference.py:7-9,
+    forward(x_int8 [M,K], w_int8 [K,N], x_scale [M,1] fp16, w_scale [1,N] fp16) -> [M,N] fp16.
+    """
+
+    def forward(self, x_int8, w_int8, x_scale, w_scale):
+        return ops.w8a8_gemm(x_int8, w_int8, x_scale, w_scale)

@@ -97,3 +97,51 @@ def w4a16_gemm(x: torch.Tensor, qweight: torch.Tensor, scales: torch.Tensor,
                             M, N, K, group, _DT_CODE[x.dtype], _stream_ptr(dev))
     _lib.check(st, "kbh_w4a16_gemm")
     return y.reshape(*lead, N)
+
+
+def _w8a8_args(x_int8, w_int8):
+    _require(x_int8.dtype == torch.int8 and w_int8.dtype == torch.int8,
+             f"x_int8/w_int8 must be int8, got {x_int8.dtype}/{w_int8.dtype}")
+    _require(w_int8.dim() == 2, "w_int8 must be [K, N]")
+    K, N = w_int8.shape
+    _require(x_int8.shape[-1] == K, f"x_int8 last dim {x_int8.shape[-1]} != K={K}")
+    dev = _check_device(x_int8, w_int8)
+    x2 = x_int8.reshape(-1, K).contiguous()
+    return dev, x2, w_int8.contiguous(), x2.shape[0], N, K
+
+
+def w8a8_gemm(x_int8: torch.Tensor, w_int8: torch.Tensor, x_scale: torch.Tensor,
+              w_scale: torch.Tensor) -> torch.Tensor:
+    """out = fp16((fp32(x_int8 @ w_int8) * x_scale) * w_scale), int32-exact accumulation.
+
+    Follows tasks/w8a8_smoothquant/w8a8_smoothquant__llama3_8b_down__M16/environment/
+    reference.py:7-9: x_int8 [M, K], w_int8 [K, N], x_scale [M, 1] fp16, w_scale [1, N] fp16."""
+    dev, x2, w, M, N, K = _w8a8_args(x_int8, w_int8)
+    _require(x_scale.dtype == torch.float16 and w_scale.dtype == torch.float16,
+             "x_scale and w_scale must be float16")
+    _require(x_scale.numel() == M and w_scale.numel() == N,
+             f"x_scale must hold {M} values and w_scale {N}")
+    _check_device(x_int8, x_scale, w_scale)
+    lead = x_int8.shape[:-1]
+    y = torch.empty((M, N), dtype=torch.float16, device=dev)
+    xs = x_scale.reshape(M).contiguous()
+    ws_ = w_scale.reshape(N).contiguous()
+    lib = _lib.load()
+    nbytes = lib.kbh_w8a8_workspace_bytes(M, N, K)
+    ws = workspaces.get(nbytes, dev)
+    st = lib.kbh_w8a8_gemm(x2.data_ptr(), w.data_ptr(), xs.data_ptr(), ws_.data_ptr(),
+                           y.data_ptr(), ws.data_ptr(), ws.numel(), M, N, K, _stream_ptr(dev))
+    _lib.check(st, "kbh_w8a8_gemm")
+    return y.reshape(*lead, N)
+
+
+def w8a8_gemm_i32(x_int8: torch.Tensor, w_int8: torch.Tensor) -> torch.Tensor:
+    """The exact int32 accumulators x_int8 @ w_int8 (reference.py:8 before the scales)."""
+    dev, x2, w, M, N, K = _w8a8_args(x_int8, w_int8)
+    acc = torch.empty((M, N), dtype=torch.int32, device=dev)
+    lib = _lib.load()
+    ws = workspaces.get(lib.kbh_w8a8_workspace_bytes(M, N, K), dev)
+    st = lib.kbh_w8a8_gemm_i32(x2.data_ptr(), w.data_ptr(), acc.data_ptr(), ws.data_ptr(),
+                               ws.numel(), M, N, K, _stream_ptr(dev))
+    _lib.check(st, "kbh_w8a8_gemm_i32")
+    return acc
