@@ -105,9 +105,8 @@ def _w8a8_args(x_int8, w_int8):
     _require(w_int8.dim() == 2, "w_int8 must be [K, N]")
     K, N = w_int8.shape
     _require(x_int8.shape[-1] == K, f"x_int8 last dim {x_int8.shape[-1]} != K={K}")
-    dev = _check_device(x_int8, w_int8)
-    x2 = x_int8.reshape(-1, K).contiguous()
-    return dev, x2, w_int8.contiguous(), x2.shape[0], N, K
+    x2 = x_int8.reshape(-1, K)
+    return x2, x2.shape[0], N, K
 
 
 def w8a8_gemm(x_int8: torch.Tensor, w_int8: torch.Tensor, x_scale: torch.Tensor,
@@ -116,12 +115,13 @@ def w8a8_gemm(x_int8: torch.Tensor, w_int8: torch.Tensor, x_scale: torch.Tensor,
 
     Follows tasks/w8a8_smoothquant/w8a8_smoothquant__llama3_8b_down__M16/environment/
     reference.py:7-9: x_int8 [M, K], w_int8 [K, N], x_scale [M, 1] fp16, w_scale [1, N] fp16."""
-    dev, x2, w, M, N, K = _w8a8_args(x_int8, w_int8)
+    x2, M, N, K = _w8a8_args(x_int8, w_int8)
     _require(x_scale.dtype == torch.float16 and w_scale.dtype == torch.float16,
              "x_scale and w_scale must be float16")
     _require(x_scale.numel() == M and w_scale.numel() == N,
              f"x_scale must hold {M} values and w_scale {N}")
-    _check_device(x_int8, x_scale, w_scale)
+    dev = _check_device(x_int8, w_int8, x_scale, w_scale)
+    x2, w = x2.contiguous(), w_int8.contiguous()
     lead = x_int8.shape[:-1]
     y = torch.empty((M, N), dtype=torch.float16, device=dev)
     xs = x_scale.reshape(M).contiguous()
@@ -137,7 +137,9 @@ def w8a8_gemm(x_int8: torch.Tensor, w_int8: torch.Tensor, x_scale: torch.Tensor,
 
 def w8a8_gemm_i32(x_int8: torch.Tensor, w_int8: torch.Tensor) -> torch.Tensor:
     """The exact int32 accumulators x_int8 @ w_int8 (reference.py:8 before the scales)."""
-    dev, x2, w, M, N, K = _w8a8_args(x_int8, w_int8)
+    x2, M, N, K = _w8a8_args(x_int8, w_int8)
+    dev = _check_device(x_int8, w_int8)
+    x2, w = x2.contiguous(), w_int8.contiguous()
     acc = torch.empty((M, N), dtype=torch.int32, device=dev)
     lib = _lib.load()
     ws = workspaces.get(lib.kbh_w8a8_workspace_bytes(M, N, K), dev)

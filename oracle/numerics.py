@@ -60,7 +60,7 @@ def e4m3fn_decode(codes) -> np.ndarray:
 
 def e4m3fn_encode_rne(a) -> np.ndarray:
     """float -> e4m3fn code, round to nearest even. |a| beyond the rounding range of 448
-    (>= 464) and NaN map to NaN (0x7F / 0xFF), matching torch's float8_e4m3fn cast."""
+    (> 464) and NaN map to NaN (0x7F / 0xFF), matching torch's float8_e4m3fn cast."""
     a = np.asarray(a, dtype=np.float64)
     sign = np.signbit(a)
     x = np.abs(a)
@@ -72,8 +72,8 @@ def e4m3fn_encode_rne(a) -> np.ndarray:
     code = np.where(d_lo < d_hi, lo, hi)
     code = np.where(d_lo == d_hi, np.where(lo % 2 == 0, lo, hi), code)   # ties to even code
     code = np.where(x <= 0.0, 0, code)
-    code = np.where(x > 448.0, 126, code)               # (448, 464) rounds down to 448
-    code = np.where((x >= 464.0) | np.isnan(x), 0x7F, code)   # 464 = midpoint of 448 and 480
+    code = np.where(x > 448.0, 126, code)               # (448, 464] rounds to 448 (464: tie, even)
+    code = np.where((x > 464.0) | np.isnan(x), 0x7F, code)    # 464 = midpoint of 448 and 480
     code = code | np.where(sign, 0x80, 0)
     return code.astype(np.uint8)
 

@@ -1,0 +1,66 @@
+"""CPU checks of the C ABI: the library builds, loads and exports every declared entry point;
+argument checks in the library reject bad shapes/pointers before any launch."""
+import ctypes
+import os
+import re
+
+import pytest
+
+from kernelbench_harbor_amd import _lib
+from kernelbench_harbor_amd.build import LIB_PATH
+
+HEADER = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "include",
+                      "kbh_qgemm.h")
+
+
+def declared_functions():
+    src = open(HEADER).read()
+    src = re.sub(r"/\*.*?\*/", "", src, flags=re.S)
+    return sorted(set(re.findall(r"\b(kbh_[a-z0-9_]+)\s*\(", src)))
+
+
+def test_library_exists():
+    assert os.path.exists(LIB_PATH), "run kernelbench_harbor_amd.build.build() first"
+
+
+def test_every_declared_symbol_is_exported_and_bound():
+    lib = ctypes.CDLL(LIB_PATH)
+    names = declared_functions()
+    assert len(names) >= 5
+    for n in names:
+        assert hasattr(lib, n), f"{n} declared in include/kbh_qgemm.h but not exported"
+        assert n in _lib.SIGNATURES, f"{n} has no ctypes signature in _lib.py"
+
+
+def test_version_and_status_strings():
+    lib = _lib.load()
+    assert lib.kbh_abi_version() == 1
+    assert lib.kbh_status_string(0) == b"ok"
+    assert b"shape" in lib.kbh_status_string(_lib.KBH_ERR_SHAPE)
+    assert lib.kbh_status_string(999) == b"unknown status"
+
+
+def test_host_checks_run_without_gpu():
+    """Bad arguments are rejected by the library before it touches the device."""
+    lib = _lib.load()
+    p = ctypes.c_void_p(16)  # aligned fake address; never dereferenced on these paths
+    assert lib.kbh_w4a16_gemm(None, p, p, p, p, p, 1 << 20, 16, 4096, 4096, 128, 0, None) == _lib.KBH_ERR_NULL
+    assert lib.kbh_w4a16_gemm(p, p, p, p, p, p, 1 << 20, 16, 4100, 4096, 128, 0, None) == _lib.KBH_ERR_SHAPE
+    assert lib.kbh_w4a16_gemm(p, p, p, p, p, p, 1 << 20, 16, 4096, 4096, 100, 0, None) == _lib.KBH_ERR_SHAPE
+    assert lib.kbh_w4a16_gemm(p, p, p, p, p, p, 1 << 20, 16, 4096, 4096, 128, 7, None) == _lib.KBH_ERR_DTYPE
+    assert lib.kbh_w4a16_gemm(p, ctypes.c_void_p(18), p, p, p, p, 1 << 20, 16, 4096, 4096, 128, 0, None) == _lib.KBH_ERR_ALIGN
+    assert lib.kbh_w4a16_gemm(p, p, p, p, p, p, 8, 16, 4096, 4096, 128, 0, None) == _lib.KBH_ERR_WORKSPACE
+    assert lib.kbh_w8a8_gemm(p, p, p, p, p, p, 1 << 20, 16, 4096, 100, None) == _lib.KBH_ERR_SHAPE
+    assert lib.kbh_w8a8_gemm(p, p, p, p, p, None, 0, 16, 4096, 4096, None) == _lib.KBH_ERR_WORKSPACE
+
+
+def test_workspace_sizes():
+    lib = _lib.load()
+    assert lib.kbh_w4a16_workspace_bytes(16, 4096, 14336, 128) >= 16 * 4096 * 4
+    assert lib.kbh_w8a8_workspace_bytes(16, 4096, 14336) >= 16 * 4096 * 4
+    assert lib.kbh_w4a16_workspace_bytes(0, 4096, 14336, 128) == 0
+
+
+def test_missing_library_fails_loudly(tmp_path):
+    with pytest.raises(_lib.KbhError, match="not built"):
+        _lib.load(str(tmp_path / "missing.so"))

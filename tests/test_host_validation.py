@@ -1,0 +1,74 @@
+"""Host-side validation of the Python ops (CPU only: errors are raised before any launch)."""
+import pytest
+import torch
+
+from kernelbench_harbor_amd import W4A16Model, W8A8Model, harness, ops
+
+
+def w4_args(M=4, K=256, N=128, G=128):
+    return [torch.zeros(M, K, dtype=torch.float16), torch.zeros(K, N // 8, dtype=torch.int32),
+            torch.zeros(K // G, N, dtype=torch.float16), torch.zeros(K // G, N, dtype=torch.float16)]
+
+
+def test_modules_take_no_constructor_args():
+    W4A16Model()
+    W8A8Model()
+    with pytest.raises(TypeError):
+        W4A16Model(128)
+
+
+def test_w4a16_rejects_bad_dtypes_and_shapes():
+    x, q, s, z = w4_args()
+    with pytest.raises(ValueError, match="float16 or bfloat16"):
+        ops.w4a16_gemm(x.float(), q, s, z)
+    with pytest.raises(ValueError, match="int32"):
+        ops.w4a16_gemm(x, q.to(torch.int64), s, z)
+    with pytest.raises(ValueError, match="last dim"):
+        ops.w4a16_gemm(x[:, :128], q, s, z)
+    with pytest.raises(ValueError, match="x's dtype"):
+        ops.w4a16_gemm(x, q, s.bfloat16(), z)
+    with pytest.raises(ValueError, match="HIP device"):
+        ops.w4a16_gemm(x, q, s, z)   # CPU tensors
+
+
+def test_w8a8_rejects_bad_inputs():
+    x = torch.zeros(4, 256, dtype=torch.int8)
+    w = torch.zeros(256, 128, dtype=torch.int8)
+    xs = torch.ones(4, 1, dtype=torch.float16)
+    ws = torch.ones(1, 128, dtype=torch.float16)
+    with pytest.raises(ValueError, match="int8"):
+        ops.w8a8_gemm(x.float(), w, xs, ws)
+    with pytest.raises(ValueError, match="float16"):
+        ops.w8a8_gemm(x, w, xs.float(), ws)
+    with pytest.raises(ValueError, match="hold"):
+        ops.w8a8_gemm(x, w, xs[:2], ws)
+    with pytest.raises(ValueError, match="HIP device"):
+        ops.w8a8_gemm(x, w, xs, ws)
+
+
+def test_harness_compare_and_gate():
+    gt = torch.randn(8, 16)
+    ok = harness.compare(gt + 1e-4, gt)
+    assert ok.ok and ok.allclose_ref
+    bad = harness.compare(gt * 1.1, gt)
+    assert not bad.ok
+    with pytest.raises(ValueError, match="shape"):
+        harness.compare(gt[:4], gt)
+
+
+def test_harness_grade_records_errors_and_continues():
+    def boom(*a):
+        raise RuntimeError("kernel exploded")
+    res = harness.grade(boom, lambda i: [torch.zeros(1)], lambda inp: torch.zeros(1), draws=2)
+    assert not res.correct and "kernel exploded" in res.error
+
+
+def test_static_check_rules():
+    ok, _ = harness.static_check("from kernelbench_harbor_amd import W4A16Model as ModelNew\n")
+    assert ok
+    ok, why = harness.static_check("import torch\nclass ModelNew:\n  def forward(self, a, b): return torch.matmul(a, b)\n")
+    assert not ok and "matmul" in why
+    ok, why = harness.static_check("import triton\n")
+    assert not ok
+    ok, why = harness.static_check("import torch\n")
+    assert not ok and "HIP library" in why
