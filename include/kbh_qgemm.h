@@ -88,6 +88,24 @@ int kbh_w8a8_gemm(const int8_t* x_int8, const int8_t* w_int8, const void* x_scal
 int kbh_w8a8_gemm_i32(const int8_t* x_int8, const int8_t* w_int8, int32_t* acc_out,
                       void* workspace, size_t workspace_bytes, int M, int N, int K, void* stream);
 
+/* ---------------------------------------------------------------------------------------
+ * FP8 (e4m3fn) block-scaled weight GEMM.
+ * Replaces tasks/fp8_microscale/fp8_microscale__llama3_8b_down__b128__fp16/environment/
+ * reference.py:9-12 (Model.forward(x, w_fp8, scales)); template generate_tasks.py:218-237.
+ *
+ *   x      [M, K] dtype (fp16 or bf16)
+ *   w_fp8  [K, N] uint8 bit patterns of float8_e4m3fn (OCP)
+ *   scales [K/block, N] fp16
+ *   y      [M, N] dtype,  y = x @ dtype(fp32(w_fp8) * fp32(scales[k/block, n]))
+ * Requirements: M >= 1, N % 128 == 0, K % 32 == 0, block in {32, 64, 128, 256},
+ * K % block == 0, x/w/scales/y 16-byte aligned.
+ * workspace: as for kbh_w4a16_gemm, with kbh_fp8w_workspace_bytes().
+ */
+size_t kbh_fp8w_workspace_bytes(int M, int N, int K, int block);
+int kbh_fp8w_gemm(const void* x, const uint8_t* w_fp8, const void* scales, void* y,
+                  void* workspace, size_t workspace_bytes, int M, int N, int K, int block,
+                  int dtype, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -25,14 +25,12 @@
 //    clears the workspace. Workgroup ids are remapped so that all K splits of a column tile run
 //    on one XCD.
 //
-// w4a16_tiled_kernel (larger M; MFMA-bound)
-//  * 256x128 output tile per 256-thread workgroup, K in 32-row slabs held in a register ring
-//    three slabs ahead of the MFMAs, two LDS stages, one barrier per slab. x rows are staged in
-//    LDS as is; packed weights are dequantized on the way into LDS with the exact
-//    reference arithmetic ((q - z) in the input dtype, times s, one rounding), stored k-major
-//    per column so that both MFMA operands are 16-byte LDS reads. 2x2 waves, each 128x64 with
-//    32x32x16 MFMAs. XCD remapping gives each XCD whole rows of tiles (shared x rows in L2).
+// Larger M: tiled_f16_gemm (tiled_f16.h) with W4SlabPolicy, which dequantizes the packed
+// weights on their way into LDS with the exact reference arithmetic ((q - z) in the input
+// dtype, times s, one rounding), stored k-major per column.
 #include "kbh_common.h"
+#include "splitk.h"
+#include "tiled_f16.h"
 
 namespace kbh {
 namespace {
@@ -62,14 +60,12 @@ __device__ inline uint32_t pair_bytes_rt(uint32_t wa, uint32_t wb, int j) {
 // ======================================================================================
 // Decode kernel
 // ======================================================================================
-constexpr int kDecodeMaxWaves = 8;
-constexpr int kCsStride = 260;  // LDS floats per MFMA column set per wave (4*64 + pad)
 
 // SPG = K steps per quantization group when a group is shorter than a wave's K range
 // (SPG < SPW), otherwise SPG == SPW (each wave lies inside one group). The fold schedule is thus
 // static, and the scales/zeros of every group a wave touches are loaded with its weights.
 template <int NW, int SPW, int SPG, bool BF16>
-__global__ __launch_bounds__(kDecodeMaxWaves * 64) void w4a16_decode_kernel(
+__global__ __launch_bounds__(kSplitKMaxWaves * 64) void w4a16_decode_kernel(
     const uint16_t* __restrict__ x, const uint32_t* __restrict__ qw,
     const uint16_t* __restrict__ scales, const uint16_t* __restrict__ zeros,
     uint16_t* __restrict__ y, float* __restrict__ acc, int* __restrict__ counters,
@@ -77,8 +73,7 @@ __global__ __launch_bounds__(kDecodeMaxWaves * 64) void w4a16_decode_kernel(
   constexpr int NWG = 128 * NW;  // output columns of one workgroup
   constexpr int NCS = 8 * NW;    // MFMA column sets per wave
   constexpr uint32_t MAGIC = BF16 ? kMagicBF16 : kMagicF16;
-  __shared__ float red[kDecodeMaxWaves * NCS * kCsStride];
-  __shared__ int s_last;
+  __shared__ SplitKSmem<NCS, float> sm;
 
   const int waves = blockDim.x >> 6;
   const int lane = threadIdx.x & 63;
@@ -184,60 +179,11 @@ __global__ __launch_bounds__(kDecodeMaxWaves * 64) void w4a16_decode_kernel(
     }
   }
 
-  // ---- reduce the waves of the workgroup through private LDS slices -----------------------
-  // Slice element (column set cs, row 4*(l/16)+i, lane column l%16) at cs*kCsStride + i*64 + l.
-  {
-    float* slice = red + wave * NCS * kCsStride;
-#pragma unroll
-    for (int cs = 0; cs < NCS; ++cs)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) slice[cs * kCsStride + i * 64 + lane] = tot[cs][i];
-  }
-  __syncthreads();
-  // Output element (r, n), n = 8*(cc*NW + w) + nib, is the sum over waves of slice entry
-  // (cs = w*8 + nib, i = r%4, lane = (r/4)*16 + cc).
-  auto lds_sum = [&](int r, int n) {
-    const int cc = n / (8 * NW), w = (n >> 3) % NW, nib = n & 7;
-    const int off = (w * 8 + nib) * kCsStride + (r & 3) * 64 + (r >> 2) * 16 + cc;
-    float v = 0.f;
-    for (int wv = 0; wv < waves; ++wv) v += red[wv * NCS * kCsStride + off];
-    return v;
-  };
   const int rows = min(16, M - m0);
-  if (splits == 1) {
-    for (int e = threadIdx.x; e < rows * NWG; e += blockDim.x) {
-      const int r = e / NWG, n = e - r * NWG;
-      y[(size_t)(m0 + r) * N + n0 + n] = f32_to_half_bits<BF16>(lds_sum(r, n));
-    }
-    return;
-  }
-  // ---- cross-workgroup reduction --------------------------------------------------------
-  // All cross-workgroup traffic uses agent-scope atomics, which are performed at the device
-  // coherence point. Each thread waits until its atomics are acknowledged (s_waitcnt 0) before
-  // the workgroup's arrival is counted, so the workgroup that sees count == splits-1 reads
-  // complete sums with agent-scope atomic loads.
-  for (int e = threadIdx.x; e < rows * NWG; e += blockDim.x) {
-    const int r = e / NWG, n = e - r * NWG;
-    __hip_atomic_fetch_add(&acc[(size_t)(m0 + r) * N + n0 + n], lds_sum(r, n), __ATOMIC_RELAXED,
-                           __HIP_MEMORY_SCOPE_AGENT);
-  }
-  __builtin_amdgcn_s_waitcnt(0);
-  __syncthreads();
-  int* counter = &counters[blockIdx.y * ntiles + tile];
-  if (threadIdx.x == 0) {
-    const int prev = __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    s_last = (prev == splits - 1);
-  }
-  __syncthreads();
-  if (!s_last) return;
-  for (int e = threadIdx.x; e < rows * NWG; e += blockDim.x) {
-    const int r = e / NWG, n = e - r * NWG;
-    float* p = &acc[(size_t)(m0 + r) * N + n0 + n];
-    const float v = __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    __hip_atomic_store(p, 0.f, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    y[(size_t)(m0 + r) * N + n0 + n] = f32_to_half_bits<BF16>(v);
-  }
-  if (threadIdx.x == 0) __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  splitk_finish<NCS, float>(tot, sm, acc, &counters[blockIdx.y * ntiles + tile], splits, rows, N,
+                            m0, n0, [&](int r, int n, float v) {
+                              y[(size_t)(m0 + r) * N + n0 + n] = f32_to_half_bits<BF16>(v);
+                            });
 }
 
 struct DecodePlan {
@@ -257,18 +203,8 @@ bool plan_decode(int M, int N, int K, int group_steps_, DecodePlan* p) {
   const int gsteps = group_steps_;
   p->spg = (gsteps % p->spw == 0) ? p->spw : gsteps;
   const int units = nsteps / p->spw;  // wave-sized K units per column tile
-  int best_w = -1, best_score = 1 << 30;
-  for (int w = kDecodeMaxWaves; w >= 1; --w) {
-    if (units % w) continue;
-    const int grid = p->ntiles * (units / w) * p->mblocks;
-    // Prefer grids of 256..512 workgroups; penalise tiny or huge grids.
-    const int score = grid < 256 ? (256 - grid) * 4 : (grid > 512 ? grid - 512 : 0) + (8 - w);
-    if (score < best_score) { best_score = score; best_w = w; }
-  }
-  if (best_w < 0) return false;
-  p->waves = best_w;
-  p->splits = units / best_w;
-  return true;
+  p->waves = splitk_pick_waves(units, p->ntiles * p->mblocks, &p->splits);
+  return p->waves > 0;
 }
 
 template <int NW, int SPW, int SPG, bool BF16>
@@ -297,10 +233,6 @@ void dispatch_decode(const DecodePlan& p, const void* x, const int32_t* qw, cons
 // ======================================================================================
 // Tiled kernel
 // ======================================================================================
-constexpr int TBM = 256, TBN = 128, TBK = 32;
-constexpr int TLD = TBK + 8;  // LDS row stride in 16-bit elements (80 B: conflict-free b128)
-constexpr int TDEPTH = 4;     // K slabs in flight in registers ahead of the MFMAs
-
 // Dequantizes one thread's 2 rows (k, k+1) x 8 columns: result column c is the dword holding
 // the two 16-bit values (k, k+1). The arithmetic is the reference's: (q - z) in the input dtype
 // (exact: small integers), times s with one rounding.
@@ -337,132 +269,36 @@ __device__ inline void dequant_2x8(uint32_t w0, uint32_t w1, kbh_u32x4 sv, kbh_u
   }
 }
 
-// One K slab of one thread, held in registers between its global load and its LDS store.
-struct TiledSlab {
-  kbh_u32x4 a[4];   // x: rows t/4 + 64i, 16-byte chunk t%4 of the slab
-  uint32_t b[2];    // qweight rows 2*(t%16), +1 of the slab, word column t/16
-  kbh_u32x4 s, z;   // scales / zeros of columns 8*(t/16) .. +7 for the slab's group
-};
-
+// Weight-slab producer for tiled_f16_gemm: thread t dequantizes rows 2*(t%16), +1 of the slab
+// for the 8 columns of packed word column t/16 and stores them k-major per column.
 template <bool BF16>
-__global__ __launch_bounds__(256) void w4a16_tiled_kernel(
-    const uint16_t* __restrict__ x, const uint32_t* __restrict__ qw,
-    const uint16_t* __restrict__ scales, const uint16_t* __restrict__ zeros,
-    uint16_t* __restrict__ y, int M, int N, int K, int group) {
-  __shared__ __attribute__((aligned(16))) uint16_t As[2][TBM * TLD];
-  __shared__ __attribute__((aligned(16))) uint16_t Bs[2][TBN * TLD];
-
-  const int t = threadIdx.x;
-  const int lane = t & 63, wave = t >> 6;
-  const int wm = wave >> 1, wn = wave & 1;
-  const int ntn = N / TBN;
-  const int id = xcd_remap(blockIdx.x, gridDim.x);
-  const int mb = id / ntn, nb = id - mb * ntn;
-  const int m0 = mb * TBM, n0 = nb * TBN;
-  const int NP = N >> 3;
-  const int KT = K / TBK;
-
-  const int a_ch = t & 3, a_row = t >> 2;
-  const int b_kp = t & 15, b_wc = t >> 4;
-  const uint16_t* xrow[4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int r = m0 + a_row + 64 * i;
-    xrow[i] = x + (size_t)(r < M ? r : M - 1) * K + a_ch * 8;  // rows >= M are never stored
+struct W4SlabPolicy {
+  const uint32_t* qw;
+  const uint16_t* scales;
+  const uint16_t* zeros;
+  int N, group;
+  struct Regs {
+    uint32_t b[2];
+    kbh_u32x4 s, z;
+  };
+  __device__ void load(Regs& r, int k0, int n0, int t) const {
+    const int kp = t & 15, wc = t >> 4;
+    const int NP = N >> 3;
+    const uint32_t* q = qw + (size_t)(k0 + 2 * kp) * NP + (n0 >> 3) + wc;
+    r.b[0] = __builtin_nontemporal_load(q);
+    r.b[1] = __builtin_nontemporal_load(q + NP);
+    const size_t off = (size_t)(k0 / group) * N + n0 + 8 * wc;
+    r.s = *reinterpret_cast<const kbh_u32x4*>(scales + off);
+    r.z = *reinterpret_cast<const kbh_u32x4*>(zeros + off);
   }
-  const uint32_t* qcol = qw + (size_t)(2 * b_kp) * NP + (n0 >> 3) + b_wc;
-  const size_t scol = (size_t)n0 + 8 * b_wc;
-
-  auto load = [&](TiledSlab& sl, int kt) {
-    const int k0 = kt * TBK;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) sl.a[i] = *reinterpret_cast<const kbh_u32x4*>(xrow[i] + k0);
-    const uint32_t* q = qcol + (size_t)k0 * NP;
-    sl.b[0] = __builtin_nontemporal_load(q);
-    sl.b[1] = __builtin_nontemporal_load(q + NP);
-    const size_t off = (size_t)(k0 / group) * N + scol;
-    sl.s = *reinterpret_cast<const kbh_u32x4*>(scales + off);
-    sl.z = *reinterpret_cast<const kbh_u32x4*>(zeros + off);
-  };
-  auto store_a = [&](const TiledSlab& sl, int buf) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-      *reinterpret_cast<kbh_u32x4*>(&As[buf][(a_row + 64 * i) * TLD + a_ch * 8]) = sl.a[i];
-  };
-  auto store_b = [&](const TiledSlab& sl, int buf) {
+  __device__ void store(const Regs& r, uint16_t* Bs, int t) const {
+    const int kp = t & 15, wc = t >> 4;
     uint32_t dq[8];
-    dequant_2x8<BF16>(sl.b[0], sl.b[1], sl.s, sl.z, dq);
+    dequant_2x8<BF16>(r.b[0], r.b[1], r.s, r.z, dq);
 #pragma unroll
-    for (int c = 0; c < 8; ++c)
-      *reinterpret_cast<uint32_t*>(&Bs[buf][(b_wc * 8 + c) * TLD + 2 * b_kp]) = dq[c];
-  };
-  auto store = [&](const TiledSlab& sl, int buf) {
-    store_a(sl, buf);
-    store_b(sl, buf);
-  };
-
-  kbh_f32x16 accv[4][2];
-#pragma unroll
-  for (int i = 0; i < 4; ++i)
-#pragma unroll
-    for (int j = 0; j < 2; ++j)
-#pragma unroll
-      for (int e = 0; e < 16; ++e) accv[i][j][e] = 0.f;
-
-  const int fr = lane & 31, fk = (lane >> 5) * 8;
-  // One 16-wide K step of the wave's 128x64 tile: 6 LDS fragment reads, 8 MFMAs.
-  auto mma_k16 = [&](int buf, int kk) {
-    const uint16_t* Ab = &As[buf][(wm * 128 + fr) * TLD + fk + kk * 16];
-    const uint16_t* Bb = &Bs[buf][(wn * 64 + fr) * TLD + fk + kk * 16];
-    kbh_u32x4 a[4], b[2];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) a[i] = *reinterpret_cast<const kbh_u32x4*>(Ab + i * 32 * TLD);
-#pragma unroll
-    for (int j = 0; j < 2; ++j) b[j] = *reinterpret_cast<const kbh_u32x4*>(Bb + j * 32 * TLD);
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-      for (int j = 0; j < 2; ++j) accv[i][j] = mfma32x32x16<BF16>(a[i], b[j], accv[i][j]);
-  };
-
-  // Register ring: slab j lives in stage j % TDEPTH from its load until its LDS store. KT is a
-  // multiple of TDEPTH and loads past the last slab re-read it, so the steady-state loop has no
-  // branches (a conditional load would make the compiler wait for every load in flight).
-  TiledSlab ring[TDEPTH];
-#pragma unroll
-  for (int d = 0; d < TDEPTH; ++d) load(ring[d], d);
-  store(ring[0], 0);
-  load(ring[0], min(TDEPTH, KT - 1));
-  __syncthreads();
-
-  for (int kt0 = 0; kt0 < KT; kt0 += TDEPTH) {
-#pragma unroll
-    for (int d = 0; d < TDEPTH; ++d) {
-      const int kt = kt0 + d;
-      const int nxt = (d + 1) % TDEPTH;      // stage of slab kt+1
-      // The MFMAs of slab kt run asynchronously while the wave stages slab kt+1 (x copy,
-      // dequantization) into the other LDS buffer; after the last slab that buffer is unused.
-      mma_k16(kt & 1, 0);
-      store_a(ring[nxt], (kt + 1) & 1);
-      mma_k16(kt & 1, 1);
-      store_b(ring[nxt], (kt + 1) & 1);
-      load(ring[nxt], min(kt + 1 + TDEPTH, KT - 1));
-      __syncthreads();
-    }
+    for (int c = 0; c < 8; ++c) *reinterpret_cast<uint32_t*>(&Bs[(wc * 8 + c) * TLD + 2 * kp]) = dq[c];
   }
-
-  // epilogue: accumulator element e of tile (i, j) is row 8(e/4) + 4(l/32) + e%4, column l%32
-#pragma unroll
-  for (int i = 0; i < 4; ++i)
-#pragma unroll
-    for (int j = 0; j < 2; ++j)
-#pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        const int r = m0 + wm * 128 + i * 32 + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
-        const int n = n0 + wn * 64 + j * 32 + (lane & 31);
-        if (r < M) y[(size_t)r * N + n] = f32_to_half_bits<BF16>(accv[i][j][e]);
-      }
-}
+};
 
 // The tiled kernel beats the split-K decode kernel once the 256-row tiles are reasonably full.
 constexpr int kTiledMinM = 128;
@@ -473,10 +309,7 @@ constexpr int kTiledMinM = 128;
 extern "C" size_t kbh_w4a16_workspace_bytes(int M, int N, int K, int group) {
   (void)K;
   (void)group;
-  if (M <= 0 || N <= 0) return 0;
-  const size_t acc = kbh::round_up((size_t)M * (size_t)N * 4u, 256);
-  const size_t cnt = kbh::round_up((size_t)((M + 15) / 16) * (size_t)(N / 128 + 1) * 4u, 256);
-  return acc + cnt;
+  return kbh::splitk_workspace_bytes(M, N);
 }
 
 extern "C" int kbh_w4a16_gemm(const void* x, const int32_t* qweight, const void* scales,
@@ -495,22 +328,24 @@ extern "C" int kbh_w4a16_gemm(const void* x, const int32_t* qweight, const void*
   hipStream_t st = (hipStream_t)stream;
 
   if (M >= kTiledMinM && K % (TBK * TDEPTH) == 0) {
-    const int tiles = ((M + TBM - 1) / TBM) * (N / TBN);
-    if (bf)
-      hipLaunchKernelGGL(w4a16_tiled_kernel<true>, dim3(tiles), dim3(256), 0, st,
-                         (const uint16_t*)x, (const uint32_t*)qweight, (const uint16_t*)scales,
-                         (const uint16_t*)zeros, (uint16_t*)y, M, N, K, group);
-    else
-      hipLaunchKernelGGL(w4a16_tiled_kernel<false>, dim3(tiles), dim3(256), 0, st,
-                         (const uint16_t*)x, (const uint32_t*)qweight, (const uint16_t*)scales,
-                         (const uint16_t*)zeros, (uint16_t*)y, M, N, K, group);
+    if (bf) {
+      const W4SlabPolicy<true> bp{(const uint32_t*)qweight, (const uint16_t*)scales,
+                                  (const uint16_t*)zeros, N, group};
+      hipLaunchKernelGGL((tiled_f16_gemm<true, W4SlabPolicy<true>>), tiled_f16_grid(M, N),
+                         dim3(256), 0, st, (const uint16_t*)x, bp, (uint16_t*)y, M, N, K);
+    } else {
+      const W4SlabPolicy<false> bp{(const uint32_t*)qweight, (const uint16_t*)scales,
+                                   (const uint16_t*)zeros, N, group};
+      hipLaunchKernelGGL((tiled_f16_gemm<false, W4SlabPolicy<false>>), tiled_f16_grid(M, N),
+                         dim3(256), 0, st, (const uint16_t*)x, bp, (uint16_t*)y, M, N, K);
+    }
     return launch_status();
   }
 
   const size_t need = kbh_w4a16_workspace_bytes(M, N, K, group);
   if (!workspace || workspace_bytes < need) return KBH_ERR_WORKSPACE;
   float* acc = (float*)workspace;
-  int* counters = (int*)((char*)workspace + round_up((size_t)M * (size_t)N * 4u, 256));
+  int* counters = splitk_counters(workspace, M, N);
   DecodePlan p;
   if (!plan_decode(M, N, K, group / 32, &p)) return KBH_ERR_SHAPE;
   if (bf) dispatch_decode<true>(p, x, qweight, scales, zeros, y, acc, counters, M, N, K, group, st);

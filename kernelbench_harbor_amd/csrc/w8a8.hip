@@ -15,6 +15,7 @@
 // w8a8_tiled_kernel (larger M): 256x128 tile, 64-deep K slabs in a register ring, the weight
 // slab transposed into LDS k-major per column, 2x2 waves of 128x64 with 32x32x32 int8 MFMAs.
 #include "kbh_common.h"
+#include "splitk.h"
 
 namespace kbh {
 namespace {
@@ -51,18 +52,15 @@ __device__ inline uint16_t w8a8_epilogue(int acc, uint16_t xs, uint16_t ws) {
 // ======================================================================================
 // Decode kernel
 // ======================================================================================
-constexpr int kW8MaxWaves = 8;
-constexpr int kW8CsStride = 260;
 
 template <int SPW, bool OUT_I32>
-__global__ __launch_bounds__(kW8MaxWaves * 64) void w8a8_decode_kernel(
+__global__ __launch_bounds__(kSplitKMaxWaves * 64) void w8a8_decode_kernel(
     const int8_t* __restrict__ x, const int8_t* __restrict__ w, const uint16_t* __restrict__ xs,
     const uint16_t* __restrict__ wsc, void* __restrict__ out, int* __restrict__ acc,
     int* __restrict__ counters, int M, int N, int K, int splits) {
   constexpr int NWG = 128;  // columns per workgroup: 16 lanes x 8 columns
   constexpr int NCS = 8;    // MFMA column sets per wave
-  __shared__ int red[kW8MaxWaves * NCS * kW8CsStride];
-  __shared__ int s_last;
+  __shared__ SplitKSmem<NCS, int> sm;
   const int waves = blockDim.x >> 6;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int c = lane & 15, g = lane >> 4;
@@ -115,60 +113,15 @@ __global__ __launch_bounds__(kW8MaxWaves * 64) void w8a8_decode_kernel(
     }
   }
 
-  // Slice element (cs, row 4g+i, lane column c) at cs*stride + i*64 + lane; output column
-  // n = n0 + 8c + cs.
-  {
-    int* slice = red + wave * NCS * kW8CsStride;
-#pragma unroll
-    for (int cs = 0; cs < NCS; ++cs)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) slice[cs * kW8CsStride + i * 64 + lane] = accv[cs][i];
-  }
-  __syncthreads();
-  auto lds_sum = [&](int r, int n) {
-    const int cc = n >> 3, cs = n & 7;
-    const int off = cs * kW8CsStride + (r & 3) * 64 + (r >> 2) * 16 + cc;
-    int v = 0;
-    for (int wv = 0; wv < waves; ++wv) v += red[wv * NCS * kW8CsStride + off];
-    return v;
-  };
+  // Lane column c owns output columns n0 + 8c + cs.
   const int rows = min(16, M - m0);
-  auto emit = [&](int r, int n, int v) {
-    const size_t o = (size_t)(m0 + r) * N + n0 + n;
-    if constexpr (OUT_I32) reinterpret_cast<int*>(out)[o] = v;
-    else reinterpret_cast<uint16_t*>(out)[o] = w8a8_epilogue(v, xs[m0 + r], wsc[n0 + n]);
-  };
-  if (splits == 1) {
-    for (int e = threadIdx.x; e < rows * NWG; e += blockDim.x) {
-      const int r = e / NWG, n = e - r * NWG;
-      emit(r, n, lds_sum(r, n));
-    }
-    return;
-  }
-  // Cross-workgroup reduction with agent-scope int32 atomics (exact); see w4a16.hip for the
-  // arrival protocol.
-  for (int e = threadIdx.x; e < rows * NWG; e += blockDim.x) {
-    const int r = e / NWG, n = e - r * NWG;
-    __hip_atomic_fetch_add(&acc[(size_t)(m0 + r) * N + n0 + n], lds_sum(r, n), __ATOMIC_RELAXED,
-                           __HIP_MEMORY_SCOPE_AGENT);
-  }
-  __builtin_amdgcn_s_waitcnt(0);
-  __syncthreads();
-  int* counter = &counters[blockIdx.y * ntiles + tile];
-  if (threadIdx.x == 0) {
-    const int prev = __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    s_last = (prev == splits - 1);
-  }
-  __syncthreads();
-  if (!s_last) return;
-  for (int e = threadIdx.x; e < rows * NWG; e += blockDim.x) {
-    const int r = e / NWG, n = e - r * NWG;
-    int* p = &acc[(size_t)(m0 + r) * N + n0 + n];
-    const int v = __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    __hip_atomic_store(p, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    emit(r, n, v);
-  }
-  if (threadIdx.x == 0) __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  splitk_finish<NCS, int>(accv, sm, acc, &counters[blockIdx.y * ntiles + tile], splits, rows, N, m0,
+                          n0, [&](int r, int n, int v) {
+                            const size_t o = (size_t)(m0 + r) * N + n0 + n;
+                            if constexpr (OUT_I32) reinterpret_cast<int*>(out)[o] = v;
+                            else reinterpret_cast<uint16_t*>(out)[o] =
+                                     w8a8_epilogue(v, xs[m0 + r], wsc[n0 + n]);
+                          });
 }
 
 struct W8Plan {
@@ -181,17 +134,8 @@ bool plan_w8_decode(int M, int N, int K, W8Plan* p) {
   p->mblocks = (M + 15) / 16;
   p->spw = (nsteps % 2 == 0) ? 2 : 1;
   const int units = nsteps / p->spw;
-  int best_w = -1, best_score = 1 << 30;
-  for (int wv = kW8MaxWaves; wv >= 1; --wv) {
-    if (units % wv) continue;
-    const int grid = p->ntiles * (units / wv) * p->mblocks;
-    const int score = grid < 256 ? (256 - grid) * 4 : (grid > 512 ? grid - 512 : 0) + (8 - wv);
-    if (score < best_score) { best_score = score; best_w = wv; }
-  }
-  if (best_w < 0) return false;
-  p->waves = best_w;
-  p->splits = units / best_w;
-  return true;
+  p->waves = splitk_pick_waves(units, p->ntiles * p->mblocks, &p->splits);
+  return p->waves > 0;
 }
 
 // ======================================================================================
@@ -330,7 +274,7 @@ int w8a8_run(const void* x, const void* w, const void* xs, const void* wsc, void
   const size_t need = kbh_w8a8_workspace_bytes(M, N, K);
   if (!workspace || workspace_bytes < need) return KBH_ERR_WORKSPACE;
   int* acc = (int*)workspace;
-  int* counters = (int*)((char*)workspace + round_up((size_t)M * (size_t)N * 4u, 256));
+  int* counters = splitk_counters(workspace, M, N);
   W8Plan p;
   if (!plan_w8_decode(M, N, K, &p)) return KBH_ERR_SHAPE;
   dim3 grid(p.ntiles * p.splits, p.mblocks);
@@ -358,9 +302,7 @@ int w8a8_check(const void* x, const void* w, const void* xs, const void* wsc, co
 
 extern "C" size_t kbh_w8a8_workspace_bytes(int M, int N, int K) {
   (void)K;
-  if (M <= 0 || N <= 0) return 0;
-  return kbh::round_up((size_t)M * (size_t)N * 4u, 256) +
-         kbh::round_up((size_t)((M + 15) / 16) * (size_t)(N / 128 + 1) * 4u, 256);
+  return kbh::splitk_workspace_bytes(M, N);
 }
 
 extern "C" int kbh_w8a8_gemm(const int8_t* x_int8, const int8_t* w_int8, const void* x_scale,

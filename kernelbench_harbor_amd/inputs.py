@@ -71,3 +71,14 @@ def w8a8(M: int, K: int = 14336, N: int = 4096, seed: int = 0, dist: str = "base
     x_int8 = torch.round(xs_ / x_scale.float()).clamp(-127, 127).to(torch.int8)
     w_int8 = torch.round(Ws_ / w_scale.float()).clamp(-127, 127).to(torch.int8)
     return [x_int8, w_int8, x_scale, w_scale]
+
+
+def fp8w(M: int, K: int = 14336, N: int = 4096, block: int = 128,
+         dtype: torch.dtype = torch.float16, seed: int = 0):
+    """[x, w_fp8, scales] with the distributions of reference.py:14-19 (FP8 task): x ~ N(0,1),
+    w = (N(0,1) * 0.3) cast to float8_e4m3fn, scales U[0.05, 0.10] fp16 [K/block, N]."""
+    g = _gen(seed)
+    x = torch.randn(M, K, generator=g).to(dtype)
+    w_fp8 = (torch.randn(K, N, generator=g) * 0.3).to(torch.float8_e4m3fn)
+    scales = (torch.rand(K // block, N, generator=g) * 0.05 + 0.05).to(torch.float16)
+    return [x, w_fp8, scales]

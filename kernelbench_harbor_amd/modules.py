@@ -32,3 +32,14 @@ class W8A8Model(nn.Module):
 
     def forward(self, x_int8, w_int8, x_scale, w_scale):
         return ops.w8a8_gemm(x_int8, w_int8, x_scale, w_scale)
+
+
+class FP8WModel(nn.Module):
+    """FP8 (e4m3) block-microscaled weight GEMM.
+
+    Reference: tasks/fp8_microscale/*/environment/reference.py:9-12,
+    forward(x [M,K], w_fp8 [K,N] float8_e4m3fn, scales [K/B,N] fp16) -> [M,N] x.dtype.
+    """
+
+    def forward(self, x, w_fp8, scales):
+        return ops.fp8w_gemm(x, w_fp8, scales)

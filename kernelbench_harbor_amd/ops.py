@@ -147,3 +147,37 @@ def w8a8_gemm_i32(x_int8: torch.Tensor, w_int8: torch.Tensor) -> torch.Tensor:
                                ws.numel(), M, N, K, _stream_ptr(dev))
     _lib.check(st, "kbh_w8a8_gemm_i32")
     return acc
+
+
+def fp8w_gemm(x: torch.Tensor, w_fp8: torch.Tensor, scales: torch.Tensor) -> torch.Tensor:
+    """y = x @ (fp32(w_fp8) * fp32(scales[k // B])).to(x.dtype), the FP8 block-scaled weight GEMM.
+
+    Follows tasks/fp8_microscale/fp8_microscale__llama3_8b_down__b128__fp16/environment/
+    reference.py:9-12: w_fp8 [K, N] float8_e4m3fn, scales [K/B, N] fp16; the block size B is
+    K / scales.shape[0]."""
+    _require(x.dtype in _DT_CODE, f"x must be float16 or bfloat16, got {x.dtype}")
+    _require(w_fp8.dtype in (torch.float8_e4m3fn, torch.uint8),
+             f"w_fp8 must be float8_e4m3fn (or its uint8 bits), got {w_fp8.dtype}")
+    _require(w_fp8.dim() == 2 and scales.dim() == 2, "w_fp8 and scales must be 2-D")
+    K, N = w_fp8.shape
+    _require(x.shape[-1] == K, f"x last dim {x.shape[-1]} != K={K}")
+    _require(scales.dtype == torch.float16, f"scales must be float16, got {scales.dtype}")
+    _require(scales.shape[1] == N and scales.shape[0] > 0 and K % scales.shape[0] == 0,
+             f"scales must be [K/B, {N}], got {tuple(scales.shape)}")
+    block = K // scales.shape[0]
+    dev = _check_device(x, w_fp8, scales)
+    lead = x.shape[:-1]
+    x2 = x.reshape(-1, K).contiguous()
+    M = x2.shape[0]
+    y = torch.empty((M, N), dtype=x.dtype, device=dev)
+    if M == 0:
+        return y.reshape(*lead, N)
+    w8 = w_fp8.contiguous().view(torch.uint8)
+    sc = scales.contiguous()
+    lib = _lib.load()
+    ws = workspaces.get(lib.kbh_fp8w_workspace_bytes(M, N, K, block), dev)
+    st = lib.kbh_fp8w_gemm(x2.data_ptr(), w8.data_ptr(), sc.data_ptr(), y.data_ptr(),
+                           ws.data_ptr(), ws.numel(), M, N, K, block, _DT_CODE[x.dtype],
+                           _stream_ptr(dev))
+    _lib.check(st, "kbh_fp8w_gemm")
+    return y.reshape(*lead, N)
