@@ -106,6 +106,24 @@ int kbh_fp8w_gemm(const void* x, const uint8_t* w_fp8, const void* scales, void*
                   void* workspace, size_t workspace_bytes, int M, int N, int K, int block,
                   int dtype, void* stream);
 
+/* ---------------------------------------------------------------------------------------
+ * MXFP8 block-scaled GEMM (OCP MX: e4m3 elements, one e8m0 exponent per 1x32 block along K).
+ * No counterpart module in the reference: it extends the FP8 family (tasks/fp8_microscale/<task>/
+ * environment/reference.py:9-12) to both operands, with the block quantisation of
+ * generate_tasks.py:337-342 (absmax / 448, e4m3 cast) and power-of-two scales.
+ *
+ *   a [M, K] e4m3fn codes, a_scale [M, K/32] e8m0 codes
+ *   b [N, K] e4m3fn codes, b_scale [N, K/32] e8m0 codes
+ *   y [M, N] out_dtype,  y[m, n] = sum_k a[m,k] 2^(a_scale[m,k/32]-127) b[n,k] 2^(b_scale[n,k/32]-127)
+ * Requirements: M >= 1, N % 64 == 0, K % 256 == 0, a/b/y 16-byte and scales 4-byte aligned.
+ * workspace: used when K is split across workgroups (small M); same contract as
+ * kbh_w4a16_gemm, size from kbh_mxfp8_workspace_bytes().
+ */
+size_t kbh_mxfp8_workspace_bytes(int M, int N, int K);
+int kbh_mxfp8_gemm(const uint8_t* a, const uint8_t* a_scale, const uint8_t* b,
+                   const uint8_t* b_scale, void* y, void* workspace, size_t workspace_bytes,
+                   int M, int N, int K, int out_dtype, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -82,3 +82,31 @@ def fp8w(M: int, K: int = 14336, N: int = 4096, block: int = 128,
     w_fp8 = (torch.randn(K, N, generator=g) * 0.3).to(torch.float8_e4m3fn)
     scales = (torch.rand(K // block, N, generator=g) * 0.05 + 0.05).to(torch.float16)
     return [x, w_fp8, scales]
+
+
+def mx_quantize(src: torch.Tensor):
+    """OCP MX block quantisation of float32 rows along the last dim in 1x32 blocks: scale =
+    2^ceil(log2(amax/448)) (e8m0 code = exponent + 127; amax = 0 gives code 0 and zero
+    elements), elements = e4m3fn(x / scale) rounded to nearest even. Returns (codes uint8,
+    scales uint8)."""
+    R, K = src.shape
+    blk = src.float().reshape(R, K // 32, 32)
+    amax = blk.abs().amax(dim=-1)
+    mant, expo = torch.frexp(amax / 448.0)
+    ceil_log2 = expo - (mant == 0.5).to(expo.dtype)      # exact ceil(log2(v)) for v > 0
+    code = (ceil_log2 + 127).clamp(0, 254)
+    code = torch.where(amax > 0, code, torch.zeros_like(code))
+    scale = torch.ldexp(torch.ones_like(amax), code - 127)
+    q = (blk / scale[..., None]).to(torch.float8_e4m3fn)
+    return q.reshape(R, K).view(torch.uint8), code.to(torch.uint8)
+
+
+def mxfp8(M: int, K: int = 14336, N: int = 4096, seed: int = 0):
+    """[a, a_scale, b, b_scale] for BASELINE configuration 3: fp32 sources ~ N(0,1), [M, K] and
+    [N, K], MX-quantised along K."""
+    g = _gen(seed)
+    a_src = torch.randn(M, K, generator=g)
+    b_src = torch.randn(N, K, generator=g)
+    a, a_s = mx_quantize(a_src)
+    b, b_s = mx_quantize(b_src)
+    return [a, a_s, b, b_s]

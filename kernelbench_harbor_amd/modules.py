@@ -43,3 +43,14 @@ class FP8WModel(nn.Module):
 
     def forward(self, x, w_fp8, scales):
         return ops.fp8w_gemm(x, w_fp8, scales)
+
+
+class MXFP8Model(nn.Module):
+    """MXFP8 block-scaled GEMM (both operands e4m3, e8m0 1x32 scales), fp16 output.
+
+    No reference module: written in the reference's Model idiom for the BASELINE MXFP8
+    configuration. forward(a [M,K], a_scale [M,K/32], b [N,K], b_scale [N,K/32]) -> [M,N] fp16.
+    """
+
+    def forward(self, a, a_scale, b, b_scale):
+        return ops.mxfp8_gemm(a, a_scale, b, b_scale)

@@ -181,3 +181,39 @@ def fp8w_gemm(x: torch.Tensor, w_fp8: torch.Tensor, scales: torch.Tensor) -> tor
                            _stream_ptr(dev))
     _lib.check(st, "kbh_fp8w_gemm")
     return y.reshape(*lead, N)
+
+
+_BYTE_DTYPES = (torch.uint8, torch.float8_e4m3fn)
+
+
+def _as_bytes(t: torch.Tensor) -> torch.Tensor:
+    return t.contiguous().view(torch.uint8)
+
+
+def mxfp8_gemm(a: torch.Tensor, a_scale: torch.Tensor, b: torch.Tensor, b_scale: torch.Tensor,
+               out_dtype: torch.dtype = torch.float16) -> torch.Tensor:
+    """MXFP8 GEMM: y[m, n] = sum_k dec(a[m, k]) dec(b[n, k]) with per-1x32-block e8m0 scales.
+
+    a [M, K] and b [N, K] are float8_e4m3fn (or their uint8 bits), K-contiguous; a_scale
+    [M, K/32] and b_scale [N, K/32] are e8m0 codes (uint8, or float8_e8m0fnu)."""
+    _require(out_dtype in _DT_CODE, f"out_dtype must be float16 or bfloat16, got {out_dtype}")
+    _require(a.dtype in _BYTE_DTYPES and b.dtype in _BYTE_DTYPES,
+             f"a and b must be float8_e4m3fn or uint8, got {a.dtype}/{b.dtype}")
+    sdt = (torch.uint8,) + ((torch.float8_e8m0fnu,) if hasattr(torch, "float8_e8m0fnu") else ())
+    _require(a_scale.dtype in sdt and b_scale.dtype in sdt, "scales must be e8m0 codes (uint8)")
+    _require(a.dim() == 2 and b.dim() == 2, "a and b must be 2-D")
+    M, K = a.shape
+    N = b.shape[0]
+    _require(b.shape[1] == K, f"b must be [N, {K}], got {tuple(b.shape)}")
+    _require(K % 32 == 0 and a_scale.shape == (M, K // 32) and b_scale.shape == (N, K // 32),
+             f"scales must be [M, K/32] and [N, K/32]")
+    dev = _check_device(a, a_scale, b, b_scale)
+    y = torch.empty((M, N), dtype=out_dtype, device=dev)
+    lib = _lib.load()
+    ws = workspaces.get(lib.kbh_mxfp8_workspace_bytes(M, N, K), dev)
+    a8, b8, as8, bs8 = _as_bytes(a), _as_bytes(b), _as_bytes(a_scale), _as_bytes(b_scale)
+    st = lib.kbh_mxfp8_gemm(a8.data_ptr(), as8.data_ptr(), b8.data_ptr(), bs8.data_ptr(),
+                            y.data_ptr(), ws.data_ptr(), ws.numel(), M, N, K, _DT_CODE[out_dtype],
+                            _stream_ptr(dev))
+    _lib.check(st, "kbh_mxfp8_gemm")
+    return y
