@@ -124,6 +124,44 @@ int kbh_mxfp8_gemm(const uint8_t* a, const uint8_t* a_scale, const uint8_t* b,
                    const uint8_t* b_scale, void* y, void* workspace, size_t workspace_bytes,
                    int M, int N, int K, int out_dtype, void* stream);
 
+/* ---------------------------------------------------------------------------------------
+ * Top-2 quantized mixture of experts.
+ *
+ * kbh_moe_route_top2: the routing stage of tasks/fused_qmoe/fused_qmoe__mixtral__fp16/
+ * environment/reference.py:14-16: probs = softmax(fp32(logits)), top-2, weights renormalised
+ * and rounded to dtype. topi [T, 2] int32 (descending probability), topw [T, 2] dtype.
+ * logits_dtype: 0 fp16, 1 bf16, 2 fp32. workspace >= kbh_qmoe_workspace_bytes(T, 0, 0, E).
+ *
+ * kbh_qmoe replaces reference.py:11-21 (Model.forward(x, qweight, scales, router_logits);
+ * template generate_tasks.py:358-387):
+ *   x [T, D] dtype; qweight [E, D, N] int8 holding int4 values; scales [E, D/group, N] dtype;
+ *   router_logits [T, E] (logits_dtype);  y [T, N] dtype,
+ *   y[t] = sum_k dtype(dtype(x[t] @ dtype(dtype(q_e) * s_e)) * w[t, k]),  e = topi[t, k].
+ * Only the routed (token, expert) pairs are computed.
+ *
+ * kbh_qmoe_ffn: the SiLU-gated FFN of the same routing (no reference module; routing and
+ * combine as above, W4A16 dequantisation as kbh_w4a16_gemm):
+ *   gate/up qweight [E, D, F/8] int32, scales/zeros [E, D/group, F];
+ *   down qweight [E, F, D/8] int32, scales/zeros [E, F/group, D];
+ *   h = dtype(silu(x @ Wg) * (x @ Wu)), o = dtype(h @ Wd), y[t] = sum_k dtype(o_k * w[t, k]).
+ * Requirements: E in [2, 256]; D, N, F multiples of 128; group in {32, 64, 128, 256}.
+ * workspace: no zero-fill needed; sizes from the *_workspace_bytes functions.
+ */
+size_t kbh_qmoe_workspace_bytes(int T, int D, int N, int E);
+int kbh_moe_route_top2(const void* router_logits, int logits_dtype, int32_t* topi, void* topw,
+                       void* workspace, size_t workspace_bytes, int T, int E, int dtype,
+                       void* stream);
+int kbh_qmoe(const void* x, const int8_t* qweight, const void* scales, const void* router_logits,
+             int logits_dtype, void* y, void* workspace, size_t workspace_bytes, int T, int D,
+             int N, int E, int group, int dtype, void* stream);
+size_t kbh_qmoe_ffn_workspace_bytes(int T, int D, int F, int E);
+int kbh_qmoe_ffn(const void* x, const void* router_logits, int logits_dtype,
+                 const int32_t* gate_qweight, const void* gate_scales, const void* gate_zeros,
+                 const int32_t* up_qweight, const void* up_scales, const void* up_zeros,
+                 const int32_t* down_qweight, const void* down_scales, const void* down_zeros,
+                 void* y, void* workspace, size_t workspace_bytes, int T, int D, int F, int E,
+                 int group, int dtype, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -45,6 +45,11 @@ SIGNATURES = {
     "kbh_fp8w_gemm": (_i, [_vp, _vp, _vp, _vp, _vp, _sz, _i, _i, _i, _i, _i, _vp]),
     "kbh_mxfp8_workspace_bytes": (_sz, [_i, _i, _i]),
     "kbh_mxfp8_gemm": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _sz, _i, _i, _i, _i, _vp]),
+    "kbh_qmoe_workspace_bytes": (_sz, [_i, _i, _i, _i]),
+    "kbh_moe_route_top2": (_i, [_vp, _i, _vp, _vp, _vp, _sz, _i, _i, _i, _vp]),
+    "kbh_qmoe": (_i, [_vp, _vp, _vp, _vp, _i, _vp, _vp, _sz, _i, _i, _i, _i, _i, _i, _vp]),
+    "kbh_qmoe_ffn_workspace_bytes": (_sz, [_i, _i, _i, _i]),
+    "kbh_qmoe_ffn": (_i, [_vp, _vp, _i] + [_vp] * 9 + [_vp, _vp, _sz, _i, _i, _i, _i, _i, _i, _vp]),
 }
 
 

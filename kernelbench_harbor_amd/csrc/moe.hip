@@ -1,0 +1,494 @@
+// Top-2 quantized mixture-of-experts on gfx950.
+//
+// Reference op (tasks/fused_qmoe/fused_qmoe__mixtral__fp16/environment/reference.py:11-21):
+//   probs = softmax(fp32(router_logits)); topv, topi = top2(probs); w = dtype(topv / sum(topv))
+//   W_e   = dtype(dtype(qweight[e]) * dtype(scales[e, d/G]))          (int4 values stored int8)
+//   y[t]  = sum_k dtype(dtype(x[t] @ W_{topi[t,k]}) * w[t,k])          (the gather of all_out)
+// SiLU FFN (no reference module, same routing and combine):
+//   h = dtype(silu(x @ Wg_e) * (x @ Wu_e)),  o = dtype(h @ Wd_e),  y[t] = sum_k dtype(o_k w_k)
+// with W4A16 g128 gate/up/down weights (packed along their output dimension).
+//
+// Kernels:
+//  * moe_route_kernel (one workgroup): softmax + top-2 per token, per-expert counts (LDS
+//    atomics), prefix sums, the slot permutation perm[slot] = 2t + k (slots grouped by expert)
+//    and a tile table of (expert, first slot, rows) with BM rows per tile; unused table entries
+//    get rows = 0. Only the routed (token, expert) pairs are computed downstream — the reference
+//    computes all experts densely (reference.py:19).
+//  * moe_gemm_kernel: expert-grouped GEMM. A workgroup takes one tile of one expert and 128
+//    output columns; x rows are gathered through perm, the expert's weights come from a slab
+//    policy (int8-stored int4 or packed int4, dequantized exactly into LDS), the K loop is the
+//    register-ring / two-LDS-buffer pipeline of tiled_f16.h, and the epilogue writes rows either
+//    per slot (the FFN intermediate h) or per (token, k) pair. GATED fuses two weight streams
+//    (gate and up) and applies silu(g) * u before rounding.
+//  * moe_combine_kernel: y[t] = dtype(o[2t] w[2t] + o[2t+1] w[2t+1]) with the reference's
+//    roundings (each product rounded to dtype, fp32 sum of the two, one rounding).
+#include "kbh_common.h"
+#include "tiled_f16.h"
+#include "w4_dequant.h"
+
+namespace kbh {
+namespace {
+
+constexpr int kMoeMaxExperts = 256;
+
+template <int LDT>  // logits dtype: 0 fp16, 1 bf16, 2 fp32
+__device__ inline float logit_at(const void* p, size_t i) {
+  if constexpr (LDT == 0) return f16_bits_to_f32(reinterpret_cast<const uint16_t*>(p)[i]);
+  else if constexpr (LDT == 1) return bf16_bits_to_f32(reinterpret_cast<const uint16_t*>(p)[i]);
+  else return reinterpret_cast<const float*>(p)[i];
+}
+
+struct MoeBuffers {
+  int* topi;        // [2T]
+  uint16_t* topw;   // [2T] routing weights in the activation dtype
+  int* slot_of;     // [2T] position of (t, k) inside its expert's slot range
+  int* perm;        // [2T] slot -> 2t + k
+  int* tiles;       // [max_tiles][3] = expert, first slot, rows
+};
+
+template <int LDT>
+__global__ __launch_bounds__(1024) void moe_route_kernel(const void* __restrict__ logits, int T,
+                                                         int E, int out_bf16, MoeBuffers mb,
+                                                         int max_tiles, int bm) {
+  __shared__ int cnt[kMoeMaxExperts];
+  __shared__ int off[kMoeMaxExperts];
+  __shared__ int tbase[kMoeMaxExperts + 1];
+  for (int e = threadIdx.x; e < E; e += blockDim.x) cnt[e] = 0;
+  __syncthreads();
+  for (int t = threadIdx.x; t < T; t += blockDim.x) {
+    const size_t row = (size_t)t * E;
+    float mx = -INFINITY;
+    int i0 = 0;
+    for (int e = 0; e < E; ++e) {
+      const float v = logit_at<LDT>(logits, row + e);
+      if (v > mx) { mx = v; i0 = e; }  // first index among equal maxima
+    }
+    float sum = 0.f, m1 = -INFINITY;
+    int i1 = (i0 == 0) ? 1 : 0;
+    for (int e = 0; e < E; ++e) {
+      const float v = logit_at<LDT>(logits, row + e);
+      sum += expf(v - mx);
+      if (e != i0 && v > m1) { m1 = v; i1 = e; }
+    }
+    // softmax probabilities of the two picks, renormalised (reference.py:14-16)
+    const float p0 = keep_f32(expf(logit_at<LDT>(logits, row + i0) - mx) / sum);
+    const float p1 = keep_f32(expf(logit_at<LDT>(logits, row + i1) - mx) / sum);
+    const float s = keep_f32(p0 + p1);
+    const float w0 = keep_f32(p0 / s), w1 = keep_f32(p1 / s);
+    mb.topi[2 * t] = i0;
+    mb.topi[2 * t + 1] = i1;
+    mb.topw[2 * t] = out_bf16 ? f32_to_bf16_bits(w0) : f32_to_f16_bits(w0);
+    mb.topw[2 * t + 1] = out_bf16 ? f32_to_bf16_bits(w1) : f32_to_f16_bits(w1);
+    mb.slot_of[2 * t] = atomicAdd(&cnt[i0], 1);
+    mb.slot_of[2 * t + 1] = atomicAdd(&cnt[i1], 1);
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    int o = 0, tb = 0;
+    for (int e = 0; e < E; ++e) {
+      off[e] = o;
+      tbase[e] = tb;
+      o += cnt[e];
+      tb += (cnt[e] + bm - 1) / bm;
+    }
+    tbase[E] = tb;
+  }
+  __syncthreads();
+  for (int i = threadIdx.x; i < 2 * T; i += blockDim.x)
+    mb.perm[off[mb.topi[i]] + mb.slot_of[i]] = i;
+  for (int e = threadIdx.x; e < E; e += blockDim.x) {
+    for (int j = 0; j < tbase[e + 1] - tbase[e]; ++j) {
+      int* tl = &mb.tiles[3 * (tbase[e] + j)];
+      tl[0] = e;
+      tl[1] = off[e] + j * bm;
+      tl[2] = min(bm, cnt[e] - j * bm);
+    }
+  }
+  for (int i = tbase[E] + threadIdx.x; i < max_tiles; i += blockDim.x) {
+    mb.tiles[3 * i] = 0;
+    mb.tiles[3 * i + 1] = 0;
+    mb.tiles[3 * i + 2] = 0;
+  }
+}
+
+// Slab producer for int8-stored weights [E][K][N] (N contiguous) with scales [E][K/G][N] in the
+// activation dtype: W = dtype(dtype(q) * s), one rounding (q is exact in either dtype).
+template <bool BF16>
+struct I8SlabPolicy {
+  const int8_t* w;
+  const uint16_t* scales;
+  int N, group;
+  size_t w_stride, s_stride;
+  __device__ I8SlabPolicy at_expert(int e) const {
+    I8SlabPolicy p = *this;
+    p.w += (size_t)e * w_stride;
+    p.scales += (size_t)e * s_stride;
+    return p;
+  }
+  struct Regs {
+    uint32_t b[4];
+    kbh_u32x2 s;
+  };
+  __device__ void load(Regs& r, int k0, int n0, int t) const {
+    const int cq = t & 31, rq = t >> 5;
+    const int8_t* p = w + (size_t)(k0 + 4 * rq) * N + n0 + 4 * cq;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      r.b[i] = __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(p + (size_t)i * N));
+    r.s = *reinterpret_cast<const kbh_u32x2*>(scales + (size_t)(k0 / group) * N + n0 + 4 * cq);
+  }
+  __device__ void store(const Regs& r, uint16_t* Bs, int t) const {
+    const int cq = t & 31, rq = t >> 5;
+    // 4x4 byte transpose: column j gets the 4 k values (rows 4rq..4rq+3)
+    const uint32_t t0 = __builtin_amdgcn_perm(r.b[1], r.b[0], 0x05010400u);
+    const uint32_t t1 = __builtin_amdgcn_perm(r.b[1], r.b[0], 0x07030602u);
+    const uint32_t t2 = __builtin_amdgcn_perm(r.b[3], r.b[2], 0x05010400u);
+    const uint32_t t3 = __builtin_amdgcn_perm(r.b[3], r.b[2], 0x07030602u);
+    const uint32_t cols[4] = {__builtin_amdgcn_perm(t2, t0, 0x05040100u),
+                              __builtin_amdgcn_perm(t2, t0, 0x07060302u),
+                              __builtin_amdgcn_perm(t3, t1, 0x05040100u),
+                              __builtin_amdgcn_perm(t3, t1, 0x07060302u)};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const uint16_t sb = (uint16_t)((j & 1) ? (r.s[j >> 1] >> 16) : (r.s[j >> 1] & 0xffffu));
+      const uint32_t v = cols[j];
+      kbh_u32x2 out;
+      if constexpr (BF16) {
+        const float sf = bf16_bits_to_f32(sb);
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          const float a = (float)(int8_t)(v >> (16 * h)) * sf;
+          const float b = (float)(int8_t)(v >> (16 * h + 8)) * sf;
+          out[h] = (uint32_t)f32_to_bf16_bits(a) | ((uint32_t)f32_to_bf16_bits(b) << 16);
+        }
+      } else {
+        // fp16 magic: (byte ^ 0x80) | 0x6400 is 1024 + (q + 128); minus 1152 gives q exactly.
+        typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+        const _Float16 sc = __builtin_bit_cast(_Float16, sb);
+        const _Float16 bias = (_Float16)1152.0f;
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          const uint32_t sel = h ? 0x0c030c02u : 0x0c010c00u;  // bytes 2h, 2h+1 -> halves
+          const uint32_t P = __builtin_amdgcn_perm(0u, v, sel);
+          const uint32_t hv = (P ^ 0x00800080u) | 0x64006400u;
+          const h2 q = __builtin_bit_cast(h2, hv) - h2{bias, bias};
+          out[h] = __builtin_bit_cast(uint32_t, q * h2{sc, sc});
+        }
+      }
+      *reinterpret_cast<kbh_u32x2*>(&Bs[(4 * cq + j) * TLD + 4 * rq]) = out;
+    }
+  }
+};
+
+__device__ inline float silu(float v) { return v / (1.0f + expf(-v)); }
+
+// Expert-grouped GEMM. BM = 64 (1x4 waves, 64x32 each) or 128 (2x2 waves, 64x64 each).
+template <bool BF16, int BM, class BP, bool GATHER, bool GATED, bool OUT_PERM>
+__global__ __launch_bounds__(256) void moe_gemm_kernel(const uint16_t* __restrict__ A, int lda,
+                                                       const int* __restrict__ perm,
+                                                       const int* __restrict__ tiles, BP bp,
+                                                       BP bp2, uint16_t* __restrict__ out,
+                                                       int ldo, int N, int K) {
+  constexpr int BN = 128;
+  constexpr int WM = BM / 64, WN = 4 / WM;  // waves along M and N
+  constexpr int WNT = BN / WN / 32;         // 32-column MFMA tiles per wave
+  constexpr int NB = GATED ? 2 : 1;
+  constexpr int AL = BM / 64;               // 16-byte x chunks per thread per slab
+  __shared__ __attribute__((aligned(16))) uint16_t As[2][BM * TLD];
+  __shared__ __attribute__((aligned(16))) uint16_t Bs[NB][2][BN * TLD];
+
+  const int* tl = &tiles[3 * blockIdx.y];
+  const int e = tl[0], s0 = tl[1], rows = tl[2];
+  if (rows == 0) return;  // unused tile-table entry (uniform across the workgroup)
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  const int wm = wave / WN, wn = wave % WN;
+  const int n0 = blockIdx.x * BN;
+  const BP bpe = bp.at_expert(e);
+  const BP bpe2 = bp2.at_expert(e);
+  const int KT = K / TBK;
+
+  const int a_ch = t & 3, a_row = t >> 2;
+  const uint16_t* arow[AL];
+#pragma unroll
+  for (int i = 0; i < AL; ++i) {
+    const int r = min(a_row + 64 * i, rows - 1);  // rows past the tile repeat the last one
+    const int s = s0 + r;
+    const int src = GATHER ? (perm[s] >> 1) : s;
+    arow[i] = A + (size_t)src * lda + a_ch * 8;
+  }
+  struct Slab {
+    kbh_u32x4 a[AL];
+    typename BP::Regs b[NB];
+  };
+  auto load = [&](Slab& sl, int kt) {
+    const int k0 = kt * TBK;
+#pragma unroll
+    for (int i = 0; i < AL; ++i) sl.a[i] = *reinterpret_cast<const kbh_u32x4*>(arow[i] + k0);
+    bpe.load(sl.b[0], k0, n0, t);
+    if constexpr (GATED) bpe2.load(sl.b[1], k0, n0, t);
+  };
+  auto store = [&](const Slab& sl, int buf) {
+#pragma unroll
+    for (int i = 0; i < AL; ++i)
+      *reinterpret_cast<kbh_u32x4*>(&As[buf][(a_row + 64 * i) * TLD + a_ch * 8]) = sl.a[i];
+    bpe.store(sl.b[0], Bs[0][buf], t);
+    if constexpr (GATED) bpe2.store(sl.b[1], Bs[1][buf], t);
+  };
+
+  kbh_f32x16 accv[NB][2][WNT];
+#pragma unroll
+  for (int q = 0; q < NB; ++q)
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int j = 0; j < WNT; ++j)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) accv[q][i][j][v] = 0.f;
+
+  const int fr = lane & 31, fk = (lane >> 5) * 8;
+  auto mma = [&](int buf) {
+#pragma unroll
+    for (int kk = 0; kk < TBK / 16; ++kk) {
+      kbh_u32x4 a[2];
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+        a[i] = *reinterpret_cast<const kbh_u32x4*>(&As[buf][(wm * 64 + i * 32 + fr) * TLD + fk + kk * 16]);
+#pragma unroll
+      for (int q = 0; q < NB; ++q)
+#pragma unroll
+        for (int j = 0; j < WNT; ++j) {
+          const kbh_u32x4 b = *reinterpret_cast<const kbh_u32x4*>(
+              &Bs[q][buf][(wn * 32 * WNT + j * 32 + fr) * TLD + fk + kk * 16]);
+#pragma unroll
+          for (int i = 0; i < 2; ++i) accv[q][i][j] = mfma32x32x16<BF16>(a[i], b, accv[q][i][j]);
+        }
+    }
+  };
+
+  Slab ring[TDEPTH];
+#pragma unroll
+  for (int d = 0; d < TDEPTH; ++d) load(ring[d], min(d, KT - 1));
+  store(ring[0], 0);
+  load(ring[0], min(TDEPTH, KT - 1));
+  __syncthreads();
+  for (int kt0 = 0; kt0 < KT; kt0 += TDEPTH) {
+#pragma unroll
+    for (int d = 0; d < TDEPTH; ++d) {
+      const int kt = kt0 + d;
+      const int nxt = (d + 1) % TDEPTH;
+      mma(kt & 1);
+      store(ring[nxt], (kt + 1) & 1);  // after the last slab: unused buffer
+      load(ring[nxt], min(kt + 1 + TDEPTH, KT - 1));
+      __syncthreads();
+    }
+  }
+
+  // Accumulator element v of tile (i, j): row 8(v/4) + 4(l/32) + v%4, column l%32.
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < WNT; ++j)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const int r = wm * 64 + i * 32 + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
+        if (r < rows) {
+          const int s = s0 + r;
+          const int orow = OUT_PERM ? perm[s] : s;
+          const int n = n0 + wn * 32 * WNT + j * 32 + fr;
+          float val = accv[0][i][j][v];
+          if constexpr (GATED) val = keep_f32(silu(val)) * accv[1][i][j][v];
+          out[(size_t)orow * ldo + n] = f32_to_half_bits<BF16>(val);
+        }
+      }
+}
+
+// y[t][n] = dtype(fp32(dtype(o0 * w0)) + fp32(dtype(o1 * w1))), o_k = o[2t+k][n].
+template <bool BF16>
+__global__ __launch_bounds__(256) void moe_combine_kernel(const uint16_t* __restrict__ o,
+                                                          const uint16_t* __restrict__ topw,
+                                                          uint16_t* __restrict__ y, int T, int N) {
+  const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= (size_t)T * N) return;
+  const size_t t = i / N, n = i - t * N;
+  const float p0 = half_bits_to_f32<BF16>(f32_to_half_bits<BF16>(
+      keep_f32(half_bits_to_f32<BF16>(o[(2 * t) * N + n]) * half_bits_to_f32<BF16>(topw[2 * t]))));
+  const float p1 = half_bits_to_f32<BF16>(f32_to_half_bits<BF16>(keep_f32(
+      half_bits_to_f32<BF16>(o[(2 * t + 1) * N + n]) * half_bits_to_f32<BF16>(topw[2 * t + 1]))));
+  y[i] = f32_to_half_bits<BF16>(keep_f32(p0 + p1));
+}
+
+// ---- host side ------------------------------------------------------------------------------
+struct MoeLayout {
+  size_t topi, topw, slot_of, perm, tiles, h, o, total;
+  int bm, max_tiles;
+};
+
+MoeLayout moe_layout(int T, int E, int hidden, int out_cols) {
+  MoeLayout L;
+  L.bm = (2 * T) / (E > 0 ? E : 1) > 96 ? 128 : 64;
+  L.max_tiles = (2 * T + L.bm - 1) / L.bm + E;
+  size_t o = 0;
+  auto take = [&](size_t bytes) {
+    const size_t at = o;
+    o += round_up(bytes, 256);
+    return at;
+  };
+  L.topi = take((size_t)2 * T * 4);
+  L.topw = take((size_t)2 * T * 2);
+  L.slot_of = take((size_t)2 * T * 4);
+  L.perm = take((size_t)2 * T * 4);
+  L.tiles = take((size_t)L.max_tiles * 3 * 4);
+  L.h = take((size_t)2 * T * hidden * 2);
+  L.o = take((size_t)2 * T * out_cols * 2);
+  L.total = o;
+  return L;
+}
+
+MoeBuffers moe_buffers(void* ws, const MoeLayout& L) {
+  char* b = (char*)ws;
+  return MoeBuffers{(int*)(b + L.topi), (uint16_t*)(b + L.topw), (int*)(b + L.slot_of),
+                    (int*)(b + L.perm), (int*)(b + L.tiles)};
+}
+
+void launch_route(const void* logits, int logits_dtype, int T, int E, bool bf16, const MoeBuffers& mb,
+                  const MoeLayout& L, hipStream_t st) {
+  const dim3 g(1), b(1024);
+  if (logits_dtype == 0)
+    hipLaunchKernelGGL(moe_route_kernel<0>, g, b, 0, st, logits, T, E, (int)bf16, mb, L.max_tiles, L.bm);
+  else if (logits_dtype == 1)
+    hipLaunchKernelGGL(moe_route_kernel<1>, g, b, 0, st, logits, T, E, (int)bf16, mb, L.max_tiles, L.bm);
+  else
+    hipLaunchKernelGGL(moe_route_kernel<2>, g, b, 0, st, logits, T, E, (int)bf16, mb, L.max_tiles, L.bm);
+}
+
+template <bool BF16, class BP, bool GATHER, bool GATED, bool OUT_PERM>
+void launch_moe_gemm(const MoeLayout& L, const void* A, int lda, const MoeBuffers& mb, const BP& bp,
+                     const BP& bp2, void* out, int ldo, int N, int K, hipStream_t st) {
+  const dim3 grid(N / 128, L.max_tiles);
+  if (L.bm == 64)
+    hipLaunchKernelGGL((moe_gemm_kernel<BF16, 64, BP, GATHER, GATED, OUT_PERM>), grid, dim3(256), 0,
+                       st, (const uint16_t*)A, lda, mb.perm, mb.tiles, bp, bp2, (uint16_t*)out, ldo, N, K);
+  else
+    hipLaunchKernelGGL((moe_gemm_kernel<BF16, 128, BP, GATHER, GATED, OUT_PERM>), grid, dim3(256), 0,
+                       st, (const uint16_t*)A, lda, mb.perm, mb.tiles, bp, bp2, (uint16_t*)out, ldo, N, K);
+}
+
+template <bool BF16>
+void launch_combine(const void* o, const uint16_t* topw, void* y, int T, int N, hipStream_t st) {
+  const size_t n = (size_t)T * N;
+  hipLaunchKernelGGL(moe_combine_kernel<BF16>, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st,
+                     (const uint16_t*)o, topw, (uint16_t*)y, T, N);
+}
+
+bool moe_shape_ok(int T, int E, int K, int N, int group) {
+  return T >= 1 && E >= 2 && E <= kMoeMaxExperts && N >= 128 && N % 128 == 0 && K >= 128 &&
+         K % (TBK * TDEPTH) == 0 && (group == 32 || group == 64 || group == 128 || group == 256) &&
+         K % group == 0;
+}
+
+}  // namespace
+}  // namespace kbh
+
+extern "C" size_t kbh_qmoe_workspace_bytes(int T, int D, int N, int E) {
+  (void)D;
+  if (T <= 0 || E <= 0) return 0;
+  return kbh::moe_layout(T, E, 0, N).total;
+}
+
+extern "C" int kbh_moe_route_top2(const void* router_logits, int logits_dtype, int32_t* topi,
+                                  void* topw, void* workspace, size_t workspace_bytes, int T,
+                                  int E, int dtype, void* stream) {
+  using namespace kbh;
+  if (!router_logits || !topi || !topw || !workspace) return KBH_ERR_NULL;
+  if (logits_dtype < 0 || logits_dtype > 2 || (dtype != KBH_F16 && dtype != KBH_BF16)) return KBH_ERR_DTYPE;
+  if (T < 1 || E < 2 || E > kMoeMaxExperts) return KBH_ERR_SHAPE;
+  const MoeLayout L = moe_layout(T, E, 0, 0);
+  if (workspace_bytes < L.total) return KBH_ERR_WORKSPACE;
+  MoeBuffers mb = moe_buffers(workspace, L);
+  mb.topi = topi;
+  mb.topw = (uint16_t*)topw;
+  launch_route(router_logits, logits_dtype, T, E, dtype == KBH_BF16, mb, L, (hipStream_t)stream);
+  return launch_status();
+}
+
+extern "C" int kbh_qmoe(const void* x, const int8_t* qweight, const void* scales,
+                        const void* router_logits, int logits_dtype, void* y, void* workspace,
+                        size_t workspace_bytes, int T, int D, int N, int E, int group, int dtype,
+                        void* stream) {
+  using namespace kbh;
+  if (!x || !qweight || !scales || !router_logits || !y || !workspace) return KBH_ERR_NULL;
+  if (dtype != KBH_F16 && dtype != KBH_BF16) return KBH_ERR_DTYPE;
+  if (logits_dtype < 0 || logits_dtype > 2) return KBH_ERR_DTYPE;
+  if (!moe_shape_ok(T, E, D, N, group)) return KBH_ERR_SHAPE;
+  if (!aligned16(x) || !aligned16(qweight) || !aligned16(scales) || !aligned16(y)) return KBH_ERR_ALIGN;
+  const MoeLayout L = moe_layout(T, E, 0, N);
+  if (workspace_bytes < L.total) return KBH_ERR_WORKSPACE;
+  const MoeBuffers mb = moe_buffers(workspace, L);
+  hipStream_t st = (hipStream_t)stream;
+  void* o = (char*)workspace + L.o;
+  const bool bf = dtype == KBH_BF16;
+  launch_route(router_logits, logits_dtype, T, E, bf, mb, L, st);
+  const size_t ws_ = (size_t)D * N, ss_ = (size_t)(D / group) * N;
+  if (bf) {
+    const I8SlabPolicy<true> bp{qweight, (const uint16_t*)scales, N, group, ws_, ss_};
+    launch_moe_gemm<true, I8SlabPolicy<true>, true, false, true>(L, x, D, mb, bp, bp, o, N, N, D, st);
+    launch_combine<true>(o, mb.topw, y, T, N, st);
+  } else {
+    const I8SlabPolicy<false> bp{qweight, (const uint16_t*)scales, N, group, ws_, ss_};
+    launch_moe_gemm<false, I8SlabPolicy<false>, true, false, true>(L, x, D, mb, bp, bp, o, N, N, D, st);
+    launch_combine<false>(o, mb.topw, y, T, N, st);
+  }
+  return launch_status();
+}
+
+extern "C" size_t kbh_qmoe_ffn_workspace_bytes(int T, int D, int F, int E) {
+  if (T <= 0 || E <= 0) return 0;
+  return kbh::moe_layout(T, E, F, D).total;
+}
+
+extern "C" int kbh_qmoe_ffn(const void* x, const void* router_logits, int logits_dtype,
+                            const int32_t* gate_qweight, const void* gate_scales,
+                            const void* gate_zeros, const int32_t* up_qweight,
+                            const void* up_scales, const void* up_zeros,
+                            const int32_t* down_qweight, const void* down_scales,
+                            const void* down_zeros, void* y, void* workspace,
+                            size_t workspace_bytes, int T, int D, int F, int E, int group,
+                            int dtype, void* stream) {
+  using namespace kbh;
+  if (!x || !router_logits || !gate_qweight || !gate_scales || !gate_zeros || !up_qweight ||
+      !up_scales || !up_zeros || !down_qweight || !down_scales || !down_zeros || !y || !workspace)
+    return KBH_ERR_NULL;
+  if (dtype != KBH_F16 && dtype != KBH_BF16) return KBH_ERR_DTYPE;
+  if (logits_dtype < 0 || logits_dtype > 2) return KBH_ERR_DTYPE;
+  if (!moe_shape_ok(T, E, D, F, group) || !moe_shape_ok(T, E, F, D, group)) return KBH_ERR_SHAPE;
+  const void* ptrs[] = {x, gate_qweight, gate_scales, gate_zeros, up_qweight, up_scales, up_zeros,
+                        down_qweight, down_scales, down_zeros, y};
+  for (const void* p : ptrs)
+    if (!aligned16(p)) return KBH_ERR_ALIGN;
+  const MoeLayout L = moe_layout(T, E, F, D);
+  if (workspace_bytes < L.total) return KBH_ERR_WORKSPACE;
+  const MoeBuffers mb = moe_buffers(workspace, L);
+  hipStream_t st = (hipStream_t)stream;
+  void* h = (char*)workspace + L.h;
+  void* o = (char*)workspace + L.o;
+  const bool bf = dtype == KBH_BF16;
+  launch_route(router_logits, logits_dtype, T, E, bf, mb, L, st);
+  // gate/up: [D -> F] packed along F; down: [F -> D] packed along D
+  const size_t gq = (size_t)D * (F / 8), gs = (size_t)(D / group) * F;
+  const size_t dq = (size_t)F * (D / 8), ds = (size_t)(F / group) * D;
+#define KBH_FFN(BF)                                                                              \
+  {                                                                                              \
+    const W4SlabPolicy<BF> gp{(const uint32_t*)gate_qweight, (const uint16_t*)gate_scales,       \
+                              (const uint16_t*)gate_zeros, F, group, gq, gs};                    \
+    const W4SlabPolicy<BF> upp{(const uint32_t*)up_qweight, (const uint16_t*)up_scales,         \
+                               (const uint16_t*)up_zeros, F, group, gq, gs};                     \
+    const W4SlabPolicy<BF> dp{(const uint32_t*)down_qweight, (const uint16_t*)down_scales,       \
+                              (const uint16_t*)down_zeros, D, group, dq, ds};                    \
+    launch_moe_gemm<BF, W4SlabPolicy<BF>, true, true, false>(L, x, D, mb, gp, upp, h, F, F, D, st); \
+    launch_moe_gemm<BF, W4SlabPolicy<BF>, false, false, true>(L, h, F, mb, dp, dp, o, D, D, F, st); \
+    launch_combine<BF>(o, mb.topw, y, T, D, st);                                                  \
+  }
+  if (bf) KBH_FFN(true) else KBH_FFN(false)
+#undef KBH_FFN
+  return launch_status();
+}

@@ -110,3 +110,41 @@ def mxfp8(M: int, K: int = 14336, N: int = 4096, seed: int = 0):
     a, a_s = mx_quantize(a_src)
     b, b_s = mx_quantize(b_src)
     return [a, a_s, b, b_s]
+
+
+def _distinct_logits(T: int, E: int, g: torch.Generator, dtype: torch.dtype) -> torch.Tensor:
+    """N(0,1) router logits in `dtype` whose top-2 per row has no ties (re-drawn otherwise)."""
+    while True:
+        lg = torch.randn(T, E, generator=g).to(dtype)
+        top = lg.float().topk(3, dim=-1).values
+        if bool((top[:, 0] > top[:, 1]).all() and (top[:, 1] > top[:, 2]).all()):
+            return lg
+
+
+def qmoe(T: int = 256, D: int = 4096, E: int = 8, N: int = 14336,
+         dtype: torch.dtype = torch.float16, seed: int = 0):
+    """[x, qweight, scales, router_logits] with the distributions of the reference qMoE task
+    (reference.py:23-29): qweight int8 in [-8, 7], scales N(0,1)*0.01, logits in x.dtype."""
+    g = _gen(seed)
+    x = torch.randn(T, D, generator=g).to(dtype)
+    qweight = torch.randint(-8, 8, (E, D, N), generator=g, dtype=torch.int8)
+    scales = (torch.randn(E, D // 128, N, generator=g) * 0.01).to(dtype)
+    logits = _distinct_logits(T, E, g, dtype)
+    return [x, qweight, scales, logits]
+
+
+def qmoe_ffn(T: int = 512, D: int = 4096, F: int = 14336, E: int = 8, group: int = 128,
+             dtype: torch.dtype = torch.float16, seed: int = 0):
+    """[x, router_logits, gate_q, gate_s, gate_z, up_q, up_s, up_z, down_q, down_s, down_z] for
+    fp32 logits N(0,1) without top-2 ties, x N(0,1), W4A16 experts
+    with scales U[0.002, 0.02] and zero points U{0..15}."""
+    g = _gen(seed)
+    x = torch.randn(T, D, generator=g).to(dtype)
+    logits = _distinct_logits(T, E, g, torch.float32)
+
+    def w4(K, Nc):
+        q = torch.stack([random_packed_int4(K, Nc, g) for _ in range(E)])
+        s = (torch.rand(E, K // group, Nc, generator=g) * 0.018 + 0.002).to(dtype)
+        z = torch.randint(0, 16, (E, K // group, Nc), generator=g).to(dtype)
+        return [q, s, z]
+    return [x, logits] + w4(D, F) + w4(D, F) + w4(F, D)

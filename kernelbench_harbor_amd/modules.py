@@ -54,3 +54,28 @@ class MXFP8Model(nn.Module):
 
     def forward(self, a, a_scale, b, b_scale):
         return ops.mxfp8_gemm(a, a_scale, b, b_scale)
+
+
+class QMoEModel(nn.Module):
+    """Quantized top-2 MoE (one projection per expert).
+
+    Reference: tasks/fused_qmoe/*/environment/reference.py:11-21,
+    forward(x [T,D], qweight [E,D,N] int8, scales [E,D/128,N], router_logits [T,E]) -> [T,N].
+    """
+
+    def forward(self, x, qweight, scales, router_logits):
+        return ops.qmoe(x, qweight, scales, router_logits)
+
+
+class QMoEFFNModel(nn.Module):
+    """Top-2 MoE SiLU FFN with W4A16 g128 experts.
+
+    No reference module; written in the reference's Model idiom with its routing and combine:
+    forward(x, router_logits, gate_qweight, gate_scales, gate_zeros, up_qweight, up_scales,
+    up_zeros, down_qweight, down_scales, down_zeros) -> [T, D] x.dtype.
+    """
+
+    def forward(self, x, router_logits, gate_qweight, gate_scales, gate_zeros, up_qweight,
+                up_scales, up_zeros, down_qweight, down_scales, down_zeros):
+        return ops.qmoe_ffn(x, router_logits, gate_qweight, gate_scales, gate_zeros, up_qweight,
+                            up_scales, up_zeros, down_qweight, down_scales, down_zeros)

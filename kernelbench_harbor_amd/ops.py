@@ -217,3 +217,102 @@ def mxfp8_gemm(a: torch.Tensor, a_scale: torch.Tensor, b: torch.Tensor, b_scale:
                             _stream_ptr(dev))
     _lib.check(st, "kbh_mxfp8_gemm")
     return y
+
+
+_LOGIT_CODE = {torch.float16: 0, torch.bfloat16: 1, torch.float32: 2}
+
+
+def _check_logits(router_logits, T):
+    _require(router_logits.dtype in _LOGIT_CODE,
+             f"router_logits must be float16, bfloat16 or float32, got {router_logits.dtype}")
+    _require(router_logits.dim() == 2 and router_logits.shape[0] == T,
+             f"router_logits must be [{T}, E], got {tuple(router_logits.shape)}")
+    E = router_logits.shape[1]
+    _require(2 <= E <= 256, f"number of experts must be in [2, 256], got {E}")
+    return E
+
+
+def moe_route_top2(router_logits: torch.Tensor, dtype: torch.dtype = torch.float16):
+    """(topi [T, 2] int32, topw [T, 2] dtype): softmax(fp32 logits), top-2, renormalised
+    (tasks/fused_qmoe/*/environment/reference.py:14-16)."""
+    _require(dtype in _DT_CODE, f"dtype must be float16 or bfloat16, got {dtype}")
+    T = router_logits.shape[0]
+    E = _check_logits(router_logits, T)
+    dev = _check_device(router_logits)
+    topi = torch.empty((T, 2), dtype=torch.int32, device=dev)
+    topw = torch.empty((T, 2), dtype=dtype, device=dev)
+    lib = _lib.load()
+    ws = workspaces.get(lib.kbh_qmoe_workspace_bytes(T, 0, 0, E), dev)
+    st = lib.kbh_moe_route_top2(router_logits.contiguous().data_ptr(), _LOGIT_CODE[router_logits.dtype],
+                                topi.data_ptr(), topw.data_ptr(), ws.data_ptr(), ws.numel(), T, E,
+                                _DT_CODE[dtype], _stream_ptr(dev))
+    _lib.check(st, "kbh_moe_route_top2")
+    return topi, topw
+
+
+def qmoe(x: torch.Tensor, qweight: torch.Tensor, scales: torch.Tensor,
+         router_logits: torch.Tensor) -> torch.Tensor:
+    """Top-2 quantized MoE of tasks/fused_qmoe/fused_qmoe__mixtral__fp16/environment/
+    reference.py:11-21: x [T, D], qweight [E, D, N] int8 (int4 values), scales [E, D/G, N] in
+    x.dtype, router_logits [T, E]; G = D / scales.shape[1]."""
+    _require(x.dtype in _DT_CODE, f"x must be float16 or bfloat16, got {x.dtype}")
+    _require(x.dim() == 2, "x must be [T, D]")
+    T, D = x.shape
+    _require(qweight.dtype == torch.int8 and qweight.dim() == 3 and qweight.shape[1] == D,
+             f"qweight must be int8 [E, {D}, N], got {qweight.dtype} {tuple(qweight.shape)}")
+    E, _, N = qweight.shape
+    _require(scales.dtype == x.dtype and scales.dim() == 3 and scales.shape[0] == E and
+             scales.shape[2] == N and D % scales.shape[1] == 0,
+             f"scales must be x.dtype [E, D/G, N], got {scales.dtype} {tuple(scales.shape)}")
+    group = D // scales.shape[1]
+    _require(_check_logits(router_logits, T) == E, "router_logits must have E columns")
+    dev = _check_device(x, qweight, scales, router_logits)
+    y = torch.empty((T, N), dtype=x.dtype, device=dev)
+    lib = _lib.load()
+    ws = workspaces.get(lib.kbh_qmoe_workspace_bytes(T, D, N, E), dev)
+    st = lib.kbh_qmoe(x.contiguous().data_ptr(), qweight.contiguous().data_ptr(),
+                      scales.contiguous().data_ptr(), router_logits.contiguous().data_ptr(),
+                      _LOGIT_CODE[router_logits.dtype], y.data_ptr(), ws.data_ptr(), ws.numel(),
+                      T, D, N, E, group, _DT_CODE[x.dtype], _stream_ptr(dev))
+    _lib.check(st, "kbh_qmoe")
+    return y
+
+
+def qmoe_ffn(x, router_logits, gate_qweight, gate_scales, gate_zeros, up_qweight, up_scales,
+             up_zeros, down_qweight, down_scales, down_zeros) -> torch.Tensor:
+    """Top-2 MoE SiLU FFN with W4A16 experts: y[t] = sum_k w_k * down_e(silu(gate_e x) * up_e x).
+
+    gate/up qweight [E, D, F/8] int32 (packed along F), scales/zeros [E, D/G, F]; down
+    qweight [E, F, D/8], scales/zeros [E, F/G, D]; all scales/zeros in x.dtype."""
+    _require(x.dtype in _DT_CODE and x.dim() == 2, "x must be a float16/bfloat16 [T, D] tensor")
+    T, D = x.shape
+    E = _check_logits(router_logits, T)
+    _require(gate_qweight.dtype == torch.int32 and gate_qweight.dim() == 3 and
+             gate_qweight.shape[:2] == (E, D), f"gate_qweight must be int32 [E, D, F/8]")
+    F = gate_qweight.shape[2] * 8
+    _require(up_qweight.shape == gate_qweight.shape and up_qweight.dtype == torch.int32,
+             "up_qweight must match gate_qweight")
+    _require(down_qweight.dtype == torch.int32 and tuple(down_qweight.shape) == (E, F, D // 8),
+             f"down_qweight must be int32 [E, {F}, {D // 8}]")
+    group = D // gate_scales.shape[1]
+    for name, t_, shape in [("gate_scales", gate_scales, (E, D // group, F)),
+                            ("gate_zeros", gate_zeros, (E, D // group, F)),
+                            ("up_scales", up_scales, (E, D // group, F)),
+                            ("up_zeros", up_zeros, (E, D // group, F)),
+                            ("down_scales", down_scales, (E, F // group, D)),
+                            ("down_zeros", down_zeros, (E, F // group, D))]:
+        _require(t_.dtype == x.dtype and tuple(t_.shape) == shape,
+                 f"{name} must be x.dtype {shape}, got {t_.dtype} {tuple(t_.shape)}")
+    ts = [x, gate_qweight, gate_scales, gate_zeros, up_qweight, up_scales, up_zeros,
+          down_qweight, down_scales, down_zeros]
+    dev = _check_device(router_logits, *ts)
+    y = torch.empty((T, D), dtype=x.dtype, device=dev)
+    lib = _lib.load()
+    ws = workspaces.get(lib.kbh_qmoe_ffn_workspace_bytes(T, D, F, E), dev)
+    ts = [t_.contiguous() for t_ in ts]
+    st = lib.kbh_qmoe_ffn(ts[0].data_ptr(), router_logits.contiguous().data_ptr(),
+                          _LOGIT_CODE[router_logits.dtype], *[t_.data_ptr() for t_ in ts[1:]],
+                          y.data_ptr(), ws.data_ptr(), ws.numel(), T, D, F, E, group,
+                          _DT_CODE[x.dtype], _stream_ptr(dev))
+    _lib.check(st, "kbh_qmoe_ffn")
+    return y
