@@ -1,15 +1,22 @@
 #!/usr/bin/env python3
-"""Benchmark of the W4A16 g128 GEMM sweep on one MI355X.
+"""Benchmark of the quantized-GEMM operator path on one MI355X.
 
-One step = one W4A16 call at every M in {1, 4, 16, 64, 256, 1024, 2048} with K=14336,
-N=4096, group 128, fp16 (the Llama-3-8B down_proj shape). Inputs are synthetic (seeded, the
-BASELINE value distributions) and resident in HBM before timing starts. Each M rotates over
-enough copies of its inputs (> 2x the 256 MB Infinity Cache) that every call streams its
-weights from HBM.
+Headline (BASELINE metric, configs[1]): the W4A16 g128 GEMM sweep. One step = one W4A16 call
+at every M in {1, 4, 16, 64, 256, 1024, 2048} with K=14336, N=4096, fp16. `value` = total
+FLOPs of a step / wall time of a step (TFLOP/s).
 
-Prints ONE JSON line: `value` = total FLOPs of a step / wall time of a step (TFLOP/s), plus the
-per-M sweep (HIP-event kernel time, TFLOP/s, GB/s, roofline fraction), the roofline of the
-dominant launch and the CPU baseline (the numpy oracle on the host cores, bounded sample).
+Also measured (reported under "configs", not part of `value`): W8A8 at M in {16, 512}, MXFP8 at
+M in {128, 2048}, the top-2 W4A16 MoE SiLU FFN (T=512, Mixtral layer), the reference qMoE op
+(T=256) and the reference FP8 weight-only op (M=16).
+
+Inputs are synthetic (seeded, BASELINE distributions) and resident in HBM before timing. Each
+configuration rotates over enough input copies (> 2x the 256 MB Infinity Cache) that every call
+streams its weights from HBM. Per configuration two timings are reported: the median of
+event-bracketed single calls (the reference grader's protocol, which includes ~4-5 us of event
+overhead per call) and the mean of a batch of back-to-back calls between two events
+(`us_batched`, close to the kernel duration); roofline fractions use the batched time.
+
+Prints ONE JSON line. The CPU baseline times the numpy oracle on the host cores.
 """
 from __future__ import annotations
 
@@ -25,24 +32,108 @@ sys.path.insert(0, REPO)
 
 K_DIM, N_DIM, GROUP = 14336, 4096, 128
 SWEEP_M = [1, 4, 16, 64, 256, 1024, 2048]
-HBM_PEAK = 8.0e12          # bytes/s, MI355X datasheet
-F16_PEAK = 2.5e15          # dense fp16 MFMA flop/s, MI355X datasheet
-ROTATE_BYTES = 640 << 20   # > 2 x 256 MB Infinity Cache
+HBM_PEAK = 8.0e12           # bytes/s, MI355X datasheet
+PEAK = {"f16": 2.5e15, "i8": 5.0e15, "f8": 5.0e15}   # dense MFMA, datasheet
+ROTATE_BYTES = 640 << 20    # > 2 x 256 MB Infinity Cache
 METRIC = "W4A16 GEMM TFLOP/s + HBM GB/s (% roofline), M=1..2048, K=14336 N=4096"
 
 
+# ---- algorithmic work ------------------------------------------------------------------------
 def w4a16_bytes(M, K=K_DIM, N=N_DIM, G=GROUP):
-    """Algorithmic HBM bytes of one call: packed weights + fp16 scales and zeros + x + y."""
+    """Packed weights + fp16 scales and zeros + x + y."""
     return K * N // 2 + 2 * (K // G) * N * 2 + 2 * M * K + 2 * M * N
 
 
-def w4a16_flops(M, K=K_DIM, N=N_DIM):
+# HBM bytes per launch of the W4A16 kernels at the sweep's two regimes, from rocprofv3 PMC runs:
+# FETCH_SIZE scaled by 2.0 (a plain 256 MiB device copy reads as 131084.5 KiB) plus WRITE_SIZE
+# (exact on the same copy). Keyed by M; other M report null.
+W4A16_PMC_TRAFFIC = {16: 39_890_343, 2048: 325_538_042}
+
+
+def gemm_flops(M, N=N_DIM, K=K_DIM):
     return 2 * M * N * K
 
 
+def w8a8_bytes(M, K=K_DIM, N=N_DIM):
+    return K * N + M * K + 2 * M + 2 * N + 2 * M * N
+
+
+def mxfp8_bytes(M, K=K_DIM, N=N_DIM):
+    return M * K + N * K + (M + N) * K // 32 + 2 * M * N
+
+
+def fp8w_bytes(M, K=K_DIM, N=N_DIM, B=128):
+    return K * N + 2 * (K // B) * N + 2 * M * K + 2 * M * N
+
+
+def ffn_bytes(T=512, D=4096, F=14336, E=8, G=GROUP):
+    per_expert = 3 * D * F // 2 + 3 * 2 * (D * F // G) * 2
+    return E * per_expert + 2 * T * D * 2 + 4 * T * E
+
+
+def ffn_flops(T=512, D=4096, F=14336):
+    return 2 * T * 6 * D * F
+
+
+def qmoe_bytes(T=256, D=4096, N=14336, E=8, G=GROUP):
+    return E * D * N + E * (D // G) * N * 2 + 2 * T * D + 2 * T * N + 2 * T * E
+
+
+def qmoe_flops(T=256, D=4096, N=14336):
+    return 2 * T * 2 * D * N
+
+
+def roofline(seconds, by, fl, peak):
+    t_mem, t_cmp = by / HBM_PEAK, fl / peak
+    bound = "hbm" if t_mem >= t_cmp else "mfma"
+    return bound, max(t_mem, t_cmp) / seconds
+
+
+# ---- timing helpers --------------------------------------------------------------------------
+def rotation(make, per_set_bytes, limit=32):
+    """Clones of one input set, enough to exceed ROTATE_BYTES."""
+    base = make()
+    R = max(2, min(limit, math.ceil(ROTATE_BYTES / per_set_bytes)))
+    return [base] + [[t.clone() for t in base] for _ in range(R - 1)]
+
+
+def time_config(torch, fn, sets, iters, batch):
+    """(per-call event times [s], batched mean [s]) over rotating input sets."""
+    for i in range(3):
+        fn(*sets[i % len(sets)])
+    torch.cuda.synchronize()
+    ts = []
+    for i in range(iters):
+        a = torch.cuda.Event(enable_timing=True)
+        b = torch.cuda.Event(enable_timing=True)
+        a.record()
+        fn(*sets[i % len(sets)])
+        b.record()
+        b.synchronize()
+        ts.append(a.elapsed_time(b) * 1e-3)
+    a = torch.cuda.Event(enable_timing=True)
+    b = torch.cuda.Event(enable_timing=True)
+    a.record()
+    for i in range(batch):
+        fn(*sets[i % len(sets)])
+    b.record()
+    b.synchronize()
+    return sorted(ts), a.elapsed_time(b) * 1e-3 / batch
+
+
+def record(name, ts, batched, by, fl, peak, **extra):
+    med = ts[len(ts) // 2]
+    bound, frac = roofline(batched, by, fl, peak)
+    out = {"name": name, **extra, "us_median": round(med * 1e6, 2),
+           "us_batched": round(batched * 1e6, 2), "tflops": round(fl / batched / 1e12, 2),
+           "gbps": round(by / batched / 1e9, 1), "bound": bound, "roofline_frac": round(frac, 4),
+           "bytes": by, "flops": fl}
+    return out
+
+
+# ---- CPU baseline ----------------------------------------------------------------------------
 def cpu_baseline(sample_m, seed=0):
     """Times the numpy oracle (oracle/w4a16.py, fp32 ground-truth path) on the host cores."""
-    import numpy as np
     import torch
 
     from kernelbench_harbor_amd import inputs
@@ -59,10 +150,9 @@ def cpu_baseline(sample_m, seed=0):
         t0 = time.perf_counter()
         ow.forward(xn, qn, sn, zn)
         dt = time.perf_counter() - t0
-        total_flops += w4a16_flops(M)
+        total_flops += gemm_flops(M)
         total_s += dt
         per.append({"M": M, "s": round(dt, 4)})
-    del np
     return {"value": total_flops / total_s / 1e12, "unit": "TFLOP/s", "cores": threads,
             "kind": "port",
             "sample": ("one call of the numpy oracle forward (unpack, fp32 dequant, fp32 BLAS "
@@ -71,6 +161,7 @@ def cpu_baseline(sample_m, seed=0):
             "per_m": per}
 
 
+# ---- main ------------------------------------------------------------------------------------
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -78,6 +169,10 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--m", type=str, default=",".join(map(str, SWEEP_M)))
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-configs", action="store_true", help="only the W4A16 sweep")
+    ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
+                    help="only run 5 device copies of MIB MiB (calibrates rocprofv3 FETCH_SIZE/"
+                         "WRITE_SIZE against a kernel of known traffic) and exit")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (got --gpus {args.gpus}); this build has no "
@@ -93,26 +188,32 @@ def main():
         kbuild.build()
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
+    if args.copy_probe:
+        n = args.copy_probe << 20
+        src = torch.ones(n, dtype=torch.uint8, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_probe_bytes": n, "copies": 5}))
+        return
     ms = [int(v) for v in args.m.split(",") if v]
 
-    # Inputs: one seeded set per M, cloned into enough device copies to defeat the MALL.
-    sets, outs = {}, {}
+    # ---- headline: W4A16 sweep ----
+    sets = {}
     for M in ms:
-        x, qw, s, z = [t.to(dev) for t in inputs.w4a16(M, K_DIM, N_DIM, GROUP, torch.float16, seed=0)]
-        per_set = w4a16_bytes(M)
-        R = max(2, min(32, math.ceil(ROTATE_BYTES / per_set)))
-        sets[M] = [(x.clone(), qw.clone(), s.clone(), z.clone()) for _ in range(R)]
-        del x, qw, s, z
+        sets[M] = rotation(lambda: [t.to(dev) for t in inputs.w4a16(M, K_DIM, N_DIM, GROUP,
+                                                                     torch.float16, seed=0)],
+                           w4a16_bytes(M))
     torch.cuda.synchronize()
-
     calls = {M: 0 for M in ms}
     ev = {M: [] for M in ms}
 
-    def step(record):
+    def step(rec):
         for M in ms:
             i = calls[M] % len(sets[M])
             calls[M] += 1
-            if record:
+            if rec:
                 a = torch.cuda.Event(enable_timing=True)
                 b = torch.cuda.Event(enable_timing=True)
                 a.record()
@@ -131,44 +232,74 @@ def main():
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
 
-    sweep = []
-    step_flops = 0
-    kernel_s = {}
+    sweep, step_flops, mean_s = [], 0, {}
     for M in ms:
-        ts = sorted(a.elapsed_time(b) for a, b in ev[M])
-        med = ts[len(ts) // 2] * 1e-3
-        mean = sum(ts) / len(ts) * 1e-3
-        kernel_s[M] = mean
-        by, fl = w4a16_bytes(M), w4a16_flops(M)
-        t_floor = max(by / HBM_PEAK, fl / F16_PEAK)
-        sweep.append({
-            "M": M, "us_median": round(med * 1e6, 2), "us_mean": round(mean * 1e6, 2),
-            "tflops": round(fl / med / 1e12, 2), "gbps": round(by / med / 1e9, 1),
-            "bound": "hbm" if by / HBM_PEAK >= fl / F16_PEAK else "mfma",
-            "roofline_frac": round(t_floor / med, 4), "bytes": by, "flops": fl})
-        step_flops += fl
+        ts = sorted(a.elapsed_time(b) * 1e-3 for a, b in ev[M])
+        mean_s[M] = sum(ts) / len(ts)
+        _, batched = time_config(torch, ops.w4a16_gemm, sets[M], 3, 20)
+        sweep.append(record(f"w4a16 M={M}", ts, batched, w4a16_bytes(M), gemm_flops(M),
+                            PEAK["f16"], M=M, us_mean=round(mean_s[M] * 1e6, 2)))
+        step_flops += gemm_flops(M)
+    del sets
+    torch.cuda.empty_cache()
 
-    # Dominant launch: the M whose calls take the most time per step.
-    Md = max(ms, key=lambda m: kernel_s[m])
+    # Dominant launch of a step: the M whose calls take the most time.
+    Md = max(ms, key=lambda m: mean_s[m])
     d = next(r for r in sweep if r["M"] == Md)
     if d["bound"] == "hbm":
-        achieved = d["bytes"] / kernel_s[Md] / 1e9
-        roof = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK / 1e9,
-                "unit": "GB/s", "frac": round(achieved / (HBM_PEAK / 1e9), 4)}
+        ach = d["bytes"] / mean_s[Md] / 1e9
+        roof = {"bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK / 1e9, "unit": "GB/s",
+                "frac": round(ach / (HBM_PEAK / 1e9), 4)}
     else:
-        achieved = d["flops"] / kernel_s[Md] / 1e12
-        roof = {"bound": "mfma", "achieved": round(achieved, 1), "peak": F16_PEAK / 1e12,
-                "unit": "TFLOP/s", "frac": round(achieved / (F16_PEAK / 1e12), 4)}
-    roof.update({"traffic": None, "launch": f"kbh_w4a16_gemm M={Md} K=14336 N=4096 g128",
-                 "avg_launch_us": round(kernel_s[Md] * 1e6, 2)})
+        ach = d["flops"] / mean_s[Md] / 1e12
+        roof = {"bound": "mfma", "achieved": round(ach, 1), "peak": PEAK["f16"] / 1e12,
+                "unit": "TFLOP/s", "frac": round(ach / (PEAK["f16"] / 1e12), 4)}
+    roof.update({"traffic": W4A16_PMC_TRAFFIC.get(Md), "launch": f"kbh_w4a16_gemm M={Md} K=14336 N=4096 g128",
+                 "avg_launch_us": round(mean_s[Md] * 1e6, 2),
+                 "timing": "mean of the HIP-event-bracketed launches of the timed steps"})
 
-    ms_per_step = wall / args.steps * 1e3
+    # ---- the other BASELINE configurations ----
+    configs = []
+    if not args.no_configs:
+        it, bt = 20, 20
+        for M in (16, 512):
+            s_ = rotation(lambda: [t.to(dev) for t in inputs.w8a8(M, K_DIM, N_DIM, seed=0)],
+                          w8a8_bytes(M))
+            ts, bm = time_config(torch, ops.w8a8_gemm, s_, it, bt)
+            configs.append(record(f"w8a8 M={M}", ts, bm, w8a8_bytes(M), gemm_flops(M), PEAK["i8"], M=M))
+            del s_
+        for M in (128, 2048):
+            s_ = rotation(lambda: [t.to(dev) for t in inputs.mxfp8(M, K_DIM, N_DIM, seed=0)],
+                          mxfp8_bytes(M))
+            ts, bm = time_config(torch, ops.mxfp8_gemm, s_, it, bt)
+            configs.append(record(f"mxfp8 M={M}", ts, bm, mxfp8_bytes(M), gemm_flops(M), PEAK["f8"], M=M))
+            del s_
+        s_ = rotation(lambda: [t.to(dev) for t in inputs.fp8w(16, K_DIM, N_DIM, 128, torch.float16, 0)],
+                      fp8w_bytes(16))
+        ts, bm = time_config(torch, ops.fp8w_gemm, s_, it, bt)
+        configs.append(record("fp8w (reference op) M=16 b128", ts, bm, fp8w_bytes(16), gemm_flops(16),
+                              PEAK["f16"], M=16))
+        del s_
+        torch.cuda.empty_cache()
+        s_ = [[t.to(dev) for t in inputs.qmoe_ffn(seed=0)]]   # 757 MB of weights: no rotation
+        ts, bm = time_config(torch, ops.qmoe_ffn, s_, 10, 10)
+        configs.append(record("qmoe_ffn T=512 D=4096 F=14336 E=8 top2", ts, bm, ffn_bytes(),
+                              ffn_flops(), PEAK["f16"], T=512))
+        del s_
+        torch.cuda.empty_cache()
+        s_ = [[t.to(dev) for t in inputs.qmoe(seed=0)]]       # 470 MB of weights
+        ts, bm = time_config(torch, ops.qmoe, s_, 10, 10)
+        configs.append(record("qmoe (reference op) T=256 D=4096 N=14336 E=8", ts, bm,
+                              qmoe_bytes(), qmoe_flops(), PEAK["f16"], T=256))
+        del s_
+        torch.cuda.empty_cache()
+
     out = {
         "metric": METRIC,
         "value": round(step_flops / (wall / args.steps) / 1e12, 3),
         "unit": "TFLOP/s",
         "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
-        "ms_per_step": round(ms_per_step, 4),
+        "ms_per_step": round(wall / args.steps * 1e3, 4),
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
         "dtype": "f16",
         "data": "synthetic (seeded; BASELINE distributions; weights rotated to stay HBM-cold)",
@@ -178,6 +309,7 @@ def main():
                    "parallelism": "none (1 GPU)"},
         "sweep": sweep,
         "roofline": roof,
+        "configs": configs,
     }
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline([m for m in ms if m <= 256] or ms[:1])

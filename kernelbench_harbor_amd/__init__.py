@@ -4,7 +4,8 @@ The compute lives in hand-written HIP kernels compiled into ``lib/libkbh_qgemm.s
 ``include/kbh_qgemm.h``); this package holds the ctypes binding, host-side validation and the
 drop-in ``nn.Module`` classes.
 """
+from ._lib import KbhError  # noqa: F401
 from .modules import (FP8WModel, MXFP8Model, QMoEFFNModel, QMoEModel,  # noqa: F401
                       W4A16Model, W8A8Model)
 
-__all__ = ["W4A16Model", "W8A8Model", "FP8WModel", "MXFP8Model", "QMoEModel", "QMoEFFNModel"]
+__all__ = ["KbhError", "W4A16Model", "W8A8Model", "FP8WModel", "MXFP8Model", "QMoEModel", "QMoEFFNModel"]

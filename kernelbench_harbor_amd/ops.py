@@ -124,6 +124,8 @@ def w8a8_gemm(x_int8: torch.Tensor, w_int8: torch.Tensor, x_scale: torch.Tensor,
     x2, w = x2.contiguous(), w_int8.contiguous()
     lead = x_int8.shape[:-1]
     y = torch.empty((M, N), dtype=torch.float16, device=dev)
+    if M == 0:
+        return y.reshape(*lead, N)
     xs = x_scale.reshape(M).contiguous()
     ws_ = w_scale.reshape(N).contiguous()
     lib = _lib.load()
@@ -141,6 +143,8 @@ def w8a8_gemm_i32(x_int8: torch.Tensor, w_int8: torch.Tensor) -> torch.Tensor:
     dev = _check_device(x_int8, w_int8)
     x2, w = x2.contiguous(), w_int8.contiguous()
     acc = torch.empty((M, N), dtype=torch.int32, device=dev)
+    if M == 0:
+        return acc
     lib = _lib.load()
     ws = workspaces.get(lib.kbh_w8a8_workspace_bytes(M, N, K), dev)
     st = lib.kbh_w8a8_gemm_i32(x2.data_ptr(), w.data_ptr(), acc.data_ptr(), ws.data_ptr(),
@@ -209,6 +213,8 @@ def mxfp8_gemm(a: torch.Tensor, a_scale: torch.Tensor, b: torch.Tensor, b_scale:
              f"scales must be [M, K/32] and [N, K/32]")
     dev = _check_device(a, a_scale, b, b_scale)
     y = torch.empty((M, N), dtype=out_dtype, device=dev)
+    if M == 0:
+        return y
     lib = _lib.load()
     ws = workspaces.get(lib.kbh_mxfp8_workspace_bytes(M, N, K), dev)
     a8, b8, as8, bs8 = _as_bytes(a), _as_bytes(b), _as_bytes(a_scale), _as_bytes(b_scale)
@@ -241,6 +247,8 @@ def moe_route_top2(router_logits: torch.Tensor, dtype: torch.dtype = torch.float
     dev = _check_device(router_logits)
     topi = torch.empty((T, 2), dtype=torch.int32, device=dev)
     topw = torch.empty((T, 2), dtype=dtype, device=dev)
+    if T == 0:
+        return topi, topw
     lib = _lib.load()
     ws = workspaces.get(lib.kbh_qmoe_workspace_bytes(T, 0, 0, E), dev)
     st = lib.kbh_moe_route_top2(router_logits.contiguous().data_ptr(), _LOGIT_CODE[router_logits.dtype],
@@ -268,6 +276,8 @@ def qmoe(x: torch.Tensor, qweight: torch.Tensor, scales: torch.Tensor,
     _require(_check_logits(router_logits, T) == E, "router_logits must have E columns")
     dev = _check_device(x, qweight, scales, router_logits)
     y = torch.empty((T, N), dtype=x.dtype, device=dev)
+    if T == 0:
+        return y
     lib = _lib.load()
     ws = workspaces.get(lib.kbh_qmoe_workspace_bytes(T, D, N, E), dev)
     st = lib.kbh_qmoe(x.contiguous().data_ptr(), qweight.contiguous().data_ptr(),
@@ -307,6 +317,8 @@ def qmoe_ffn(x, router_logits, gate_qweight, gate_scales, gate_zeros, up_qweight
           down_qweight, down_scales, down_zeros]
     dev = _check_device(router_logits, *ts)
     y = torch.empty((T, D), dtype=x.dtype, device=dev)
+    if T == 0:
+        return y
     lib = _lib.load()
     ws = workspaces.get(lib.kbh_qmoe_ffn_workspace_bytes(T, D, F, E), dev)
     ts = [t_.contiguous() for t_ in ts]

@@ -6,7 +6,9 @@ reference file:line it follows). It is the checker: only ``tests/``,
 ``__graft_entry__.smoke()`` and the ``cpu_baseline`` leg of ``bench.py`` may import it. The
 product path (``kernelbench_harbor_amd``) never imports, calls or falls back to it.
 
-Pinning (what keeps each function honest, beyond re-typing the formula):
+Pinning (what keeps each function honest, beyond re-typing the formula). Every op also has
+committed golden vectors under tests/golden/ (torch's CPU library routines running the reference
+modules' op sequences on small seeded inputs; the reference itself ships none):
   numerics      fp16 / bf16 rounding checked against torch's CPU casts (library routines);
                 e4m3fn decode table exhaustively against torch.float8_e4m3fn; e4m3fn RNE
                 encoder exhaustively on all fp16 inputs against torch; e8m0 closed form KATs.

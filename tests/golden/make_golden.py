@@ -1,0 +1,117 @@
+"""Writes the golden vectors under tests/golden/ (run: python tests/golden/make_golden.py).
+
+The reference repository holds no test vectors, so these are produced here by torch's CPU
+library routines executing each reference module's op sequence on small seeded inputs. They
+freeze those library semantics (int32 shift/mask, fp16/bf16 RNE, the e4m3fn cast, softmax/topk)
+as data, so the numpy oracle is checked against an independent implementation that does not
+move with the installed torch. The sequences follow:
+  W4A16   tasks/quant_w4a16_pa/<task>/environment/reference.py:11-17 (packing :21-25)
+  W8A8    tasks/w8a8_smoothquant/<task>/environment/reference.py:7-9 (int64 accumulate instead
+          of the reference's fp32 matmul, which is inexact above 2^24)
+  FP8     tasks/fp8_microscale/<task>/environment/reference.py:9-12
+  MXFP8   generate_tasks.py:337-342 (amax/448, e4m3fn cast) with a power-of-two block scale
+  qMoE    tasks/fused_qmoe/<task>/environment/reference.py:14-21
+"""
+from __future__ import annotations
+
+import json
+import os
+
+import numpy as np
+import torch
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+
+
+def _np(t):
+    return t.detach().cpu().numpy()
+
+
+def w4a16(g):
+    M, K, N, G = 3, 256, 16, 128
+    x = torch.randn(M, K, generator=g).half()
+    nib = torch.randint(0, 16, (K, N), generator=g, dtype=torch.int64)
+    packed = torch.zeros(K, N // 8, dtype=torch.int64)
+    for i in range(8):
+        packed |= nib[:, i::8] << (4 * i)
+    qweight = packed.to(torch.int32)  # keeps the low 32 bits (two's complement)
+    scales = (torch.rand(K // G, N, generator=g) * 0.018 + 0.002).half()
+    zeros = torch.randint(0, 16, (K // G, N), generator=g).half()
+    shifts = torch.arange(0, 32, 4, dtype=torch.int32)
+    w = ((qweight.unsqueeze(-1) >> shifts) & 0xF).reshape(K, N)
+    se = scales.repeat_interleave(G, dim=0)
+    ze = zeros.repeat_interleave(G, dim=0)
+    W16 = (w.half() - ze) * se
+    Wgt = (w.float() - ze.float()) * se.float()
+    y_gt = x.float() @ Wgt
+    return dict(x=_np(x), qweight=_np(qweight), scales=_np(scales), zeros=_np(zeros),
+                nib=_np(nib).astype(np.uint8), W_f16=_np(W16), y_gt=_np(y_gt))
+
+
+def w8a8(g):
+    M, K, N = 4, 512, 16
+    x = torch.randint(-127, 128, (M, K), generator=g, dtype=torch.int8)
+    w = torch.randint(-127, 128, (K, N), generator=g, dtype=torch.int8)
+    x[0, :] = 127
+    w[:, 0] = 127
+    x[1, :] = -128
+    xs = (torch.rand(M, 1, generator=g) * 0.01 + 0.001).half()
+    ws = (torch.rand(1, N, generator=g) * 0.01 + 0.001).half()
+    acc = x.long() @ w.long()
+    out = (acc.float() * xs.float() * ws.float()).half()
+    return dict(x_int8=_np(x), w_int8=_np(w), x_scale=_np(xs), w_scale=_np(ws),
+                acc=_np(acc), out=_np(out))
+
+
+def fp8w(g):
+    M, K, N, B = 2, 256, 16, 128
+    x = torch.randn(M, K, generator=g).half()
+    w = (torch.randn(K, N, generator=g) * 0.3).to(torch.float8_e4m3fn)
+    s = (torch.rand(K // B, N, generator=g) * 0.05 + 0.05).half()
+    W = (w.float() * s.float().repeat_interleave(B, dim=0)).half()
+    y_gt = x.float() @ (w.float() * s.float().repeat_interleave(B, dim=0))
+    return dict(x=_np(x), w_codes=_np(w.view(torch.uint8)), scales=_np(s), W_f16=_np(W),
+                y_gt=_np(y_gt))
+
+
+def mxfp8(g):
+    R, K = 6, 128
+    src = torch.randn(R, K, generator=g) * torch.logspace(-3, 3, R).unsqueeze(1)
+    src[5, 32:64] = 0.0  # an all-zero block: code 0
+    blk = src.reshape(R, K // 32, 32)
+    amax = blk.abs().amax(-1)
+    e = torch.where(amax > 0, torch.ceil(torch.log2(amax / 448.0)), torch.full_like(amax, -127.0))
+    code = (e + 127).clamp(0, 254).to(torch.uint8)
+    scale = torch.exp2(code.float() - 127)
+    q = (blk / scale.unsqueeze(-1)).to(torch.float8_e4m3fn).reshape(R, K)
+    deq = (q.float().reshape(R, K // 32, 32) * scale.unsqueeze(-1)).reshape(R, K)
+    return dict(src=_np(src), codes=_np(q.view(torch.uint8)), scales=_np(code), deq=_np(deq))
+
+
+def qmoe_route(g):
+    T, E = 9, 8
+    logits = torch.randn(T, E, generator=g)
+    p = torch.softmax(logits.float(), dim=-1)
+    topv, topi = torch.topk(p, 2, dim=-1)
+    w = (topv / topv.sum(-1, keepdim=True)).half()
+    return dict(logits=_np(logits), topi=_np(topi), topw=_np(w))
+
+
+def e4m3fn_table():
+    v = torch.arange(256, dtype=torch.uint8).view(torch.float8_e4m3fn).float()
+    return ["nan" if np.isnan(a) else float(a).hex() for a in v.tolist()]
+
+
+def main():
+    g = torch.Generator().manual_seed(20240611)
+    for name, fn in (("w4a16", w4a16), ("w8a8", w8a8), ("fp8w", fp8w), ("mxfp8", mxfp8),
+                     ("qmoe_route", qmoe_route)):
+        np.savez(os.path.join(HERE, f"{name}.npz"), **fn(g))
+    with open(os.path.join(HERE, "e4m3fn_table.json"), "w") as f:
+        json.dump({"source": "torch.float8_e4m3fn -> float32, codes 0..255",
+                   "values": e4m3fn_table()}, f, indent=0)
+        f.write("\n")
+
+
+if __name__ == "__main__":
+    main()
