@@ -60,11 +60,15 @@ int kbh_last_hip_error(void);
  * workspace: >= kbh_w4a16_workspace_bytes(M, N, K, group) bytes, zero-filled before its first
  * use; every call leaves it zero-filled again. Calls that share a workspace must be ordered
  * (same stream); concurrent calls on one workspace race.
+ * scratch: >= kbh_w4a16_scratch_bytes(M, N, K, group) bytes (may be 0, then NULL is accepted)
+ * of device memory with no content requirement (split-K partial sums of the large-M kernel);
+ * it must not overlap the workspace, and calls that share it must be ordered like workspace.
  */
 size_t kbh_w4a16_workspace_bytes(int M, int N, int K, int group);
+size_t kbh_w4a16_scratch_bytes(int M, int N, int K, int group);
 int kbh_w4a16_gemm(const void* x, const int32_t* qweight, const void* scales, const void* zeros,
-                   void* y, void* workspace, size_t workspace_bytes,
-                   int M, int N, int K, int group, int dtype, void* stream);
+                   void* y, void* workspace, size_t workspace_bytes, void* scratch,
+                   size_t scratch_bytes, int M, int N, int K, int group, int dtype, void* stream);
 
 /* ---------------------------------------------------------------------------------------
  * W8A8 SmoothQuant int8 GEMM.

@@ -37,7 +37,8 @@ SIGNATURES = {
     "kbh_status_string": (ctypes.c_char_p, [_i]),
     "kbh_last_hip_error": (_i, []),
     "kbh_w4a16_workspace_bytes": (_sz, [_i, _i, _i, _i]),
-    "kbh_w4a16_gemm": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _sz, _i, _i, _i, _i, _i, _vp]),
+    "kbh_w4a16_scratch_bytes": (_sz, [_i, _i, _i, _i]),
+    "kbh_w4a16_gemm": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _sz, _vp, _sz, _i, _i, _i, _i, _i, _vp]),
     "kbh_w8a8_workspace_bytes": (_sz, [_i, _i, _i]),
     "kbh_w8a8_gemm": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _sz, _i, _i, _i, _vp]),
     "kbh_w8a8_gemm_i32": (_i, [_vp, _vp, _vp, _vp, _sz, _i, _i, _i, _vp]),

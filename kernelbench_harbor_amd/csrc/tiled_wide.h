@@ -1,0 +1,296 @@
+// Wide-tile fp16/bf16 MFMA GEMM for large M with a pluggable weight-slab producer.
+//
+// y[M, N] = x[M, K] @ W[K, N]; x, y fp16 or bf16; W produced 32 K-rows x TN columns at a time by
+// a policy from its packed/quantized storage. One 256-thread workgroup owns a TM x TN output tile
+// and one K range (split-K); the tile is sized so that two workgroups fit on a CU (<= 128
+// accumulator and <= 128 other VGPRs per lane), which lets one workgroup's MFMAs run while the
+// other waits on memory or a barrier:
+//  * x never passes through LDS: each wave loads its own rows' MFMA A fragments straight from
+//    global memory (16 bytes per lane per 32x16 fragment), two slabs ahead of their use.
+//  * The weight slab is dequantized once per workgroup into LDS in MFMA B-fragment order
+//    (wide_b_offset), so a fragment read is one conflict-free ds_read_b128 per wave.
+//  * WM x (4/WM) waves, each (TM/WM) x (TN*WM/4) with 32x32x16 MFMAs; accumulators in AGPRs.
+//  * Per slab, one barrier: B fragments of k16 step 1 are read before the step-0 MFMAs, the next
+//    slab's weights are dequantized and written in parts between the step-0 MFMAs, and the next
+//    slab's step-0 fragments are read after the barrier while the step-1 MFMAs run, interleaved
+//    with the next global loads.
+//  * Per-group constants of the weight format (scales, zero points) are loaded once per
+//    quantization group into one of two register sets; the loop is unrolled over two groups
+//    (2*SPG slabs, SPG = slabs per group), so the set in use is known at compile time and no
+//    register copies are needed.
+//  * Split-K (splits > 1): partial tiles go to per-split fp32 slices of a workspace (plain
+//    stores), summed in split order by wide_reduce_kernel.
+//  * Workgroup ids are remapped so that each XCD runs consecutive tiles of the same rows of x
+//    and K range (its L2 then serves the shared x fragments).
+//
+// Policy interface (BP), for 256 threads and a 32 x TN slab:
+//   struct Raw;  struct Grp;                            per-thread slab data / group constants
+//   static constexpr int kTN, kParts;
+//   void load(Raw&, int k0, int n0, int t) const;       issue the slab's global loads
+//   void load_group(Grp&, int k0, int n0, int t) const; constants of the group holding row k0
+//   void store_part(const Raw&, const Grp&, uint8_t* Bs, int t, int p) const;
+//                                                       part p < kParts of the slab into LDS
+//   The LDS byte offset of element (k, n) of the slab is wide_b_offset<kTN>(k, n).
+#pragma once
+
+#include "kbh_common.h"
+
+namespace kbh {
+
+constexpr int WBK = 32;  // K rows per slab
+
+// Column slot within a slab: columns are permuted within groups of 8 (slot = 8q + ((n ^ f(q)) &
+// 7), q = n/8, f(q) = q ^ (q >> 3)) so that producer writes, which step through packed words 8
+// columns apart, spread over all LDS banks.
+__device__ __host__ inline int wide_slot(int n) {
+  const int q = n >> 3;
+  return (n & ~7) | ((n ^ q ^ (q >> 3)) & 7);
+}
+// Byte offset of W[k, n] (k < 32, n < TN) in a slab buffer: [k16 step][k half][column slot]
+// [8 values]. The 8 consecutive k of one column that a lane feeds to an MFMA are one 16-byte
+// chunk and the 32 lanes of a fragment read 512 contiguous bytes.
+template <int TN>
+__device__ __host__ inline int wide_b_offset(int k, int n) {
+  return (k >> 4) * (TN * 32) + ((k >> 3) & 1) * (TN * 16) + wide_slot(n) * 16 + (k & 7) * 2;
+}
+
+template <int TM, int TN, int WM>
+struct WideShape {
+  static constexpr int WN = 4 / WM;
+  static constexpr int RB = TM / (32 * WM);  // 32-row MFMA blocks per wave
+  static constexpr int CB = TN / (32 * WN);  // 32-column MFMA blocks per wave
+  static_assert(RB >= 1 && CB >= 1 && WM * WN == 4, "tile shape");
+  // Two workgroups per CU when the accumulators fit in 128 registers per lane.
+  static constexpr int kMinBlocks = RB * CB <= 8 ? 2 : 1;
+};
+
+template <bool BF16, int TM, int WM, int SPG, class BP>
+__global__ __launch_bounds__(256, (WideShape<TM, BP::kTN, WM>::kMinBlocks)) void tiled_wide_gemm(
+    const uint16_t* __restrict__ x, BP bp, uint16_t* __restrict__ y, float* __restrict__ ws, int M,
+    int N, int K, int splits, int slabs_per_split) {
+  constexpr int TN = BP::kTN;
+  using Shape = WideShape<TM, TN, WM>;
+  constexpr int RB = Shape::RB, CB = Shape::CB, WN = Shape::WN;
+  constexpr int SLAB = TN * 64;  // LDS bytes per slab buffer
+  constexpr int U = 2 * SPG;  // slabs per loop iteration (two groups)
+  __shared__ __attribute__((aligned(16))) uint8_t Bs[2][SLAB];
+
+  const int t = threadIdx.x;
+  const int lane = t & 63, wave = t >> 6;
+  const int wm = wave / WN, wn = wave % WN;
+  const int NB = N / TN;
+  const int id = xcd_remap(blockIdx.x, gridDim.x);
+  const int nb = id % NB;
+  const int rest = id / NB;
+  const int split = rest % splits;
+  const int mb = rest / splits;
+  const int m0 = mb * TM, n0 = nb * TN;
+  const int kt0 = split * slabs_per_split;
+  const int KT = slabs_per_split;
+
+  // A fragments: lane (r = lane%32, g = lane/32) of row block rb holds row
+  // m0 + wm*TM/WM + 32rb + r, k = k0 + 16*step + 8g .. +8.
+  const int fr = lane & 31, fg = lane >> 5;
+  const uint16_t* xrow[RB];
+#pragma unroll
+  for (int rb = 0; rb < RB; ++rb) {
+    const int r = m0 + wm * (TM / WM) + rb * 32 + fr;
+    xrow[rb] = x + (size_t)(r < M ? r : M - 1) * K + fg * 8;  // rows >= M are never stored
+  }
+  struct AStage {
+    kbh_u32x4 a[RB][2];
+  };
+  auto load_a_step = [&](AStage& st, int kt, int s) {
+    const int k0 = (kt0 + kt) * WBK + 16 * s;
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) st.a[rb][s] = *reinterpret_cast<const kbh_u32x4*>(xrow[rb] + k0);
+  };
+  auto load_b = [&](typename BP::Raw& r, int kt) { bp.load(r, (kt0 + kt) * WBK, n0, t); };
+  auto load_g = [&](typename BP::Grp& g, int kt) { bp.load_group(g, (kt0 + kt) * WBK, n0, t); };
+
+  // B fragment of step s, column block j of this wave: lane (c = lane%32, g) reads column
+  // wn*32CB + 32j + c, k = 16s + 8g .. +8.
+  int boff[CB];
+#pragma unroll
+  for (int j = 0; j < CB; ++j) boff[j] = wide_b_offset<TN>(8 * fg, wn * 32 * CB + 32 * j + fr);
+  auto read_b = [&](kbh_u32x4 (&bf)[CB], int buf, int s) {
+#pragma unroll
+    for (int j = 0; j < CB; ++j)
+      bf[j] = *reinterpret_cast<const kbh_u32x4*>(&Bs[buf][boff[j] + s * (TN * 32)]);
+  };
+
+  kbh_f32x16 acc[RB][CB];
+#pragma unroll
+  for (int i = 0; i < RB; ++i)
+#pragma unroll
+    for (int j = 0; j < CB; ++j)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
+
+  auto mma = [&](const AStage& st, int s, const kbh_u32x4 (&bf)[CB]) {
+#pragma unroll
+    for (int i = 0; i < RB; ++i)
+#pragma unroll
+      for (int j = 0; j < CB; ++j) acc[i][j] = mfma32x32x16<BF16>(st.a[i][s], bf[j], acc[i][j]);
+  };
+  // MFMAs q in [lo, hi) of a k16 step (q = CB*i + j).
+  auto mma_range = [&](const AStage& st, int s, const kbh_u32x4 (&bf)[CB], int lo, int hi) {
+#pragma unroll
+    for (int q = 0; q < RB * CB; ++q)
+      if (q >= lo && q < hi)
+        acc[q / CB][q % CB] = mfma32x32x16<BF16>(st.a[q / CB][s], bf[q % CB], acc[q / CB][q % CB]);
+  };
+
+  // Prologue: slab 0 in LDS, step-0 fragments of slab 0 in registers, A of slabs 0 and 1, raw
+  // weights of slabs 1 and 2 and the constants of the second group in flight.
+  AStage A[2];
+  typename BP::Raw R[2];
+  typename BP::Grp G[2];  // constants of groups with even / odd index within the K range
+  const int last = KT - 1;
+  load_b(R[0], 0);
+  load_g(G[0], 0);
+#pragma unroll
+  for (int st = 0; st < 2; ++st) {
+    load_a_step(A[0], 0, st);
+    load_a_step(A[1], min(1, last), st);
+  }
+#pragma unroll
+  for (int p = 0; p < BP::kParts; ++p) bp.store_part(R[0], G[0], Bs[0], t, p);
+  load_b(R[1], min(1, last));
+  load_b(R[0], min(2, last));
+  load_g(G[1], min(SPG, last));
+  __syncthreads();
+  kbh_u32x4 b0[CB], b1[CB];
+  read_b(b0, 0, 0);
+
+  // Steady state: KT is a multiple of U; loads past the end re-read the last slab or group
+  // (never used), so the loop body is branch-free. Slab s+1, dequantized during slab s, belongs
+  // to group (u+1)/SPG of the iteration (register set ((u+1)/SPG) & 1); when it starts a group,
+  // the set of the group just finished is reloaded with the group after next. The order inside
+  // a slab is fixed with scheduling barriers (the scheduler otherwise clusters the
+  // dequantisation and moves MFMAs across s_barrier).
+  constexpr int NMF = RB * CB;  // MFMAs per k16 step
+  constexpr int NP = BP::kParts;
+  for (int kt = 0; kt < KT; kt += U) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int s = kt + u;  // slab in registers / LDS buffer u&1
+      const int cur = u & 1;
+      const bool new_group = (u + 1) % SPG == 0;  // slab s+1 starts a group
+      const int gsel = ((u + 1) / SPG) & 1;
+      read_b(b1, cur, 1);
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int p = 0; p < NP; ++p) {
+        mma_range(A[cur], 0, b0, p * NMF / NP, (p + 1) * NMF / NP);
+        __builtin_amdgcn_sched_barrier(0);
+        bp.store_part(R[1 - cur], G[gsel], Bs[1 - cur], t, p);  // slab s+1 (after last: unused)
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      __syncthreads();  // s_barrier alone does not stop MFMAs moving across: fenced both sides
+      __builtin_amdgcn_sched_barrier(0);
+      read_b(b0, 1 - cur, 0);  // step 0 of slab s+1
+      mma(A[cur], 1, b1);
+      load_a_step(A[cur], min(s + 2, last), 0);
+      load_b(R[1 - cur], min(s + 3, last));
+      if (new_group) load_g(G[gsel ^ 1], min(s + 1 + SPG, last));
+      load_a_step(A[cur], min(s + 2, last), 1);
+      __builtin_amdgcn_sched_group_barrier(0x100, CB, 1);
+#pragma unroll
+      for (int i = 0; i < NMF; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);
+        __builtin_amdgcn_sched_group_barrier(0x020, 1, 1);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+
+  // Accumulator element e of tile (i, j): row 8(e/4) + 4(lane/32) + e%4, column lane%32.
+  const int rbase = m0 + wm * (TM / WM) + 4 * fg;
+  const int cbase = n0 + wn * 32 * CB + fr;
+  if (splits == 1) {
+#pragma unroll
+    for (int i = 0; i < RB; ++i)
+#pragma unroll
+      for (int j = 0; j < CB; ++j)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+          const int r = rbase + 32 * i + 8 * (e >> 2) + (e & 3);
+          if (r < M) y[(size_t)r * N + cbase + 32 * j] = f32_to_half_bits<BF16>(acc[i][j][e]);
+        }
+    return;
+  }
+  // Split-K: the fp32 partial tile goes to this split's slice of the workspace (plain stores);
+  // wide_reduce_kernel sums the slices afterwards. The launch boundary orders the two, so no
+  // device-scope fences or atomics are needed (both cost far more here than a second small
+  // launch), and the sum order is fixed.
+  float* part = ws + (size_t)split * M * N;
+#pragma unroll
+  for (int i = 0; i < RB; ++i)
+#pragma unroll
+    for (int j = 0; j < CB; ++j)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const int r = rbase + 32 * i + 8 * (e >> 2) + (e & 3);
+        if (r < M) part[(size_t)r * N + cbase + 32 * j] = acc[i][j][e];
+      }
+}
+
+// y = sum over splits of ws[split] (in split order), converted to fp16/bf16. One thread per 4
+// consecutive outputs; n4 = M * N / 4.
+template <bool BF16>
+__global__ __launch_bounds__(256) void wide_reduce_kernel(const float* __restrict__ ws,
+                                                          uint16_t* __restrict__ y, size_t n4,
+                                                          int splits) {
+  const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= n4) return;
+  const kbh_f32x4* p = reinterpret_cast<const kbh_f32x4*>(ws) + i;
+  kbh_f32x4 v = __builtin_nontemporal_load(p);
+  for (int sp = 1; sp < splits; ++sp) v += __builtin_nontemporal_load(p + sp * n4);
+  kbh_u32x2 o;
+  o[0] = (uint32_t)f32_to_half_bits<BF16>(v[0]) | ((uint32_t)f32_to_half_bits<BF16>(v[1]) << 16);
+  o[1] = (uint32_t)f32_to_half_bits<BF16>(v[2]) | ((uint32_t)f32_to_half_bits<BF16>(v[3]) << 16);
+  *reinterpret_cast<kbh_u32x2*>(y + 4 * i) = o;
+}
+
+// Launch geometry: tiles ordered (row block, split, column block) so that consecutive ids,
+// which share an XCD, share rows of x and a K range.
+struct WidePlan {
+  int tm;               // 128 or 256
+  int splits;           // K ranges
+  int slabs_per_split;  // multiple of the loop unroll
+  int grid;
+};
+
+// Picks the tile height and the split count. `slots` is the number of workgroups the GPU runs
+// at once (256 CUs x workgroups per CU). A split count is valid when it divides the K slabs into
+// ranges of at least 8 slabs that are a multiple of `unroll`; among those, the plan minimises
+// (waves of workgroups) x (slabs per workgroup), preferring fewer splits on a tie.
+inline bool plan_wide(int M, int N, int K, int tn, int unroll, int slots, WidePlan* p) {
+  if (N % tn != 0 || K % (unroll * WBK) != 0 || M < 1) return false;
+  const int KT = K / WBK;
+  p->tm = M > 128 ? 256 : 128;
+  const int tiles = ((M + p->tm - 1) / p->tm) * (N / tn);
+  long best = -1;
+  for (int s = 1; s <= KT / unroll; ++s) {
+    if (KT % s != 0) continue;
+    const int spp = KT / s;
+    if (spp % unroll != 0 || (spp < 8 && s > 1)) continue;
+    const long waves = ((long)tiles * s + slots - 1) / slots;
+    const long cost = waves * spp;
+    if (best < 0 || cost < best) {
+      best = cost;
+      p->splits = s;
+      p->slabs_per_split = spp;
+    }
+  }
+  p->grid = tiles * p->splits;
+  return true;
+}
+
+// Workspace: `splits` fp32 slices of M x N (none without split-K).
+inline size_t wide_workspace_bytes(int M, int N, int splits) {
+  return splits <= 1 ? 0 : round_up((size_t)splits * M * N * 4u, 256);
+}
+
+}  // namespace kbh

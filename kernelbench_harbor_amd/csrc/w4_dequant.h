@@ -3,6 +3,7 @@
 
 #include "kbh_common.h"
 #include "tiled_f16.h"
+#include "tiled_wide.h"
 
 namespace kbh {
 
@@ -29,8 +30,8 @@ __device__ inline uint32_t pair_bytes_rt(uint32_t wa, uint32_t wb, int j) {
 }
 
 // Dequantizes one thread's 2 rows (k, k+1) x 8 columns: result column c is the dword holding
-// the two 16-bit values (k, k+1). The arithmetic is the reference's: (q - z) in the input dtype
-// (exact: small integers), times s with one rounding.
+// the two 16-bit values (k, k+1). The arithmetic is the reference's: (q - z) rounded to the
+// input dtype (exact for integer zero points), times s rounded to the input dtype.
 template <bool BF16>
 __device__ inline void dequant_2x8(uint32_t w0, uint32_t w1, kbh_u32x4 sv, kbh_u32x4 zv,
                                    uint32_t out[8]) {
@@ -47,18 +48,22 @@ __device__ inline void dequant_2x8(uint32_t w0, uint32_t w1, kbh_u32x4 sv, kbh_u
       const uint16_t sb = (uint16_t)((col & 1) ? (sv[col >> 1] >> 16) : (sv[col >> 1] & 0xffffu));
       const uint16_t zb = (uint16_t)((col & 1) ? (zv[col >> 1] >> 16) : (zv[col >> 1] & 0xffffu));
       if constexpr (BF16) {
-        // (128+q) - (128+z) is exact in fp32, times s is exact in fp32; one rounding to bf16.
+        // q - z is exact in fp32 and rounds once to bf16; times s is exact in fp32 and rounds.
         const float s = bf16_bits_to_f32(sb);
-        const float bz = 128.0f + bf16_bits_to_f32(zb);
-        const float lo = (bf16_bits_to_f32((uint16_t)(h & 0xffffu)) - bz) * s;
-        const float hi = (bf16_bits_to_f32((uint16_t)(h >> 16)) - bz) * s;
-        out[col] = (uint32_t)f32_to_bf16_bits(lo) | ((uint32_t)f32_to_bf16_bits(hi) << 16);
+        const float z = bf16_bits_to_f32(zb);
+        const __bf16 dl = (__bf16)((bf16_bits_to_f32((uint16_t)(h & 0xffffu)) - 128.0f) - z);
+        const __bf16 dh = (__bf16)((bf16_bits_to_f32((uint16_t)(h >> 16)) - 128.0f) - z);
+        const __bf16 el = (__bf16)((float)dl * s);
+        const __bf16 eh = (__bf16)((float)dh * s);
+        out[col] = (uint32_t)__builtin_bit_cast(uint16_t, el) |
+                   ((uint32_t)__builtin_bit_cast(uint16_t, eh) << 16);
       } else {
         typedef _Float16 h2 __attribute__((ext_vector_type(2)));
         const _Float16 sc = __builtin_bit_cast(_Float16, sb);
-        const _Float16 bz = (_Float16)1024.0f + __builtin_bit_cast(_Float16, zb);
-        const h2 d = __builtin_bit_cast(h2, h) - h2{bz, bz};  // q - z, exact
-        out[col] = __builtin_bit_cast(uint32_t, d * h2{sc, sc});
+        const _Float16 zc = __builtin_bit_cast(_Float16, zb);
+        const h2 magic = {(_Float16)1024.0f, (_Float16)1024.0f};
+        const h2 q = __builtin_bit_cast(h2, h) - magic;  // exact
+        out[col] = __builtin_bit_cast(uint32_t, (q - h2{zc, zc}) * h2{sc, sc});
       }
     }
   }
@@ -100,6 +105,108 @@ struct W4SlabPolicy {
     dequant_2x8<BF16>(r.b[0], r.b[1], r.s, r.z, dq);
 #pragma unroll
     for (int c = 0; c < 8; ++c) *reinterpret_cast<uint32_t*>(&Bs[(wc * 8 + c) * TLD + 2 * kp]) = dq[c];
+  }
+};
+
+// Weight-slab producer for tiled_wide_gemm (32 rows x TN columns per slab, TN = 128 or 256).
+// Thread t owns packed word column w (8 output columns) and kRows consecutive rows of the slab
+// (word_of, rows_of); its LDS writes are bank-conflict free. The arithmetic is the reference's,
+// exactly: (q - z) rounded to the input dtype, times s rounded to the input dtype.
+template <bool BF16, int TN>
+struct W4WidePolicy {
+  static constexpr int kTN = TN;
+  static constexpr int kRows = TN / 64;  // rows per thread: 4 (TN = 256) or 2 (TN = 128)
+  static constexpr int kParts = 8;       // store_part(p) writes column p of the thread's word
+  const uint32_t* qw;
+  const uint16_t* scales;
+  const uint16_t* zeros;
+  int N, group;
+  size_t q_stride, s_stride;  // elements between experts (grouped GEMMs); 0 for one matrix
+  uint32_t mask;              // 0x000F000F, as a kernel argument so it lives in an SGPR
+  __device__ W4WidePolicy at_expert(int e) const {
+    W4WidePolicy p = *this;
+    p.qw += (size_t)e * q_stride;
+    p.scales += (size_t)e * s_stride;
+    p.zeros += (size_t)e * s_stride;
+    return p;
+  }
+  struct Raw {
+    uint32_t w[kRows];
+  };
+  struct Grp {
+    kbh_u32x4 s, z;
+  };
+  // TN = 256: t = [w bits 0-2][h bit 0][w bits 3-4][h bits 1-2], rows 4h..4h+3.
+  // TN = 128: t = [h bits 0-1][w bits 0-2][w bit 3][h bits 2-3], rows 2h, 2h+1.
+  // Either way the lanes of one LDS write pass cover distinct banks.
+  __device__ static int word_of(int t) {
+    if constexpr (TN == 256) return (t & 7) | (((t >> 4) & 3) << 3);
+    else return ((t >> 2) & 7) | (((t >> 5) & 1) << 3);
+  }
+  __device__ static int rows_of(int t) {  // index h of the thread's row block
+    if constexpr (TN == 256) return ((t >> 3) & 1) | ((t >> 6) << 1);
+    else return (t & 3) | ((t >> 6) << 2);
+  }
+
+  __device__ void load(Raw& r, int k0, int n0, int t) const {
+    const int w = word_of(t), h = rows_of(t);
+    const int NP = N >> 3;
+    const uint32_t* q = qw + (size_t)(k0 + kRows * h) * NP + (n0 >> 3) + w;
+#pragma unroll
+    for (int i = 0; i < kRows; ++i) r.w[i] = __builtin_nontemporal_load(q + (size_t)i * NP);
+  }
+  __device__ void load_group(Grp& g, int k0, int n0, int t) const {
+    const size_t off = (size_t)(k0 / group) * N + n0 + 8 * word_of(t);
+    g.s = *reinterpret_cast<const kbh_u32x4*>(scales + off);
+    g.z = *reinterpret_cast<const kbh_u32x4*>(zeros + off);
+  }
+
+  // Rows (2i, 2i+1) of column c of the thread's word, dequantized: one dword (two values).
+  template <int C>
+  __device__ uint32_t pair(const Raw& r, const Grp& g, int i) const {
+    const uint32_t P = pair_bytes<(C >> 1)>(r.w[2 * i], r.w[2 * i + 1]);
+    const uint32_t m = (C & 1) ? ((P >> 4) & mask) : (P & mask);
+    const uint32_t zw = g.z[C >> 1], sw = g.s[C >> 1];
+    const uint16_t zb = (uint16_t)((C & 1) ? (zw >> 16) : (zw & 0xffffu));
+    const uint16_t sb = (uint16_t)((C & 1) ? (sw >> 16) : (sw & 0xffffu));
+    if constexpr (BF16) {
+      // q - z is exact in fp32 and rounds once to bf16; times s is exact in fp32 and rounds once.
+      const float z = bf16_bits_to_f32(zb), s = bf16_bits_to_f32(sb);
+      const __bf16 d0 = (__bf16)((float)(m & 0xffu) - z);
+      const __bf16 d1 = (__bf16)((float)(m >> 16) - z);
+      const __bf16 e0 = (__bf16)((float)d0 * s);
+      const __bf16 e1 = (__bf16)((float)d1 * s);
+      return (uint32_t)__builtin_bit_cast(uint16_t, e0) |
+             ((uint32_t)__builtin_bit_cast(uint16_t, e1) << 16);
+    } else {
+      typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+      const _Float16 z = __builtin_bit_cast(_Float16, zb), sc = __builtin_bit_cast(_Float16, sb);
+      const h2 magic = {(_Float16)1024.0f, (_Float16)1024.0f};
+      const h2 q = __builtin_bit_cast(h2, m | kMagicF16) - magic;  // exact
+      return __builtin_bit_cast(uint32_t, (q - h2{z, z}) * h2{sc, sc});
+    }
+  }
+  template <int C>
+  __device__ void put(const Raw& r, const Grp& g, uint8_t* base, int fw) const {
+    uint8_t* p = base + ((C ^ fw) << 4);
+    if constexpr (kRows == 4) *reinterpret_cast<kbh_u32x2*>(p) = kbh_u32x2{pair<C>(r, g, 0), pair<C>(r, g, 1)};
+    else *reinterpret_cast<uint32_t*>(p) = pair<C>(r, g, 0);
+  }
+  __device__ void store_part(const Raw& r, const Grp& g, uint8_t* Bs, int t, int p) const {
+    const int w = word_of(t), h = rows_of(t);
+    // wide_b_offset<TN>(kRows*h, 8w + c) = base + 16 * (c ^ f(w)).
+    uint8_t* base = Bs + wide_b_offset<TN>(kRows * h, 8 * w) - wide_slot(8 * w) * 16 + w * 128;
+    const int fw = (w ^ (w >> 3)) & 7;
+    switch (p) {
+      case 0: put<0>(r, g, base, fw); break;
+      case 1: put<1>(r, g, base, fw); break;
+      case 2: put<2>(r, g, base, fw); break;
+      case 3: put<3>(r, g, base, fw); break;
+      case 4: put<4>(r, g, base, fw); break;
+      case 5: put<5>(r, g, base, fw); break;
+      case 6: put<6>(r, g, base, fw); break;
+      default: put<7>(r, g, base, fw); break;
+    }
   }
 };
 

@@ -25,12 +25,16 @@
 //    clears the workspace. Workgroup ids are remapped so that all K splits of a column tile run
 //    on one XCD.
 //
-// Larger M: tiled_f16_gemm (tiled_f16.h) with W4SlabPolicy, which dequantizes the packed
-// weights on their way into LDS with the exact reference arithmetic ((q - z) in the input
-// dtype, times s, one rounding), stored k-major per column.
+// Larger M (M > 32): tiled_wide_gemm (tiled_wide.h) with W4WidePolicy, which dequantizes each
+// packed 32 x TN weight slab once per workgroup into LDS with the exact reference arithmetic
+// ((q - z) rounded to the input dtype, times s rounded), in MFMA fragment order; x goes from
+// global memory straight into MFMA registers. Split-K partial sums use the caller's scratch.
+// Shapes it does not cover fall back to tiled_f16_gemm (256 x 128 LDS-staged tiles) or to the
+// decode kernel.
 #include "kbh_common.h"
 #include "splitk.h"
 #include "tiled_f16.h"
+#include "tiled_wide.h"
 #include "w4_dequant.h"
 
 namespace kbh {
@@ -210,10 +214,65 @@ void dispatch_decode(const DecodePlan& p, const void* x, const int32_t* qw, cons
 }
 
 // ======================================================================================
-// Tiled kernel
+// Large-M kernels
 // ======================================================================================
-// The tiled kernel beats the split-K decode kernel once the 256-row tiles are reasonably full.
+// Above kWideMinM rows the wide-tile kernel (tiled_wide.h) takes over from the split-K decode
+// kernel: 128 x 128 tiles (two workgroups per CU) up to 128 rows, 256 x 256 tiles above. The
+// older 256 x 128 LDS-staged kernel remains for shapes the wide kernel does not cover.
+constexpr int kWideMinM = 33;
 constexpr int kTiledMinM = 128;
+
+struct W4Wide {
+  WidePlan plan;
+  int tn;
+  int spg;  // K slabs (32 rows) per quantization group
+};
+
+bool plan_w4_wide(int M, int N, int K, int group, W4Wide* w) {
+  if (M < kWideMinM) return false;
+  w->spg = group / WBK;
+  const bool small = M <= 128;
+  w->tn = small ? 128 : 256;
+  if (N % w->tn != 0) return false;
+  return plan_wide(M, N, K, w->tn, 2 * w->spg, small ? 512 : 256, &w->plan);
+}
+
+template <bool BF16, int TM, int TN, int SPG>
+void launch_w4_wide(const W4Wide& w, const void* x, const int32_t* qw, const void* s, const void* z,
+                    void* y, float* scratch, int M, int N, int K, int group, hipStream_t st) {
+  const W4WidePolicy<BF16, TN> bp{(const uint32_t*)qw, (const uint16_t*)s, (const uint16_t*)z,
+                                  N, group, 0, 0, 0x000F000Fu};
+  hipLaunchKernelGGL((tiled_wide_gemm<BF16, TM, 4, SPG, W4WidePolicy<BF16, TN>>),
+                     dim3(w.plan.grid), dim3(256), 0, st, (const uint16_t*)x, bp, (uint16_t*)y,
+                     scratch, M, N, K, w.plan.splits, w.plan.slabs_per_split);
+  if (w.plan.splits > 1) {
+    const size_t n4 = (size_t)M * N / 4;
+    hipLaunchKernelGGL((wide_reduce_kernel<BF16>), dim3((unsigned)((n4 + 255) / 256)), dim3(256), 0,
+                       st, scratch, (uint16_t*)y, n4, w.plan.splits);
+  }
+}
+
+template <bool BF16, int TM, int TN>
+void dispatch_w4_wide_spg(const W4Wide& w, const void* x, const int32_t* qw, const void* s,
+                          const void* z, void* y, float* scratch, int M, int N, int K, int group,
+                          hipStream_t st) {
+  switch (w.spg) {
+    case 1: return launch_w4_wide<BF16, TM, TN, 1>(w, x, qw, s, z, y, scratch, M, N, K, group, st);
+    case 2: return launch_w4_wide<BF16, TM, TN, 2>(w, x, qw, s, z, y, scratch, M, N, K, group, st);
+    case 4: return launch_w4_wide<BF16, TM, TN, 4>(w, x, qw, s, z, y, scratch, M, N, K, group, st);
+    default: return launch_w4_wide<BF16, TM, TN, 8>(w, x, qw, s, z, y, scratch, M, N, K, group, st);
+  }
+}
+
+template <bool BF16>
+void dispatch_w4_wide(const W4Wide& w, const void* x, const int32_t* qw, const void* s,
+                      const void* z, void* y, float* scratch, int M, int N, int K, int group,
+                      hipStream_t st) {
+  if (w.tn == 128)
+    dispatch_w4_wide_spg<BF16, 128, 128>(w, x, qw, s, z, y, scratch, M, N, K, group, st);
+  else
+    dispatch_w4_wide_spg<BF16, 256, 256>(w, x, qw, s, z, y, scratch, M, N, K, group, st);
+}
 
 }  // namespace
 }  // namespace kbh
@@ -224,9 +283,16 @@ extern "C" size_t kbh_w4a16_workspace_bytes(int M, int N, int K, int group) {
   return kbh::splitk_workspace_bytes(M, N);
 }
 
+extern "C" size_t kbh_w4a16_scratch_bytes(int M, int N, int K, int group) {
+  kbh::W4Wide w;
+  if (M < 1 || N < 128 || K < 32 || group < 32 || !kbh::plan_w4_wide(M, N, K, group, &w)) return 0;
+  return kbh::wide_workspace_bytes(M, N, w.plan.splits);
+}
+
 extern "C" int kbh_w4a16_gemm(const void* x, const int32_t* qweight, const void* scales,
                               const void* zeros, void* y, void* workspace, size_t workspace_bytes,
-                              int M, int N, int K, int group, int dtype, void* stream) {
+                              void* scratch, size_t scratch_bytes, int M, int N, int K, int group,
+                              int dtype, void* stream) {
   using namespace kbh;
   if (!x || !qweight || !scales || !zeros || !y) return KBH_ERR_NULL;
   if (dtype != KBH_F16 && dtype != KBH_BF16) return KBH_ERR_DTYPE;
@@ -238,6 +304,16 @@ extern "C" int kbh_w4a16_gemm(const void* x, const int32_t* qweight, const void*
     return KBH_ERR_ALIGN;
   const bool bf = dtype == KBH_BF16;
   hipStream_t st = (hipStream_t)stream;
+
+  W4Wide wide;
+  if (plan_w4_wide(M, N, K, group, &wide)) {
+    const size_t need = wide_workspace_bytes(M, N, wide.plan.splits);
+    if (need > 0 && (!scratch || scratch_bytes < need)) return KBH_ERR_WORKSPACE;
+    if (need > 0 && !aligned16(scratch)) return KBH_ERR_ALIGN;
+    if (bf) dispatch_w4_wide<true>(wide, x, qweight, scales, zeros, y, (float*)scratch, M, N, K, group, st);
+    else dispatch_w4_wide<false>(wide, x, qweight, scales, zeros, y, (float*)scratch, M, N, K, group, st);
+    return launch_status();
+  }
 
   if (M >= kTiledMinM && K % (TBK * TDEPTH) == 0) {
     if (bf) {

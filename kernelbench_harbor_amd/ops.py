@@ -16,13 +16,15 @@ _DT_CODE = {torch.float16: _lib.KBH_F16, torch.bfloat16: _lib.KBH_BF16}
 
 
 class _WorkspacePool:
-    """Zero-filled device scratch per (device, stream), grown on demand.
+    """Device buffers per (device, stream), grown on demand.
 
-    The kernels leave the workspace zero-filled after every call, so one buffer serves every
-    call that is ordered on the same stream.
+    zeroed=True: zero-filled workspace; the kernels leave it zero-filled after every call, so
+    one buffer serves every call ordered on the same stream. zeroed=False: scratch with no
+    content requirement (never shared with the zero-filled pool).
     """
 
-    def __init__(self):
+    def __init__(self, zeroed: bool):
+        self._zeroed = zeroed
         self._bufs: dict[tuple[int, int], torch.Tensor] = {}
         self._lock = threading.Lock()
 
@@ -32,12 +34,14 @@ class _WorkspacePool:
         with self._lock:
             buf = self._bufs.get(key)
             if buf is None or buf.numel() < nbytes:
-                buf = torch.zeros(max(nbytes, 256), dtype=torch.uint8, device=device)
+                alloc = torch.zeros if self._zeroed else torch.empty
+                buf = alloc(max(nbytes, 256), dtype=torch.uint8, device=device)
                 self._bufs[key] = buf
             return buf
 
 
-workspaces = _WorkspacePool()
+workspaces = _WorkspacePool(zeroed=True)
+scratches = _WorkspacePool(zeroed=False)
 
 
 def _require(cond: bool, msg: str) -> None:
@@ -90,11 +94,12 @@ def w4a16_gemm(x: torch.Tensor, qweight: torch.Tensor, scales: torch.Tensor,
     scales = scales.contiguous()
     zeros = zeros.contiguous()
     lib = _lib.load()
-    nbytes = lib.kbh_w4a16_workspace_bytes(M, N, K, group)
-    ws = workspaces.get(nbytes, dev)
+    ws = workspaces.get(lib.kbh_w4a16_workspace_bytes(M, N, K, group), dev)
+    sc = scratches.get(lib.kbh_w4a16_scratch_bytes(M, N, K, group), dev)
     st = lib.kbh_w4a16_gemm(x2.data_ptr(), qweight.data_ptr(), scales.data_ptr(),
                             zeros.data_ptr(), y.data_ptr(), ws.data_ptr(), ws.numel(),
-                            M, N, K, group, _DT_CODE[x.dtype], _stream_ptr(dev))
+                            sc.data_ptr(), sc.numel(), M, N, K, group, _DT_CODE[x.dtype],
+                            _stream_ptr(dev))
     _lib.check(st, "kbh_w4a16_gemm")
     return y.reshape(*lead, N)
 
@@ -250,7 +255,7 @@ def moe_route_top2(router_logits: torch.Tensor, dtype: torch.dtype = torch.float
     if T == 0:
         return topi, topw
     lib = _lib.load()
-    ws = workspaces.get(lib.kbh_qmoe_workspace_bytes(T, 0, 0, E), dev)
+    ws = scratches.get(lib.kbh_qmoe_workspace_bytes(T, 0, 0, E), dev)
     st = lib.kbh_moe_route_top2(router_logits.contiguous().data_ptr(), _LOGIT_CODE[router_logits.dtype],
                                 topi.data_ptr(), topw.data_ptr(), ws.data_ptr(), ws.numel(), T, E,
                                 _DT_CODE[dtype], _stream_ptr(dev))
@@ -279,7 +284,7 @@ def qmoe(x: torch.Tensor, qweight: torch.Tensor, scales: torch.Tensor,
     if T == 0:
         return y
     lib = _lib.load()
-    ws = workspaces.get(lib.kbh_qmoe_workspace_bytes(T, D, N, E), dev)
+    ws = scratches.get(lib.kbh_qmoe_workspace_bytes(T, D, N, E), dev)
     st = lib.kbh_qmoe(x.contiguous().data_ptr(), qweight.contiguous().data_ptr(),
                       scales.contiguous().data_ptr(), router_logits.contiguous().data_ptr(),
                       _LOGIT_CODE[router_logits.dtype], y.data_ptr(), ws.data_ptr(), ws.numel(),
@@ -320,7 +325,7 @@ def qmoe_ffn(x, router_logits, gate_qweight, gate_scales, gate_zeros, up_qweight
     if T == 0:
         return y
     lib = _lib.load()
-    ws = workspaces.get(lib.kbh_qmoe_ffn_workspace_bytes(T, D, F, E), dev)
+    ws = scratches.get(lib.kbh_qmoe_ffn_workspace_bytes(T, D, F, E), dev)
     ts = [t_.contiguous() for t_ in ts]
     st = lib.kbh_qmoe_ffn(ts[0].data_ptr(), router_logits.contiguous().data_ptr(),
                           _LOGIT_CODE[router_logits.dtype], *[t_.data_ptr() for t_ in ts[1:]],

@@ -41,8 +41,10 @@ def dequant(qweight, scales, zeros, dtype: str) -> np.ndarray:
     """W = (unpack(qweight) - zeros[k//G]) * scales[k//G] in `dtype` (float32 values).
 
     reference.py:14-17: the nibbles are cast to x.dtype, scales/zeros are expanded per group of
-    G = K / scales.shape[0] rows, `(w - ze)` is exact (small integers) and `* se` rounds once to
-    x.dtype. dtype 'f32' is the ground-truth mode (all floating inputs upcast)."""
+    G = K / scales.shape[0] rows, `(w - ze)` rounds to x.dtype (exact when the zero points are
+    integers, as the reference generates them) and `* se` rounds once more to x.dtype. dtype
+    'f32' is the ground-truth mode (all floating inputs upcast; both steps exact in fp32 for
+    fp16/bf16 inputs)."""
     w = unpack_int4_along_n(qweight).astype(np.float32)
     s = np.asarray(scales, dtype=np.float32)
     z = np.asarray(zeros, dtype=np.float32)
@@ -50,7 +52,8 @@ def dequant(qweight, scales, zeros, dtype: str) -> np.ndarray:
     G = K // s.shape[0]
     se = np.repeat(s, G, axis=0)
     ze = np.repeat(z, G, axis=0)
-    return round_to((w - ze) * se, dtype)
+    d = round_to(w - ze, dtype)
+    return round_to(d * se, dtype)
 
 
 def forward(x, qweight, scales, zeros, dtype: str = F32) -> np.ndarray:

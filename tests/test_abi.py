@@ -44,12 +44,16 @@ def test_host_checks_run_without_gpu():
     """Bad arguments are rejected by the library before it touches the device."""
     lib = _lib.load()
     p = ctypes.c_void_p(16)  # aligned fake address; never dereferenced on these paths
-    assert lib.kbh_w4a16_gemm(None, p, p, p, p, p, 1 << 20, 16, 4096, 4096, 128, 0, None) == _lib.KBH_ERR_NULL
-    assert lib.kbh_w4a16_gemm(p, p, p, p, p, p, 1 << 20, 16, 4100, 4096, 128, 0, None) == _lib.KBH_ERR_SHAPE
-    assert lib.kbh_w4a16_gemm(p, p, p, p, p, p, 1 << 20, 16, 4096, 4096, 100, 0, None) == _lib.KBH_ERR_SHAPE
-    assert lib.kbh_w4a16_gemm(p, p, p, p, p, p, 1 << 20, 16, 4096, 4096, 128, 7, None) == _lib.KBH_ERR_DTYPE
-    assert lib.kbh_w4a16_gemm(p, ctypes.c_void_p(18), p, p, p, p, 1 << 20, 16, 4096, 4096, 128, 0, None) == _lib.KBH_ERR_ALIGN
-    assert lib.kbh_w4a16_gemm(p, p, p, p, p, p, 8, 16, 4096, 4096, 128, 0, None) == _lib.KBH_ERR_WORKSPACE
+    assert lib.kbh_w4a16_gemm(None, p, p, p, p, p, 1 << 20, p, 1 << 20, 16, 4096, 4096, 128, 0, None) == _lib.KBH_ERR_NULL
+    assert lib.kbh_w4a16_gemm(p, p, p, p, p, p, 1 << 20, p, 1 << 20, 16, 4100, 4096, 128, 0, None) == _lib.KBH_ERR_SHAPE
+    assert lib.kbh_w4a16_gemm(p, p, p, p, p, p, 1 << 20, p, 1 << 20, 16, 4096, 4096, 100, 0, None) == _lib.KBH_ERR_SHAPE
+    assert lib.kbh_w4a16_gemm(p, p, p, p, p, p, 1 << 20, p, 1 << 20, 16, 4096, 4096, 128, 7, None) == _lib.KBH_ERR_DTYPE
+    assert lib.kbh_w4a16_gemm(p, ctypes.c_void_p(18), p, p, p, p, 1 << 20, p, 1 << 20, 16, 4096, 4096, 128, 0, None) == _lib.KBH_ERR_ALIGN
+    assert lib.kbh_w4a16_gemm(p, p, p, p, p, p, 8, p, 1 << 20, 16, 4096, 4096, 128, 0, None) == _lib.KBH_ERR_WORKSPACE
+    # large M runs the wide-tile kernel, whose split-K partials need the scratch buffer
+    need = lib.kbh_w4a16_scratch_bytes(2048, 4096, 14336, 128)
+    assert lib.kbh_w4a16_gemm(p, p, p, p, p, p, 1 << 20, p, need - 1, 2048, 4096, 14336, 128, 0, None) == _lib.KBH_ERR_WORKSPACE
+    assert lib.kbh_w4a16_gemm(p, p, p, p, p, p, 1 << 20, None, 0, 2048, 4096, 14336, 128, 0, None) == _lib.KBH_ERR_WORKSPACE
     assert lib.kbh_w8a8_gemm(p, p, p, p, p, p, 1 << 20, 16, 4096, 100, None) == _lib.KBH_ERR_SHAPE
     assert lib.kbh_w8a8_gemm(p, p, p, p, p, None, 0, 16, 4096, 4096, None) == _lib.KBH_ERR_WORKSPACE
 
@@ -59,6 +63,8 @@ def test_workspace_sizes():
     assert lib.kbh_w4a16_workspace_bytes(16, 4096, 14336, 128) >= 16 * 4096 * 4
     assert lib.kbh_w8a8_workspace_bytes(16, 4096, 14336) >= 16 * 4096 * 4
     assert lib.kbh_w4a16_workspace_bytes(0, 4096, 14336, 128) == 0
+    assert lib.kbh_w4a16_scratch_bytes(16, 4096, 14336, 128) == 0       # decode kernel
+    assert lib.kbh_w4a16_scratch_bytes(2048, 4096, 14336, 128) >= 2048 * 4096 * 4 * 2  # split-K
 
 
 def test_missing_library_fails_loudly(tmp_path):

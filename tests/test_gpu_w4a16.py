@@ -38,6 +38,16 @@ CASES = [
     (513, 4096, 256, 128, torch.float16, "reference"),
     # K not a multiple of 64 -> split-K path even for large M
     (96, 1056, 256, 32, torch.float16, "baseline"),
+    # wide-tile kernel: 128x128 tiles (33 <= M <= 128), 256x256 tiles (M > 128, N % 256 == 0),
+    # every group size, split-K and not, ragged M
+    (33, 2048, 256, 64, torch.float16, "baseline"),
+    (128, 4096, 384, 256, torch.bfloat16, "reference"),
+    (129, 2048, 512, 32, torch.float16, "reference"),
+    (200, 1024, 768, 128, torch.bfloat16, "baseline"),
+    (384, 4096, 512, 64, torch.float16, "baseline"),
+    (257, 8192, 256, 128, torch.float16, "baseline"),
+    # N % 256 != 0 above 128 rows: the 256 x 128 LDS-staged kernel
+    (160, 2048, 384, 128, torch.float16, "baseline"),
 ]
 
 
@@ -61,21 +71,27 @@ def test_w4a16_full_size_decode(dev, M):
     assert cmp.ok, cmp
 
 
-@pytest.mark.parametrize("M", [16, 64])
+@pytest.mark.parametrize("M,N,frac_zeros", [(16, 512, False), (64, 512, False), (64, 512, True),
+                                             (200, 512, False), (200, 512, True), (160, 384, False)])
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
-def test_w4a16_dequant_bit_exact(dev, dtype, M):
+def test_w4a16_dequant_bit_exact(dev, dtype, M, N, frac_zeros):
     """One-hot activations select single weight rows, so y[m, :] is the dequantized row
     k_m rounded once to the output dtype: it must equal the reference's own dequantization
-    (unpack, subtract zero, multiply by scale, one rounding) bit for bit. M=16 exercises the
-    split-K decode kernel, M=64 the tiled kernel."""
-    K, N, G = 4096, 512, 128
+    (unpack, subtract zero with one rounding, multiply by scale with one rounding) bit for bit.
+    M=16 exercises the split-K decode kernel, M=64 and M=200 the wide-tile kernel (128- and
+    256-column tiles), N=384 at M=160 the 256 x 128 LDS-staged kernel. Zero points with a
+    fractional part make the subtraction round, which the wide kernel reproduces exactly."""
+    K, G = 4096, 128
     g = torch.Generator().manual_seed(7 + M)
     qw = inputs.random_packed_int4(K, N, g)
     ks = torch.randperm(K, generator=g)[:M]
     x = torch.zeros(M, K, dtype=dtype)
     x[torch.arange(M), ks] = 1.0
     s = (torch.randn(K // G, N, generator=g) * 0.01).to(dtype)
-    z = torch.randint(0, 16, (K // G, N), generator=g).to(dtype)
+    z = torch.randint(0, 16, (K // G, N), generator=g).to(torch.float32)
+    if frac_zeros:
+        z = z + torch.rand(K // G, N, generator=g) * 0.999
+    z = z.to(dtype)
     y = ops.w4a16_gemm(x.to(dev), qw.to(dev), s.to(dev), z.to(dev)).float().cpu().numpy()
     dt = "f16" if dtype == torch.float16 else "bf16"
     W = ow.dequant(qw.numpy(), s.float().numpy(), z.float().numpy(), dt)
