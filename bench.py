@@ -44,10 +44,11 @@ def w4a16_bytes(M, K=K_DIM, N=N_DIM, G=GROUP):
     return K * N // 2 + 2 * (K // G) * N * 2 + 2 * M * K + 2 * M * N
 
 
-# HBM bytes per launch of the W4A16 kernels at the sweep's two regimes, from rocprofv3 PMC runs:
-# FETCH_SIZE scaled by 2.0 (a plain 256 MiB device copy reads as 131084.5 KiB) plus WRITE_SIZE
-# (exact on the same copy). Keyed by M; other M report null.
-W4A16_PMC_TRAFFIC = {16: 39_890_343, 2048: 325_538_042}
+# HBM bytes per kbh_w4a16_gemm call at the sweep's two regimes, from rocprofv3 PMC runs:
+# FETCH_SIZE scaled by 2.0 (a plain 256 MiB device copy reads as 131085.3 KiB) plus WRITE_SIZE
+# (exact on the same copy), summed over the call's launches (GEMM + split-K finalize/reduce).
+# Keyed by M; other M report null.
+W4A16_PMC_TRAFFIC = {16: 39_911_116, 2048: 466_557_595}
 
 
 def gemm_flops(M, N=N_DIM, K=K_DIM):

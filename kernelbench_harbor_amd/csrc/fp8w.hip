@@ -63,14 +63,13 @@ template <int SPW, bool BF16>
 __global__ __launch_bounds__(kSplitKMaxWaves * 64) void fp8w_decode_kernel(
     const uint16_t* __restrict__ x, const uint8_t* __restrict__ w,
     const uint16_t* __restrict__ scales, uint16_t* __restrict__ y, float* __restrict__ acc,
-    int* __restrict__ counters, int M, int N, int K, int block, int splits) {
+    int M, int N, int K, int block, int splits) {
   constexpr int NCS = 8;  // lane column c owns output columns n0 + 8c .. +7
   constexpr int NWG = 128;
   __shared__ SplitKSmem<NCS, float> sm;
   const int waves = blockDim.x >> 6;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int c = lane & 15, g = lane >> 4;
-  const int ntiles = N / NWG;
   const int id = xcd_remap(blockIdx.x, gridDim.x);
   const int tile = id / splits, split = id - tile * splits;
   const int n0 = tile * NWG;
@@ -124,10 +123,9 @@ __global__ __launch_bounds__(kSplitKMaxWaves * 64) void fp8w_decode_kernel(
     }
   }
   const int rows = min(16, M - m0);
-  splitk_finish<NCS, float>(part, sm, acc, &counters[blockIdx.y * ntiles + tile], splits, rows, N,
-                            m0, n0, [&](int r, int n, float v) {
-                              y[(size_t)(m0 + r) * N + n0 + n] = f32_to_half_bits<BF16>(v);
-                            });
+  splitk_reduce<NCS, float>(part, sm, acc, splits, rows, N, m0, n0, [&](int r, int n, float v) {
+    y[(size_t)(m0 + r) * N + n0 + n] = f32_to_half_bits<BF16>(v);
+  });
 }
 
 // Weight-slab producer for tiled_f16_gemm: thread t loads rows 4*(t/32) .. +3 of the slab for
@@ -181,14 +179,16 @@ int fp8w_run(const void* x, const void* w, const void* scales, void* y, void* wo
   if (!waves) return KBH_ERR_SHAPE;
   dim3 grid(ntiles * splits, mblocks);
   float* acc = (float*)workspace;
-  int* counters = splitk_counters(workspace, M, N);
 #define KBH_FP8_DEC(SPW_)                                                                        \
   if (spw == SPW_)                                                                               \
     hipLaunchKernelGGL((fp8w_decode_kernel<SPW_, BF16>), grid, dim3(waves * 64), 0, st,          \
                        (const uint16_t*)x, (const uint8_t*)w, (const uint16_t*)scales,           \
-                       (uint16_t*)y, acc, counters, M, N, K, block, splits);
+                       (uint16_t*)y, acc, M, N, K, block, splits);
   KBH_FP8_DEC(4) else KBH_FP8_DEC(2) else KBH_FP8_DEC(1)
 #undef KBH_FP8_DEC
+  if (splits > 1)
+    hipLaunchKernelGGL((splitk_finalize_half<BF16>), dim3(splitk_finalize_blocks(M, N)), dim3(256),
+                       0, st, acc, (uint16_t*)y, (size_t)M * N / 4);
   return launch_status();
 }
 

@@ -2,16 +2,16 @@
 //
 // Every decode kernel leaves each wavefront with a 16-row x (16*NCS)-column partial tile in the
 // 16x16 MFMA accumulator layout: lane l holds, for column set cs < NCS, rows 4*(l/16)+i (i < 4)
-// of output column n0 + (l%16)*NCS + cs. splitk_finish() sums the waves of the workgroup through
-// private LDS slices (no LDS atomics: waves adding into one slice serialise), then sums the
-// K-split workgroups of the tile:
+// of output column n0 + (l%16)*NCS + cs. splitk_reduce() sums the waves of the workgroup through
+// private LDS slices (one 16-byte write per column set and lane; the reads of the summing pass
+// are 16-byte and bank-conflict free; lanes whose rows are all beyond M skip the write), then:
 //  * splits == 1: the workgroup emits its tile directly;
-//  * otherwise each workgroup adds its tile into the workspace with agent-scope atomics, waits
-//    until its atomics are acknowledged (s_waitcnt 0), and counts its arrival on the tile's
-//    counter; the workgroup that arrives last reads the complete sums with agent-scope atomic
-//    loads, emits them and clears the workspace tile and the counter for the next call.
-// Agent-scope atomics are performed at the device coherence point, so partial sums from
-// workgroups on different XCDs meet there.
+//  * otherwise it adds its tile into the workspace accumulators with agent-scope atomics
+//    (performed at the device coherence point, so partial sums from workgroups on different
+//    XCDs meet there) and ends. A finalize kernel launched after it on the same stream applies
+//    the epilogue to the sums and clears the accumulators, so the workspace is zero again for
+//    the next call. (An in-kernel last-arriver protocol costs three serialised memory round
+//    trips, far more than the second launch.)
 #pragma once
 
 #include "kbh_common.h"
@@ -23,71 +23,68 @@ constexpr int kSplitKCsStride = 260;  // LDS elements per column set per wave (4
 
 template <int NCS, typename T>
 struct SplitKSmem {
-  T red[kSplitKMaxWaves * NCS * kSplitKCsStride];
-  int last;
+  __attribute__((aligned(16))) T red[kSplitKMaxWaves * NCS * kSplitKCsStride];
 };
 
-// emit(r, n, v): row r (< rows) of the tile, column n (< 16*NCS), reduced value v.
+// V is the 4-element vector of T held per column set (kbh_f32x4 / kbh_i32x4).
+// emit(r, n, v): row r (< rows) of the tile, column n (< 16*NCS), reduced value v (splits == 1).
 template <int NCS, typename T, typename V, typename Emit>
-__device__ inline void splitk_finish(const V (&tot)[NCS], SplitKSmem<NCS, T>& sm, T* acc,
-                                     int* counter, int splits, int rows, int ld, int m0, int n0,
-                                     Emit emit) {
-  constexpr int NWG = 16 * NCS;
+__device__ inline void splitk_reduce(const V (&tot)[NCS], SplitKSmem<NCS, T>& sm, T* acc,
+                                     int splits, int rows, int ld, int m0, int n0, Emit emit) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, waves = blockDim.x >> 6;
-  {
+  if (4 * (lane >> 4) < rows) {
     T* slice = sm.red + wave * NCS * kSplitKCsStride;
 #pragma unroll
     for (int cs = 0; cs < NCS; ++cs)
+      *reinterpret_cast<V*>(&slice[cs * kSplitKCsStride + lane * 4]) = tot[cs];
+  }
+  __syncthreads();
+  // Position p = (lane l, column set cs), cs fastest: consecutive threads read consecutive
+  // 16-byte chunks (the slice stride is 16 bytes mod 256) and own consecutive output columns.
+  const int npos = NCS * 16 * ((rows + 3) >> 2);
+  for (int p = threadIdx.x; p < npos; p += blockDim.x) {
+    const int cs = p % NCS, l = p / NCS;
+    const T* src = &sm.red[cs * kSplitKCsStride + l * 4];
+    V v = *reinterpret_cast<const V*>(src);
+    for (int wv = 1; wv < waves; ++wv)
+      v += *reinterpret_cast<const V*>(src + wv * NCS * kSplitKCsStride);
+    const int n = (l & 15) * NCS + cs;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) slice[cs * kSplitKCsStride + i * 64 + lane] = tot[cs][i];
-  }
-  __syncthreads();
-  auto lds_sum = [&](int r, int n) {
-    const int cc = n / NCS, cs = n - cc * NCS;
-    const int off = cs * kSplitKCsStride + (r & 3) * 64 + (r >> 2) * 16 + cc;
-    T v = 0;
-    for (int wv = 0; wv < waves; ++wv) v += sm.red[wv * NCS * kSplitKCsStride + off];
-    return v;
-  };
-  if (splits == 1) {
-    for (int e = threadIdx.x; e < rows * NWG; e += blockDim.x) {
-      const int r = e / NWG, n = e - r * NWG;
-      emit(r, n, lds_sum(r, n));
+    for (int i = 0; i < 4; ++i) {
+      const int r = 4 * (l >> 4) + i;
+      if (r >= rows) continue;
+      if (splits == 1)
+        emit(r, n, v[i]);
+      else
+        __hip_atomic_fetch_add(&acc[(size_t)(m0 + r) * ld + n0 + n], v[i], __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
     }
-    return;
   }
-  for (int e = threadIdx.x; e < rows * NWG; e += blockDim.x) {
-    const int r = e / NWG, n = e - r * NWG;
-    __hip_atomic_fetch_add(&acc[(size_t)(m0 + r) * ld + n0 + n], lds_sum(r, n), __ATOMIC_RELAXED,
-                           __HIP_MEMORY_SCOPE_AGENT);
-  }
-  __builtin_amdgcn_s_waitcnt(0);
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    const int prev = __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    sm.last = (prev == splits - 1);
-  }
-  __syncthreads();
-  if (!sm.last) return;
-  for (int e = threadIdx.x; e < rows * NWG; e += blockDim.x) {
-    const int r = e / NWG, n = e - r * NWG;
-    T* p = &acc[(size_t)(m0 + r) * ld + n0 + n];
-    const T v = __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    __hip_atomic_store(p, (T)0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    emit(r, n, v);
-  }
-  if (threadIdx.x == 0) __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// Workspace layout of a split-K call: fp32/int32 accumulators [M, N], then one arrival counter
-// per (16-row block, 128-column tile).
+// Converts the fp32 split-K sums acc[M*N] to fp16/bf16 y and clears them. n4 = M*N/4.
+template <bool BF16>
+__global__ __launch_bounds__(256) void splitk_finalize_half(float* __restrict__ acc,
+                                                            uint16_t* __restrict__ y, size_t n4) {
+  const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= n4) return;
+  kbh_f32x4* p = reinterpret_cast<kbh_f32x4*>(acc) + i;
+  const kbh_f32x4 v = *p;
+  *p = kbh_f32x4{0.f, 0.f, 0.f, 0.f};
+  kbh_u32x2 o;
+  o[0] = (uint32_t)f32_to_half_bits<BF16>(v[0]) | ((uint32_t)f32_to_half_bits<BF16>(v[1]) << 16);
+  o[1] = (uint32_t)f32_to_half_bits<BF16>(v[2]) | ((uint32_t)f32_to_half_bits<BF16>(v[3]) << 16);
+  *reinterpret_cast<kbh_u32x2*>(y + 4 * i) = o;
+}
+
+inline unsigned splitk_finalize_blocks(int M, int N) {
+  return (unsigned)(((size_t)M * N / 4 + 255) / 256);
+}
+
+// Workspace of a split-K call: fp32/int32 accumulators [M, N], zero between calls.
 inline size_t splitk_workspace_bytes(int M, int N) {
   if (M <= 0 || N <= 0) return 0;
-  return round_up((size_t)M * (size_t)N * 4u, 256) +
-         round_up((size_t)((M + 15) / 16) * (size_t)(N / 128 + 1) * 4u, 256);
-}
-inline int* splitk_counters(void* workspace, int M, int N) {
-  return (int*)((char*)workspace + round_up((size_t)M * (size_t)N * 4u, 256));
+  return round_up((size_t)M * (size_t)N * 4u, 256);
 }
 
 // Picks waves per workgroup (<= kSplitKMaxWaves) so that `units` wave-sized K ranges per column

@@ -20,10 +20,9 @@
 //      sum_k x_k (q_k - z) s = s * (sum_k x_k (B + f q_k) / f - (B/f + z) * sum_k x_k)
 //    with sum_k x_k from one extra MFMA against a ones fragment.
 //  * The waves of a workgroup (consecutive K ranges of one column tile) reduce through private
-//    LDS slices; workgroups (K splits) reduce with fp32 atomics into a workspace tile, and the
-//    last workgroup of a tile (per-tile arrival counter) converts it to the output dtype and
-//    clears the workspace. Workgroup ids are remapped so that all K splits of a column tile run
-//    on one XCD.
+//    LDS slices; workgroups (K splits) add their tiles into the workspace with fp32 atomics, and
+//    a finalize kernel converts the sums to the output dtype and clears the workspace
+//    (splitk.h). Workgroup ids are remapped so that all K splits of a column tile run on one XCD.
 //
 // Larger M (M > 32): tiled_wide_gemm (tiled_wide.h) with W4WidePolicy, which dequantizes each
 // packed 32 x TN weight slab once per workgroup into LDS with the exact reference arithmetic
@@ -51,8 +50,8 @@ template <int NW, int SPW, int SPG, bool BF16>
 __global__ __launch_bounds__(kSplitKMaxWaves * 64) void w4a16_decode_kernel(
     const uint16_t* __restrict__ x, const uint32_t* __restrict__ qw,
     const uint16_t* __restrict__ scales, const uint16_t* __restrict__ zeros,
-    uint16_t* __restrict__ y, float* __restrict__ acc, int* __restrict__ counters,
-    int M, int N, int K, int group, int splits) {
+    uint16_t* __restrict__ y, float* __restrict__ acc, int M, int N, int K, int group,
+    int splits) {
   constexpr int NWG = 128 * NW;  // output columns of one workgroup
   constexpr int NCS = 8 * NW;    // MFMA column sets per wave
   constexpr uint32_t MAGIC = BF16 ? kMagicBF16 : kMagicF16;
@@ -63,7 +62,6 @@ __global__ __launch_bounds__(kSplitKMaxWaves * 64) void w4a16_decode_kernel(
   const int wave = threadIdx.x >> 6;
   const int c = lane & 15;
   const int g = lane >> 4;
-  const int ntiles = N / NWG;
   const int id = xcd_remap(blockIdx.x, gridDim.x);
   const int tile = id / splits;
   const int split = id - tile * splits;
@@ -163,10 +161,9 @@ __global__ __launch_bounds__(kSplitKMaxWaves * 64) void w4a16_decode_kernel(
   }
 
   const int rows = min(16, M - m0);
-  splitk_finish<NCS, float>(tot, sm, acc, &counters[blockIdx.y * ntiles + tile], splits, rows, N,
-                            m0, n0, [&](int r, int n, float v) {
-                              y[(size_t)(m0 + r) * N + n0 + n] = f32_to_half_bits<BF16>(v);
-                            });
+  splitk_reduce<NCS, float>(tot, sm, acc, splits, rows, N, m0, n0, [&](int r, int n, float v) {
+    y[(size_t)(m0 + r) * N + n0 + n] = f32_to_half_bits<BF16>(v);
+  });
 }
 
 struct DecodePlan {
@@ -192,21 +189,24 @@ bool plan_decode(int M, int N, int K, int group_steps_, DecodePlan* p) {
 
 template <int NW, int SPW, int SPG, bool BF16>
 void launch_decode(const DecodePlan& p, const void* x, const int32_t* qw, const void* s,
-                   const void* z, void* y, float* acc, int* counters, int M, int N, int K,
-                   int group, hipStream_t stream) {
+                   const void* z, void* y, float* acc, int M, int N, int K, int group,
+                   hipStream_t stream) {
   dim3 grid(p.ntiles * p.splits, p.mblocks);
   hipLaunchKernelGGL((w4a16_decode_kernel<NW, SPW, SPG, BF16>), grid, dim3(p.waves * 64), 0, stream,
                      (const uint16_t*)x, (const uint32_t*)qw, (const uint16_t*)s,
-                     (const uint16_t*)z, (uint16_t*)y, acc, counters, M, N, K, group, p.splits);
+                     (const uint16_t*)z, (uint16_t*)y, acc, M, N, K, group, p.splits);
+  if (p.splits > 1)
+    hipLaunchKernelGGL((splitk_finalize_half<BF16>), dim3(splitk_finalize_blocks(M, N)), dim3(256),
+                       0, stream, acc, (uint16_t*)y, (size_t)M * N / 4);
 }
 
 template <bool BF16>
 void dispatch_decode(const DecodePlan& p, const void* x, const int32_t* qw, const void* s,
-                     const void* z, void* y, float* acc, int* counters, int M, int N, int K,
-                     int group, hipStream_t st) {
+                     const void* z, void* y, float* acc, int M, int N, int K, int group,
+                     hipStream_t st) {
 #define KBH_DEC(NW_, SPW_, SPG_)                                                                 \
   if (p.nw == NW_ && p.spw == SPW_ && p.spg == SPG_)                                             \
-    return launch_decode<NW_, SPW_, SPG_, BF16>(p, x, qw, s, z, y, acc, counters, M, N, K, group, st);
+    return launch_decode<NW_, SPW_, SPG_, BF16>(p, x, qw, s, z, y, acc, M, N, K, group, st);
   KBH_DEC(2, 4, 4) KBH_DEC(2, 4, 2) KBH_DEC(2, 4, 1) KBH_DEC(2, 2, 2) KBH_DEC(2, 2, 1)
   KBH_DEC(2, 1, 1) KBH_DEC(1, 4, 4) KBH_DEC(1, 4, 2) KBH_DEC(1, 4, 1) KBH_DEC(1, 2, 2)
   KBH_DEC(1, 2, 1) KBH_DEC(1, 1, 1)
@@ -333,10 +333,9 @@ extern "C" int kbh_w4a16_gemm(const void* x, const int32_t* qweight, const void*
   const size_t need = kbh_w4a16_workspace_bytes(M, N, K, group);
   if (!workspace || workspace_bytes < need) return KBH_ERR_WORKSPACE;
   float* acc = (float*)workspace;
-  int* counters = splitk_counters(workspace, M, N);
   DecodePlan p;
   if (!plan_decode(M, N, K, group / 32, &p)) return KBH_ERR_SHAPE;
-  if (bf) dispatch_decode<true>(p, x, qweight, scales, zeros, y, acc, counters, M, N, K, group, st);
-  else dispatch_decode<false>(p, x, qweight, scales, zeros, y, acc, counters, M, N, K, group, st);
+  if (bf) dispatch_decode<true>(p, x, qweight, scales, zeros, y, acc, M, N, K, group, st);
+  else dispatch_decode<false>(p, x, qweight, scales, zeros, y, acc, M, N, K, group, st);
   return launch_status();
 }

@@ -56,15 +56,14 @@ __device__ inline uint16_t w8a8_epilogue(int acc, uint16_t xs, uint16_t ws) {
 template <int SPW, bool OUT_I32>
 __global__ __launch_bounds__(kSplitKMaxWaves * 64) void w8a8_decode_kernel(
     const int8_t* __restrict__ x, const int8_t* __restrict__ w, const uint16_t* __restrict__ xs,
-    const uint16_t* __restrict__ wsc, void* __restrict__ out, int* __restrict__ acc,
-    int* __restrict__ counters, int M, int N, int K, int splits) {
+    const uint16_t* __restrict__ wsc, void* __restrict__ out, int* __restrict__ acc, int M, int N,
+    int K, int splits) {
   constexpr int NWG = 128;  // columns per workgroup: 16 lanes x 8 columns
   constexpr int NCS = 8;    // MFMA column sets per wave
   __shared__ SplitKSmem<NCS, int> sm;
   const int waves = blockDim.x >> 6;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int c = lane & 15, g = lane >> 4;
-  const int ntiles = N / NWG;
   const int id = xcd_remap(blockIdx.x, gridDim.x);
   const int tile = id / splits, split = id - tile * splits;
   const int n0 = tile * NWG;
@@ -115,13 +114,37 @@ __global__ __launch_bounds__(kSplitKMaxWaves * 64) void w8a8_decode_kernel(
 
   // Lane column c owns output columns n0 + 8c + cs.
   const int rows = min(16, M - m0);
-  splitk_finish<NCS, int>(accv, sm, acc, &counters[blockIdx.y * ntiles + tile], splits, rows, N, m0,
-                          n0, [&](int r, int n, int v) {
-                            const size_t o = (size_t)(m0 + r) * N + n0 + n;
-                            if constexpr (OUT_I32) reinterpret_cast<int*>(out)[o] = v;
-                            else reinterpret_cast<uint16_t*>(out)[o] =
-                                     w8a8_epilogue(v, xs[m0 + r], wsc[n0 + n]);
-                          });
+  splitk_reduce<NCS, int>(accv, sm, acc, splits, rows, N, m0, n0, [&](int r, int n, int v) {
+    const size_t o = (size_t)(m0 + r) * N + n0 + n;
+    if constexpr (OUT_I32) reinterpret_cast<int*>(out)[o] = v;
+    else reinterpret_cast<uint16_t*>(out)[o] = w8a8_epilogue(v, xs[m0 + r], wsc[n0 + n]);
+  });
+}
+
+// Applies the epilogue to the int32 split-K sums acc[M*N] (exact integers) and clears them: 4
+// consecutive outputs of one row per thread (N % 4 == 0), n4 = M*N/4.
+template <bool OUT_I32>
+__global__ __launch_bounds__(256) void w8a8_finalize(int* __restrict__ acc,
+                                                     const uint16_t* __restrict__ xs,
+                                                     const uint16_t* __restrict__ wsc,
+                                                     void* __restrict__ out, int N, size_t n4) {
+  const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= n4) return;
+  kbh_i32x4* p = reinterpret_cast<kbh_i32x4*>(acc) + i;
+  const kbh_i32x4 v = *p;
+  *p = kbh_i32x4{0, 0, 0, 0};
+  if constexpr (OUT_I32) {
+    reinterpret_cast<kbh_i32x4*>(out)[i] = v;
+  } else {
+    const size_t e = 4 * i;
+    const int r = (int)(e / (size_t)N), n = (int)(e - (size_t)r * N);
+    kbh_u32x2 o;
+    o[0] = (uint32_t)w8a8_epilogue(v[0], xs[r], wsc[n]) |
+           ((uint32_t)w8a8_epilogue(v[1], xs[r], wsc[n + 1]) << 16);
+    o[1] = (uint32_t)w8a8_epilogue(v[2], xs[r], wsc[n + 2]) |
+           ((uint32_t)w8a8_epilogue(v[3], xs[r], wsc[n + 3]) << 16);
+    reinterpret_cast<kbh_u32x2*>(out)[i] = o;
+  }
 }
 
 struct W8Plan {
@@ -274,18 +297,21 @@ int w8a8_run(const void* x, const void* w, const void* xs, const void* wsc, void
   const size_t need = kbh_w8a8_workspace_bytes(M, N, K);
   if (!workspace || workspace_bytes < need) return KBH_ERR_WORKSPACE;
   int* acc = (int*)workspace;
-  int* counters = splitk_counters(workspace, M, N);
   W8Plan p;
   if (!plan_w8_decode(M, N, K, &p)) return KBH_ERR_SHAPE;
   dim3 grid(p.ntiles * p.splits, p.mblocks);
   if (p.spw == 2)
     hipLaunchKernelGGL((w8a8_decode_kernel<2, OUT_I32>), grid, dim3(p.waves * 64), 0, st,
                        (const int8_t*)x, (const int8_t*)w, (const uint16_t*)xs,
-                       (const uint16_t*)wsc, out, acc, counters, M, N, K, p.splits);
+                       (const uint16_t*)wsc, out, acc, M, N, K, p.splits);
   else
     hipLaunchKernelGGL((w8a8_decode_kernel<1, OUT_I32>), grid, dim3(p.waves * 64), 0, st,
                        (const int8_t*)x, (const int8_t*)w, (const uint16_t*)xs,
-                       (const uint16_t*)wsc, out, acc, counters, M, N, K, p.splits);
+                       (const uint16_t*)wsc, out, acc, M, N, K, p.splits);
+  if (p.splits > 1)
+    hipLaunchKernelGGL((w8a8_finalize<OUT_I32>), dim3(splitk_finalize_blocks(M, N)), dim3(256), 0,
+                       st, acc, (const uint16_t*)xs, (const uint16_t*)wsc, out, N,
+                       (size_t)M * N / 4);
   return launch_status();
 }
 
