@@ -98,8 +98,42 @@ def rotation(make, per_set_bytes, limit=32):
     return [base] + [[t.clone() for t in base] for _ in range(R - 1)]
 
 
+def graph_batch(torch, fn, sets, batch, reps=4):
+    """Mean device seconds per call of `batch` calls over rotating input sets, captured in one
+    HIP graph and replayed `reps` times (no host launch overhead, which otherwise dominates
+    kernels of a few microseconds). Every replay's outputs are checked against eager runs of
+    the same calls; returns None when capture is not possible or a replay disagrees."""
+    st = torch.cuda.Stream()
+    st.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(st):
+        ref = [fn(*sets[i % len(sets)]).float() for i in range(batch)]  # also sizes the pools
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    try:
+        with torch.cuda.graph(g, stream=st):
+            outs = [fn(*sets[i % len(sets)]) for i in range(batch)]
+    except RuntimeError:
+        return None
+    times = []
+    for _ in range(reps):
+        a = torch.cuda.Event(enable_timing=True)
+        b = torch.cuda.Event(enable_timing=True)
+        with torch.cuda.stream(st):  # replay() launches on the current stream
+            a.record()
+            g.replay()
+            b.record()
+        b.synchronize()
+        times.append(a.elapsed_time(b) * 1e-3 / batch)
+        for o, r in zip(outs, ref):  # fp32 atomics may reorder sums: tolerance, not bits
+            if float((o.float() - r).abs().max()) > 1e-3 * float(r.abs().max()):
+                return None
+    del g
+    return sorted(times)[len(times) // 2]
+
+
 def time_config(torch, fn, sets, iters, batch):
-    """(per-call event times [s], batched mean [s]) over rotating input sets."""
+    """(per-call event times [s], batched mean [s]) over rotating input sets. The batched time
+    comes from graph_batch, falling back to back-to-back eager calls."""
     for i in range(3):
         fn(*sets[i % len(sets)])
     torch.cuda.synchronize()
@@ -112,6 +146,9 @@ def time_config(torch, fn, sets, iters, batch):
         b.record()
         b.synchronize()
         ts.append(a.elapsed_time(b) * 1e-3)
+    gb = graph_batch(torch, fn, sets, batch)
+    if gb is not None:
+        return sorted(ts), gb
     a = torch.cuda.Event(enable_timing=True)
     b = torch.cuda.Event(enable_timing=True)
     a.record()

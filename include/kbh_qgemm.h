@@ -81,16 +81,19 @@ int kbh_w4a16_gemm(const void* x, const int32_t* qweight, const void* scales, co
  *   y       [M, N] fp16,  y = fp16((fp32(x_int8 @ w_int8) * x_scale[m]) * w_scale[n])
  * The int8 x int8 products are accumulated exactly in int32.
  * Requirements: M >= 1, N % 128 == 0, K % 64 == 0, x/w/y 16-byte aligned.
- * workspace: as for kbh_w4a16_gemm, with kbh_w8a8_workspace_bytes().
+ * workspace / scratch: as for kbh_w4a16_gemm, with kbh_w8a8_workspace_bytes() and
+ * kbh_w8a8_scratch_bytes().
  */
 size_t kbh_w8a8_workspace_bytes(int M, int N, int K);
+size_t kbh_w8a8_scratch_bytes(int M, int N, int K);
 int kbh_w8a8_gemm(const int8_t* x_int8, const int8_t* w_int8, const void* x_scale,
                   const void* w_scale, void* y, void* workspace, size_t workspace_bytes,
-                  int M, int N, int K, void* stream);
+                  void* scratch, size_t scratch_bytes, int M, int N, int K, void* stream);
 /* Same GEMM returning the raw int32 accumulators acc_out [M, N] (no scale epilogue); exposes
  * the integer stage of the reference (reference.py:8) for bit-exact checks. */
 int kbh_w8a8_gemm_i32(const int8_t* x_int8, const int8_t* w_int8, int32_t* acc_out,
-                      void* workspace, size_t workspace_bytes, int M, int N, int K, void* stream);
+                      void* workspace, size_t workspace_bytes, void* scratch,
+                      size_t scratch_bytes, int M, int N, int K, void* stream);
 
 /* ---------------------------------------------------------------------------------------
  * FP8 (e4m3fn) block-scaled weight GEMM.

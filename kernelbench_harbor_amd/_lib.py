@@ -40,8 +40,9 @@ SIGNATURES = {
     "kbh_w4a16_scratch_bytes": (_sz, [_i, _i, _i, _i]),
     "kbh_w4a16_gemm": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _sz, _vp, _sz, _i, _i, _i, _i, _i, _vp]),
     "kbh_w8a8_workspace_bytes": (_sz, [_i, _i, _i]),
-    "kbh_w8a8_gemm": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _sz, _i, _i, _i, _vp]),
-    "kbh_w8a8_gemm_i32": (_i, [_vp, _vp, _vp, _vp, _sz, _i, _i, _i, _vp]),
+    "kbh_w8a8_scratch_bytes": (_sz, [_i, _i, _i]),
+    "kbh_w8a8_gemm": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _sz, _vp, _sz, _i, _i, _i, _vp]),
+    "kbh_w8a8_gemm_i32": (_i, [_vp, _vp, _vp, _vp, _sz, _vp, _sz, _i, _i, _i, _vp]),
     "kbh_fp8w_workspace_bytes": (_sz, [_i, _i, _i, _i]),
     "kbh_fp8w_gemm": (_i, [_vp, _vp, _vp, _vp, _vp, _sz, _i, _i, _i, _i, _i, _vp]),
     "kbh_mxfp8_workspace_bytes": (_sz, [_i, _i, _i]),

@@ -1,7 +1,10 @@
-// Wide-tile fp16/bf16 MFMA GEMM for large M with a pluggable weight-slab producer.
+// Wide-tile MFMA GEMM for large M with a pluggable weight-slab producer and output policy.
 //
-// y[M, N] = x[M, K] @ W[K, N]; x, y fp16 or bf16; W produced 32 K-rows x TN columns at a time by
-// a policy from its packed/quantized storage. One 256-thread workgroup owns a TM x TN output tile
+// y[M, N] = x[M, K] @ W[K, N] with x and W in fp16/bf16 (E = WideHalf) or int8 (E = WideI8);
+// a slab is 64 bytes of K per row (32 fp16 or 64 int8 elements), i.e. two 32x32 MFMA k-steps of
+// 16 bytes per lane, and W is produced one 64-byte x TN slab at a time by a policy from its
+// packed/quantized storage. The output policy (EP) turns fp32 or exact int32 sums into the
+// output format. One 256-thread workgroup owns a TM x TN output tile
 // and one K range (split-K); the tile is sized so that two workgroups fit on a CU (<= 128
 // accumulator and <= 128 other VGPRs per lane), which lets one workgroup's MFMAs run while the
 // other waits on memory or a barrier:
@@ -18,26 +21,67 @@
 //    quantization group into one of two register sets; the loop is unrolled over two groups
 //    (2*SPG slabs, SPG = slabs per group), so the set in use is known at compile time and no
 //    register copies are needed.
-//  * Split-K (splits > 1): partial tiles go to per-split fp32 slices of a workspace (plain
-//    stores), summed in split order by wide_reduce_kernel.
+//  * Split-K (splits > 1): partial tiles go to per-split slices of a workspace (plain stores of
+//    E::Part: fp32, or int32 which sums exactly), summed in split order by wide_reduce_kernel.
 //  * Workgroup ids are remapped so that each XCD runs consecutive tiles of the same rows of x
 //    and K range (its L2 then serves the shared x fragments).
 //
-// Policy interface (BP), for 256 threads and a 32 x TN slab:
+// Output policy (EP): void emit(int r, int n, E::Part v) const; one output element, and
+//   void emit4(int r, int n, vec4 v) const; four consecutive outputs of one row (n % 4 == 0).
+//
+// Policy interface (BP), for 256 threads and a (E::kSlabK) x TN slab:
 //   struct Raw;  struct Grp;                            per-thread slab data / group constants
 //   static constexpr int kTN, kParts;
 //   void load(Raw&, int k0, int n0, int t) const;       issue the slab's global loads
 //   void load_group(Grp&, int k0, int n0, int t) const; constants of the group holding row k0
 //   void store_part(const Raw&, const Grp&, uint8_t* Bs, int t, int p) const;
 //                                                       part p < kParts of the slab into LDS
-//   The LDS byte offset of element (k, n) of the slab is wide_b_offset<kTN>(k, n).
+//   The LDS byte offset of byte kb (= k * element size) of column n of the slab is
+//   wide_b_offset<kTN>(kb, n).
 #pragma once
 
 #include "kbh_common.h"
 
 namespace kbh {
 
-constexpr int WBK = 32;  // K rows per slab
+constexpr int WSLAB_BYTES = 64;  // bytes of K per row per slab
+
+// Element traits: MFMA and accumulator types of the two operand families.
+template <bool BF16>
+struct WideHalf {
+  using Acc = kbh_f32x16;
+  using Part = float;
+  using Part4 = kbh_f32x4;
+  static constexpr int kSlabK = 32;  // K elements per slab
+  __device__ static Acc mma(kbh_u32x4 a, kbh_u32x4 b, Acc c) { return mfma32x32x16<BF16>(a, b, c); }
+};
+struct WideI8 {
+  using Acc = kbh_i32x16;
+  using Part = int;
+  using Part4 = kbh_i32x4;
+  static constexpr int kSlabK = 64;
+  // 32x32x32 int8: lane l holds A[row l%32][k 16(l/32)..+16], B[k 16(l/32)..+16][col l%32].
+  __device__ static Acc mma(kbh_u32x4 a, kbh_u32x4 b, Acc c) {
+    return __builtin_amdgcn_mfma_i32_32x32x32_i8(__builtin_bit_cast(kbh_i32x4, a),
+                                                 __builtin_bit_cast(kbh_i32x4, b), c, 0, 0, 0);
+  }
+};
+
+// fp16/bf16 output of fp32 sums.
+template <bool BF16>
+struct HalfOut {
+  uint16_t* y;
+  int N;
+  __device__ void emit(int r, int n, float v) const {
+    y[(size_t)r * N + n] = f32_to_half_bits<BF16>(v);
+  }
+  __device__ void emit4(int r, int n, kbh_f32x4 v) const {
+    kbh_u32x2 o;
+    o[0] = (uint32_t)f32_to_half_bits<BF16>(v[0]) | ((uint32_t)f32_to_half_bits<BF16>(v[1]) << 16);
+    o[1] = (uint32_t)f32_to_half_bits<BF16>(v[2]) | ((uint32_t)f32_to_half_bits<BF16>(v[3]) << 16);
+    *reinterpret_cast<kbh_u32x2*>(y + (size_t)r * N + n) = o;
+  }
+};
 
 // Column slot within a slab: columns are permuted within groups of 8 (slot = 8q + ((n ^ f(q)) &
 // 7), q = n/8, f(q) = q ^ (q >> 3)) so that producer writes, which step through packed words 8
@@ -46,12 +90,12 @@ __device__ __host__ inline int wide_slot(int n) {
   const int q = n >> 3;
   return (n & ~7) | ((n ^ q ^ (q >> 3)) & 7);
 }
-// Byte offset of W[k, n] (k < 32, n < TN) in a slab buffer: [k16 step][k half][column slot]
-// [8 values]. The 8 consecutive k of one column that a lane feeds to an MFMA are one 16-byte
-// chunk and the 32 lanes of a fragment read 512 contiguous bytes.
+// Byte offset of byte kb (< 64) of the K run of column n (< TN) in a slab buffer: [k-step (32
+// bytes)][lane half (16 bytes)][column slot][16 bytes]. The 16 bytes of one column that a lane
+// feeds to an MFMA are one chunk and the 32 lanes of a fragment read 512 contiguous bytes.
 template <int TN>
-__device__ __host__ inline int wide_b_offset(int k, int n) {
-  return (k >> 4) * (TN * 32) + ((k >> 3) & 1) * (TN * 16) + wide_slot(n) * 16 + (k & 7) * 2;
+__device__ __host__ inline int wide_b_offset(int kb, int n) {
+  return (kb >> 5) * (TN * 32) + ((kb >> 4) & 1) * (TN * 16) + wide_slot(n) * 16 + (kb & 15);
 }
 
 template <int TM, int TN, int WM>
@@ -64,11 +108,13 @@ struct WideShape {
   static constexpr int kMinBlocks = RB * CB <= 8 ? 2 : 1;
 };
 
-template <bool BF16, int TM, int WM, int SPG, class BP>
+template <class E, int TM, int WM, int SPG, class BP, class EP>
 __global__ __launch_bounds__(256, (WideShape<TM, BP::kTN, WM>::kMinBlocks)) void tiled_wide_gemm(
-    const uint16_t* __restrict__ x, BP bp, uint16_t* __restrict__ y, float* __restrict__ ws, int M,
-    int N, int K, int splits, int slabs_per_split) {
+    const void* __restrict__ x, BP bp, EP ep, typename E::Part* __restrict__ ws, int M, int N,
+    int K, int splits, int slabs_per_split) {
   constexpr int TN = BP::kTN;
+  constexpr int SK = E::kSlabK;
+  constexpr int EB = WSLAB_BYTES / SK;  // bytes per element
   using Shape = WideShape<TM, TN, WM>;
   constexpr int RB = Shape::RB, CB = Shape::CB, WN = Shape::WN;
   constexpr int SLAB = TN * 64;  // LDS bytes per slab buffer
@@ -89,56 +135,57 @@ __global__ __launch_bounds__(256, (WideShape<TM, BP::kTN, WM>::kMinBlocks)) void
   const int KT = slabs_per_split;
 
   // A fragments: lane (r = lane%32, g = lane/32) of row block rb holds row
-  // m0 + wm*TM/WM + 32rb + r, k = k0 + 16*step + 8g .. +8.
+  // m0 + wm*TM/WM + 32rb + r, bytes 32*step + 16g .. +16 of the slab's 64-byte K run.
   const int fr = lane & 31, fg = lane >> 5;
-  const uint16_t* xrow[RB];
+  const uint8_t* xrow[RB];
 #pragma unroll
   for (int rb = 0; rb < RB; ++rb) {
     const int r = m0 + wm * (TM / WM) + rb * 32 + fr;
-    xrow[rb] = x + (size_t)(r < M ? r : M - 1) * K + fg * 8;  // rows >= M are never stored
+    // rows >= M are never stored
+    xrow[rb] = (const uint8_t*)x + (size_t)(r < M ? r : M - 1) * K * EB + fg * 16;
   }
   struct AStage {
     kbh_u32x4 a[RB][2];
   };
   auto load_a_step = [&](AStage& st, int kt, int s) {
-    const int k0 = (kt0 + kt) * WBK + 16 * s;
+    const size_t b0 = (size_t)(kt0 + kt) * WSLAB_BYTES + 32 * s;
 #pragma unroll
-    for (int rb = 0; rb < RB; ++rb) st.a[rb][s] = *reinterpret_cast<const kbh_u32x4*>(xrow[rb] + k0);
+    for (int rb = 0; rb < RB; ++rb) st.a[rb][s] = *reinterpret_cast<const kbh_u32x4*>(xrow[rb] + b0);
   };
-  auto load_b = [&](typename BP::Raw& r, int kt) { bp.load(r, (kt0 + kt) * WBK, n0, t); };
-  auto load_g = [&](typename BP::Grp& g, int kt) { bp.load_group(g, (kt0 + kt) * WBK, n0, t); };
+  auto load_b = [&](typename BP::Raw& r, int kt) { bp.load(r, (kt0 + kt) * SK, n0, t); };
+  auto load_g = [&](typename BP::Grp& g, int kt) { bp.load_group(g, (kt0 + kt) * SK, n0, t); };
 
   // B fragment of step s, column block j of this wave: lane (c = lane%32, g) reads column
-  // wn*32CB + 32j + c, k = 16s + 8g .. +8.
+  // wn*32CB + 32j + c, bytes 32s + 16g .. +16.
   int boff[CB];
 #pragma unroll
-  for (int j = 0; j < CB; ++j) boff[j] = wide_b_offset<TN>(8 * fg, wn * 32 * CB + 32 * j + fr);
+  for (int j = 0; j < CB; ++j) boff[j] = wide_b_offset<TN>(16 * fg, wn * 32 * CB + 32 * j + fr);
   auto read_b = [&](kbh_u32x4 (&bf)[CB], int buf, int s) {
 #pragma unroll
     for (int j = 0; j < CB; ++j)
       bf[j] = *reinterpret_cast<const kbh_u32x4*>(&Bs[buf][boff[j] + s * (TN * 32)]);
   };
 
-  kbh_f32x16 acc[RB][CB];
+  typename E::Acc acc[RB][CB];
 #pragma unroll
   for (int i = 0; i < RB; ++i)
 #pragma unroll
     for (int j = 0; j < CB; ++j)
 #pragma unroll
-      for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
+      for (int e = 0; e < 16; ++e) acc[i][j][e] = 0;
 
   auto mma = [&](const AStage& st, int s, const kbh_u32x4 (&bf)[CB]) {
 #pragma unroll
     for (int i = 0; i < RB; ++i)
 #pragma unroll
-      for (int j = 0; j < CB; ++j) acc[i][j] = mfma32x32x16<BF16>(st.a[i][s], bf[j], acc[i][j]);
+      for (int j = 0; j < CB; ++j) acc[i][j] = E::mma(st.a[i][s], bf[j], acc[i][j]);
   };
   // MFMAs q in [lo, hi) of a k16 step (q = CB*i + j).
   auto mma_range = [&](const AStage& st, int s, const kbh_u32x4 (&bf)[CB], int lo, int hi) {
 #pragma unroll
     for (int q = 0; q < RB * CB; ++q)
       if (q >= lo && q < hi)
-        acc[q / CB][q % CB] = mfma32x32x16<BF16>(st.a[q / CB][s], bf[q % CB], acc[q / CB][q % CB]);
+        acc[q / CB][q % CB] = E::mma(st.a[q / CB][s], bf[q % CB], acc[q / CB][q % CB]);
   };
 
   // Prologue: slab 0 in LDS, step-0 fragments of slab 0 in registers, A of slabs 0 and 1, raw
@@ -216,7 +263,7 @@ __global__ __launch_bounds__(256, (WideShape<TM, BP::kTN, WM>::kMinBlocks)) void
 #pragma unroll
         for (int e = 0; e < 16; ++e) {
           const int r = rbase + 32 * i + 8 * (e >> 2) + (e & 3);
-          if (r < M) y[(size_t)r * N + cbase + 32 * j] = f32_to_half_bits<BF16>(acc[i][j][e]);
+          if (r < M) ep.emit(r, cbase + 32 * j, acc[i][j][e]);
         }
     return;
   }
@@ -224,7 +271,7 @@ __global__ __launch_bounds__(256, (WideShape<TM, BP::kTN, WM>::kMinBlocks)) void
   // wide_reduce_kernel sums the slices afterwards. The launch boundary orders the two, so no
   // device-scope fences or atomics are needed (both cost far more here than a second small
   // launch), and the sum order is fixed.
-  float* part = ws + (size_t)split * M * N;
+  typename E::Part* part = ws + (size_t)split * M * N;
 #pragma unroll
   for (int i = 0; i < RB; ++i)
 #pragma unroll
@@ -236,21 +283,20 @@ __global__ __launch_bounds__(256, (WideShape<TM, BP::kTN, WM>::kMinBlocks)) void
       }
 }
 
-// y = sum over splits of ws[split] (in split order), converted to fp16/bf16. One thread per 4
-// consecutive outputs; n4 = M * N / 4.
-template <bool BF16>
-__global__ __launch_bounds__(256) void wide_reduce_kernel(const float* __restrict__ ws,
-                                                          uint16_t* __restrict__ y, size_t n4,
-                                                          int splits) {
+// Output = sum over splits of ws[split] (in split order), through the output policy. One thread
+// per 4 consecutive outputs of a row (N % 4 == 0); n4 = M * N / 4.
+template <class E, class EP>
+__global__ __launch_bounds__(256) void wide_reduce_kernel(const typename E::Part* __restrict__ ws,
+                                                          EP ep, int N, size_t n4, int splits) {
+  using P4 = typename E::Part4;
   const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
   if (i >= n4) return;
-  const kbh_f32x4* p = reinterpret_cast<const kbh_f32x4*>(ws) + i;
-  kbh_f32x4 v = __builtin_nontemporal_load(p);
+  const P4* p = reinterpret_cast<const P4*>(ws) + i;
+  P4 v = __builtin_nontemporal_load(p);
   for (int sp = 1; sp < splits; ++sp) v += __builtin_nontemporal_load(p + sp * n4);
-  kbh_u32x2 o;
-  o[0] = (uint32_t)f32_to_half_bits<BF16>(v[0]) | ((uint32_t)f32_to_half_bits<BF16>(v[1]) << 16);
-  o[1] = (uint32_t)f32_to_half_bits<BF16>(v[2]) | ((uint32_t)f32_to_half_bits<BF16>(v[3]) << 16);
-  *reinterpret_cast<kbh_u32x2*>(y + 4 * i) = o;
+  const size_t e = 4 * i;
+  const int r = (int)(e / (size_t)N);
+  ep.emit4(r, (int)(e - (size_t)r * N), v);
 }
 
 // Launch geometry: tiles ordered (row block, split, column block) so that consecutive ids,
@@ -262,14 +308,16 @@ struct WidePlan {
   int grid;
 };
 
-// Picks the tile height and the split count. `slots` is the number of workgroups the GPU runs
+// Picks the tile height (256 rows, or tm_small up to 128 rows) and the split count. `slots` is
+// the number of workgroups the GPU runs
 // at once (256 CUs x workgroups per CU). A split count is valid when it divides the K slabs into
 // ranges of at least 8 slabs that are a multiple of `unroll`; among those, the plan minimises
 // (waves of workgroups) x (slabs per workgroup), preferring fewer splits on a tie.
-inline bool plan_wide(int M, int N, int K, int tn, int unroll, int slots, WidePlan* p) {
-  if (N % tn != 0 || K % (unroll * WBK) != 0 || M < 1) return false;
-  const int KT = K / WBK;
-  p->tm = M > 128 ? 256 : 128;
+inline bool plan_wide(int M, int N, int K, int tn, int slab_k, int unroll, int slots,
+                      WidePlan* p, int tm_small = 128) {
+  if (N % tn != 0 || K % (unroll * slab_k) != 0 || M < 1) return false;
+  const int KT = K / slab_k;
+  p->tm = M > 128 ? 256 : tm_small;
   const int tiles = ((M + p->tm - 1) / p->tm) * (N / tn);
   long best = -1;
   for (int s = 1; s <= KT / unroll; ++s) {
@@ -288,7 +336,7 @@ inline bool plan_wide(int M, int N, int K, int tn, int unroll, int slots, WidePl
   return true;
 }
 
-// Workspace: `splits` fp32 slices of M x N (none without split-K).
+// Workspace: `splits` slices of M x N 4-byte partial sums (none without split-K).
 inline size_t wide_workspace_bytes(int M, int N, int splits) {
   return splits <= 1 ? 0 : round_up((size_t)splits * M * N * 4u, 256);
 }

@@ -194,8 +194,9 @@ struct W4WidePolicy {
   }
   __device__ void store_part(const Raw& r, const Grp& g, uint8_t* Bs, int t, int p) const {
     const int w = word_of(t), h = rows_of(t);
-    // wide_b_offset<TN>(kRows*h, 8w + c) = base + 16 * (c ^ f(w)).
-    uint8_t* base = Bs + wide_b_offset<TN>(kRows * h, 8 * w) - wide_slot(8 * w) * 16 + w * 128;
+    // Rows kRows*h.. are bytes 2*kRows*h.. of the column's K run:
+    // wide_b_offset<TN>(2 kRows h, 8w + c) = base + 16 * (c ^ f(w)).
+    uint8_t* base = Bs + wide_b_offset<TN>(2 * kRows * h, 8 * w) - wide_slot(8 * w) * 16 + w * 128;
     const int fw = (w ^ (w >> 3)) & 7;
     switch (p) {
       case 0: put<0>(r, g, base, fw); break;

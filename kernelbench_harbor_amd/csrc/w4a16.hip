@@ -230,25 +230,28 @@ struct W4Wide {
 
 bool plan_w4_wide(int M, int N, int K, int group, W4Wide* w) {
   if (M < kWideMinM) return false;
-  w->spg = group / WBK;
+  w->spg = group / 32;
   const bool small = M <= 128;
   w->tn = small ? 128 : 256;
   if (N % w->tn != 0) return false;
-  return plan_wide(M, N, K, w->tn, 2 * w->spg, small ? 512 : 256, &w->plan);
+  return plan_wide(M, N, K, w->tn, 32, 2 * w->spg, small ? 512 : 256, &w->plan);
 }
 
 template <bool BF16, int TM, int TN, int SPG>
 void launch_w4_wide(const W4Wide& w, const void* x, const int32_t* qw, const void* s, const void* z,
                     void* y, float* scratch, int M, int N, int K, int group, hipStream_t st) {
-  const W4WidePolicy<BF16, TN> bp{(const uint32_t*)qw, (const uint16_t*)s, (const uint16_t*)z,
-                                  N, group, 0, 0, 0x000F000Fu};
-  hipLaunchKernelGGL((tiled_wide_gemm<BF16, TM, 4, SPG, W4WidePolicy<BF16, TN>>),
-                     dim3(w.plan.grid), dim3(256), 0, st, (const uint16_t*)x, bp, (uint16_t*)y,
-                     scratch, M, N, K, w.plan.splits, w.plan.slabs_per_split);
+  using E = WideHalf<BF16>;
+  using BP = W4WidePolicy<BF16, TN>;
+  using EP = HalfOut<BF16>;
+  const BP bp{(const uint32_t*)qw, (const uint16_t*)s, (const uint16_t*)z, N, group, 0, 0,
+              0x000F000Fu};
+  const EP ep{(uint16_t*)y, N};
+  hipLaunchKernelGGL((tiled_wide_gemm<E, TM, 4, SPG, BP, EP>), dim3(w.plan.grid), dim3(256), 0, st,
+                     x, bp, ep, scratch, M, N, K, w.plan.splits, w.plan.slabs_per_split);
   if (w.plan.splits > 1) {
     const size_t n4 = (size_t)M * N / 4;
-    hipLaunchKernelGGL((wide_reduce_kernel<BF16>), dim3((unsigned)((n4 + 255) / 256)), dim3(256), 0,
-                       st, scratch, (uint16_t*)y, n4, w.plan.splits);
+    hipLaunchKernelGGL((wide_reduce_kernel<E, EP>), dim3((unsigned)((n4 + 255) / 256)), dim3(256),
+                       0, st, scratch, ep, N, n4, w.plan.splits);
   }
 }
 

@@ -16,6 +16,7 @@
 // slab transposed into LDS k-major per column, 2x2 waves of 128x64 with 32x32x32 int8 MFMAs.
 #include "kbh_common.h"
 #include "splitk.h"
+#include "tiled_wide.h"
 
 namespace kbh {
 namespace {
@@ -284,9 +285,116 @@ __global__ __launch_bounds__(256) void w8a8_tiled_kernel(
 
 constexpr int kW8TiledMinM = 128;
 
+// ======================================================================================
+// Wide-tile kernel (M > 32)
+// ======================================================================================
+
+// int8 weight-slab producer for tiled_wide_gemm: 64 K rows x 256 columns per slab. Thread t owns
+// rows 8rb..8rb+7 of columns 8cb..8cb+7 (rb, cb below): eight 8-byte loads (two rows x 256
+// contiguous bytes per wave instruction), two 4x4 byte transposes per 4-column part, and one
+// 8-byte LDS write per column holding its 8 consecutive K values (bank-conflict free).
+struct W8WidePolicy {
+  static constexpr int kTN = 256;
+  static constexpr int kParts = 2;  // part p: columns 4p..4p+3
+  const int8_t* w;
+  int N;
+  struct Raw {
+    kbh_u32x2 r[8];
+  };
+  struct Grp {};
+  __device__ static int cb_of(int t) { return (t & 7) | (((t >> 4) & 3) << 3); }
+  __device__ static int rb_of(int t) { return ((t >> 3) & 1) | ((t >> 6) << 1); }
+  __device__ void load(Raw& r, int k0, int n0, int t) const {
+    const int8_t* p = w + (size_t)(k0 + 8 * rb_of(t)) * N + n0 + 8 * cb_of(t);
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+      r.r[i] = __builtin_nontemporal_load(reinterpret_cast<const kbh_u32x2*>(p + (size_t)i * N));
+  }
+  __device__ void load_group(Grp&, int, int, int) const {}
+  __device__ void store_part(const Raw& r, const Grp&, uint8_t* Bs, int t, int p) const {
+    const int cb = cb_of(t), rb = rb_of(t);
+    uint32_t lo[4], hi[4], clo[4], chi[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      lo[i] = r.r[i][p];
+      hi[i] = r.r[4 + i][p];
+    }
+    transpose4x4(lo, clo);  // column 4p+j, K bytes 0..3 of the thread's 8
+    transpose4x4(hi, chi);  // K bytes 4..7
+    // wide_b_offset<256>(8rb, 8cb + c) = base + 16 * (c ^ f(cb)).
+    uint8_t* base = Bs + wide_b_offset<256>(8 * rb, 8 * cb) - wide_slot(8 * cb) * 16 + cb * 128;
+    const int fw = (cb ^ (cb >> 3)) & 7;
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      *reinterpret_cast<kbh_u32x2*>(base + (((4 * p + j) ^ fw) << 4)) = kbh_u32x2{clo[j], chi[j]};
+  }
+};
+
+// Output policy: the reference epilogue (fp16) or the raw int32 sums.
+template <bool OUT_I32>
+struct W8Out {
+  void* out;
+  const uint16_t* xs;
+  const uint16_t* wsc;
+  int N;
+  __device__ void emit(int r, int n, int v) const {
+    const size_t o = (size_t)r * N + n;
+    if constexpr (OUT_I32) reinterpret_cast<int*>(out)[o] = v;
+    else reinterpret_cast<uint16_t*>(out)[o] = w8a8_epilogue(v, xs[r], wsc[n]);
+  }
+  __device__ void emit4(int r, int n, kbh_i32x4 v) const {
+    const size_t o = (size_t)r * N + n;
+    if constexpr (OUT_I32) {
+      *reinterpret_cast<kbh_i32x4*>(reinterpret_cast<int*>(out) + o) = v;
+    } else {
+      const uint16_t x = xs[r];
+      kbh_u32x2 h;
+      h[0] = (uint32_t)w8a8_epilogue(v[0], x, wsc[n]) |
+             ((uint32_t)w8a8_epilogue(v[1], x, wsc[n + 1]) << 16);
+      h[1] = (uint32_t)w8a8_epilogue(v[2], x, wsc[n + 2]) |
+             ((uint32_t)w8a8_epilogue(v[3], x, wsc[n + 3]) << 16);
+      *reinterpret_cast<kbh_u32x2*>(reinterpret_cast<uint16_t*>(out) + o) = h;
+    }
+  }
+};
+
+constexpr int kW8WideMinM = 33;
+
+// 256-row tiles at every M: the int8 slab producer holds 8 rows x 8 columns per thread, which
+// does not fit the register budget of two 128-row workgroups per CU.
+bool plan_w8_wide(int M, int N, int K, WidePlan* p) {
+  if (M < kW8WideMinM || N % 256 != 0) return false;
+  return plan_wide(M, N, K, 256, 64, 2, 256, p, 256);
+}
+
+template <bool OUT_I32, int TM>
+void launch_w8_wide(const WidePlan& p, const void* x, const void* w, const void* xs,
+                    const void* wsc, void* out, int* scratch, int M, int N, int K,
+                    hipStream_t st) {
+  using EP = W8Out<OUT_I32>;
+  const W8WidePolicy bp{(const int8_t*)w, N};
+  const EP ep{out, (const uint16_t*)xs, (const uint16_t*)wsc, N};
+  hipLaunchKernelGGL((tiled_wide_gemm<WideI8, TM, 4, 1, W8WidePolicy, EP>), dim3(p.grid),
+                     dim3(256), 0, st, x, bp, ep, scratch, M, N, K, p.splits, p.slabs_per_split);
+  if (p.splits > 1) {
+    const size_t n4 = (size_t)M * N / 4;
+    hipLaunchKernelGGL((wide_reduce_kernel<WideI8, EP>), dim3((unsigned)((n4 + 255) / 256)),
+                       dim3(256), 0, st, scratch, ep, N, n4, p.splits);
+  }
+}
+
 template <bool OUT_I32>
 int w8a8_run(const void* x, const void* w, const void* xs, const void* wsc, void* out,
-             void* workspace, size_t workspace_bytes, int M, int N, int K, hipStream_t st) {
+             void* workspace, size_t workspace_bytes, void* scratch, size_t scratch_bytes, int M,
+             int N, int K, hipStream_t st) {
+  WidePlan wp;
+  if (plan_w8_wide(M, N, K, &wp)) {
+    const size_t need = wide_workspace_bytes(M, N, wp.splits);
+    if (need > 0 && (!scratch || scratch_bytes < need)) return KBH_ERR_WORKSPACE;
+    if (need > 0 && !aligned16(scratch)) return KBH_ERR_ALIGN;
+    launch_w8_wide<OUT_I32, 256>(wp, x, w, xs, wsc, out, (int*)scratch, M, N, K, st);
+    return launch_status();
+  }
   if (M >= kW8TiledMinM && K % (WBK * WDEPTH) == 0) {
     const int tiles = ((M + WBM - 1) / WBM) * (N / WBN);
     hipLaunchKernelGGL(w8a8_tiled_kernel<OUT_I32>, dim3(tiles), dim3(256), 0, st,
@@ -331,21 +439,28 @@ extern "C" size_t kbh_w8a8_workspace_bytes(int M, int N, int K) {
   return kbh::splitk_workspace_bytes(M, N);
 }
 
+extern "C" size_t kbh_w8a8_scratch_bytes(int M, int N, int K) {
+  kbh::WidePlan p;
+  if (M < 1 || N < 128 || K < 64 || !kbh::plan_w8_wide(M, N, K, &p)) return 0;
+  return kbh::wide_workspace_bytes(M, N, p.splits);
+}
+
 extern "C" int kbh_w8a8_gemm(const int8_t* x_int8, const int8_t* w_int8, const void* x_scale,
                              const void* w_scale, void* y, void* workspace, size_t workspace_bytes,
-                             int M, int N, int K, void* stream) {
+                             void* scratch, size_t scratch_bytes, int M, int N, int K,
+                             void* stream) {
   const int st = kbh::w8a8_check(x_int8, w_int8, x_scale, w_scale, y, M, N, K);
   if (st != KBH_OK) return st;
-  return kbh::w8a8_run<false>(x_int8, w_int8, x_scale, w_scale, y, workspace, workspace_bytes, M,
-                              N, K, (hipStream_t)stream);
+  return kbh::w8a8_run<false>(x_int8, w_int8, x_scale, w_scale, y, workspace, workspace_bytes,
+                              scratch, scratch_bytes, M, N, K, (hipStream_t)stream);
 }
 
 extern "C" int kbh_w8a8_gemm_i32(const int8_t* x_int8, const int8_t* w_int8, int32_t* acc_out,
-                                 void* workspace, size_t workspace_bytes, int M, int N, int K,
-                                 void* stream) {
+                                 void* workspace, size_t workspace_bytes, void* scratch,
+                                 size_t scratch_bytes, int M, int N, int K, void* stream) {
   // The scale pointers are not read on this path; pass the inputs to satisfy the NULL checks.
   const int st = kbh::w8a8_check(x_int8, w_int8, x_int8, x_int8, acc_out, M, N, K);
   if (st != KBH_OK) return st;
   return kbh::w8a8_run<true>(x_int8, w_int8, nullptr, nullptr, acc_out, workspace,
-                             workspace_bytes, M, N, K, (hipStream_t)stream);
+                             workspace_bytes, scratch, scratch_bytes, M, N, K, (hipStream_t)stream);
 }

@@ -134,10 +134,11 @@ def w8a8_gemm(x_int8: torch.Tensor, w_int8: torch.Tensor, x_scale: torch.Tensor,
     xs = x_scale.reshape(M).contiguous()
     ws_ = w_scale.reshape(N).contiguous()
     lib = _lib.load()
-    nbytes = lib.kbh_w8a8_workspace_bytes(M, N, K)
-    ws = workspaces.get(nbytes, dev)
+    ws = workspaces.get(lib.kbh_w8a8_workspace_bytes(M, N, K), dev)
+    sc = scratches.get(lib.kbh_w8a8_scratch_bytes(M, N, K), dev)
     st = lib.kbh_w8a8_gemm(x2.data_ptr(), w.data_ptr(), xs.data_ptr(), ws_.data_ptr(),
-                           y.data_ptr(), ws.data_ptr(), ws.numel(), M, N, K, _stream_ptr(dev))
+                           y.data_ptr(), ws.data_ptr(), ws.numel(), sc.data_ptr(), sc.numel(),
+                           M, N, K, _stream_ptr(dev))
     _lib.check(st, "kbh_w8a8_gemm")
     return y.reshape(*lead, N)
 
@@ -152,8 +153,9 @@ def w8a8_gemm_i32(x_int8: torch.Tensor, w_int8: torch.Tensor) -> torch.Tensor:
         return acc
     lib = _lib.load()
     ws = workspaces.get(lib.kbh_w8a8_workspace_bytes(M, N, K), dev)
+    sc = scratches.get(lib.kbh_w8a8_scratch_bytes(M, N, K), dev)
     st = lib.kbh_w8a8_gemm_i32(x2.data_ptr(), w.data_ptr(), acc.data_ptr(), ws.data_ptr(),
-                               ws.numel(), M, N, K, _stream_ptr(dev))
+                               ws.numel(), sc.data_ptr(), sc.numel(), M, N, K, _stream_ptr(dev))
     _lib.check(st, "kbh_w8a8_gemm_i32")
     return acc
 

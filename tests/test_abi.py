@@ -54,8 +54,11 @@ def test_host_checks_run_without_gpu():
     need = lib.kbh_w4a16_scratch_bytes(2048, 4096, 14336, 128)
     assert lib.kbh_w4a16_gemm(p, p, p, p, p, p, 1 << 20, p, need - 1, 2048, 4096, 14336, 128, 0, None) == _lib.KBH_ERR_WORKSPACE
     assert lib.kbh_w4a16_gemm(p, p, p, p, p, p, 1 << 20, None, 0, 2048, 4096, 14336, 128, 0, None) == _lib.KBH_ERR_WORKSPACE
-    assert lib.kbh_w8a8_gemm(p, p, p, p, p, p, 1 << 20, 16, 4096, 100, None) == _lib.KBH_ERR_SHAPE
-    assert lib.kbh_w8a8_gemm(p, p, p, p, p, None, 0, 16, 4096, 4096, None) == _lib.KBH_ERR_WORKSPACE
+    assert lib.kbh_w8a8_gemm(p, p, p, p, p, p, 1 << 20, p, 1 << 20, 16, 4096, 100, None) == _lib.KBH_ERR_SHAPE
+    assert lib.kbh_w8a8_gemm(p, p, p, p, p, None, 0, p, 1 << 20, 16, 4096, 4096, None) == _lib.KBH_ERR_WORKSPACE
+    need = lib.kbh_w8a8_scratch_bytes(512, 4096, 14336)
+    assert need >= 512 * 4096 * 4 * 2
+    assert lib.kbh_w8a8_gemm(p, p, p, p, p, p, 1 << 20, p, need - 1, 512, 4096, 14336, None) == _lib.KBH_ERR_WORKSPACE
 
 
 def test_workspace_sizes():

@@ -22,6 +22,12 @@ CASES = [
     (128, 1024, 256, "reference"),
     (300, 2048, 384, "baseline"),
     (100, 1088, 256, "reference"),   # K % 128 != 0: split-K path at large M
+    # wide-tile int8 kernel (M > 32, N % 256 == 0, K % 128 == 0): with and without split-K,
+    # ragged M, 1-3 row blocks
+    (33, 2048, 256, "baseline"),
+    (257, 1024, 768, "reference"),
+    (512, 4096, 512, "baseline"),
+    (600, 8192, 256, "reference"),
 ]
 
 
@@ -50,7 +56,7 @@ def test_w8a8_full_size(dev, M):
     assert compare(y, want).ok
 
 
-@pytest.mark.parametrize("M", [16, 256])
+@pytest.mark.parametrize("M", [16, 100, 256])
 def test_w8a8_int32_extremes(dev, M):
     """|acc| reaches K*127^2 = 231,225,344 (all +127) and K*128*127 (-128 against +127)."""
     K, N = 14336, 256
