@@ -24,6 +24,7 @@
 //    roundings (each product rounded to dtype, fp32 sum of the two, one rounding).
 #include "kbh_common.h"
 #include "tiled_f16.h"
+#include "tiled_wide.h"
 #include "w4_dequant.h"
 
 namespace kbh {
@@ -317,15 +318,113 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(const uint16_t* __rest
   y[i] = f32_to_half_bits<BF16>(keep_f32(p0 + p1));
 }
 
+// ---- SiLU FFN on the wide-tile kernel -------------------------------------------------------
+
+// Gate and up weights as one virtual TN-column slab: in each 16-word chunk c of the tile, packed
+// words 0..7 come from the gate matrix and words 8..15 from the up matrix, both at real output
+// columns n0/2 + 64c + 8(w % 8) .. +7, so each lane ends with matching gate and up accumulators
+// (virtual columns 128c + v and 128c + 64 + v).
+template <bool BF16, int TN>
+struct W4PairPolicy {
+  using Half = W4WidePolicy<BF16, TN>;
+  static constexpr int kTN = TN;
+  static constexpr int kParts = Half::kParts;
+  using Raw = typename Half::Raw;
+  using Grp = typename Half::Grp;
+  Half g, u;  // N = real output columns (F)
+  __device__ W4PairPolicy at_expert(int e) const {
+    return W4PairPolicy{g.at_expert(e), u.at_expert(e)};
+  }
+  // Word w of the tile: chunk c = w / 16, matrix (w / 8) % 2, real column n0/2 + 64c + 8(w % 8).
+  // Half::load reads word w at column n0' + 8w, so n0' = n0/2 - 64c - 64 * matrix.
+  __device__ static int shift(int w) { return 4 * (w & 16) + 8 * (w & 8); }
+  __device__ void load(Raw& r, int k0, int n0, int t) const {
+    const int w = Half::word_of(t);
+    const Half& m = (w & 8) ? u : g;  // per-lane matrix, uniform instruction
+    m.load(r, k0, n0 / 2 - shift(w), t);
+  }
+  __device__ void load_group(Grp& gr, int k0, int n0, int t) const {
+    const int w = Half::word_of(t);
+    const Half& m = (w & 8) ? u : g;
+    m.load_group(gr, k0, n0 / 2 - shift(w), t);
+  }
+  __device__ void store_part(const Raw& r, const Grp& gr, uint8_t* Bs, int t, int p) const {
+    g.store_part(r, gr, Bs, t, p);  // dequantisation and LDS layout do not depend on the matrix
+  }
+};
+
+// h[slot][n] = dtype(silu(gate) * up) from the paired accumulators (fp32 math, one rounding).
+template <bool BF16>
+struct SiluPairOut {
+  static constexpr bool kPaired = true;
+  uint16_t* h;
+  int ldh;
+  __device__ void emit_pair(int r, int n, float g, float u) const {
+    h[(size_t)r * ldh + n] = f32_to_half_bits<BF16>(keep_f32(silu(g)) * u);
+  }
+};
+
+// Split-K down projection: the partial slices hold rows 2t + k; y[t] combines the two rows
+// after summing the slices in split order and rounding each expert output to dtype, exactly as
+// moe_combine_kernel does with unsplit outputs. One thread per 4 columns of one token.
+template <bool BF16>
+__global__ __launch_bounds__(256) void moe_reduce_combine_kernel(
+    const float* __restrict__ part, int splits, const uint16_t* __restrict__ topw,
+    uint16_t* __restrict__ y, int T, int N) {
+  const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+  const size_t n4 = (size_t)T * N / 4;
+  if (i >= n4) return;
+  const size_t e = 4 * i;
+  const int t = (int)(e / (size_t)N), n = (int)(e - (size_t)t * N);
+  const size_t slice4 = (size_t)2 * T * N / 4;  // one split's slice, in 4-float units
+  const kbh_f32x4* p0 = reinterpret_cast<const kbh_f32x4*>(part + (size_t)(2 * t) * N + n);
+  const kbh_f32x4* p1 = reinterpret_cast<const kbh_f32x4*>(part + (size_t)(2 * t + 1) * N + n);
+  kbh_f32x4 a = __builtin_nontemporal_load(p0), b = __builtin_nontemporal_load(p1);
+  for (int sp = 1; sp < splits; ++sp) {
+    a += __builtin_nontemporal_load(p0 + sp * slice4);
+    b += __builtin_nontemporal_load(p1 + sp * slice4);
+  }
+  const float w0 = half_bits_to_f32<BF16>(topw[2 * t]), w1 = half_bits_to_f32<BF16>(topw[2 * t + 1]);
+  uint16_t r[4];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const float o0 = half_bits_to_f32<BF16>(f32_to_half_bits<BF16>(a[q]));
+    const float o1 = half_bits_to_f32<BF16>(f32_to_half_bits<BF16>(b[q]));
+    const float q0 = half_bits_to_f32<BF16>(f32_to_half_bits<BF16>(keep_f32(o0 * w0)));
+    const float q1 = half_bits_to_f32<BF16>(f32_to_half_bits<BF16>(keep_f32(o1 * w1)));
+    r[q] = f32_to_half_bits<BF16>(keep_f32(q0 + q1));
+  }
+  kbh_u32x2 o;
+  o[0] = (uint32_t)r[0] | ((uint32_t)r[1] << 16);
+  o[1] = (uint32_t)r[2] | ((uint32_t)r[3] << 16);
+  *reinterpret_cast<kbh_u32x2*>(y + e) = o;
+}
+
+// FFN plan: 128 x 256 expert tiles, one workgroup per CU with a 4-slab prefetch ring; gate/up
+// unsplit (about 2T/128 x 2F/256 workgroups), down split over K until the estimated
+// 2T/128 x D/256 tiles fill the CUs.
+constexpr int kFfnPD = 4;
+struct FfnPlan {
+  int spg;
+  WidePlan down;
+};
+bool plan_ffn(int T, int D, int F, int group, FfnPlan* p) {
+  p->spg = group / 32;
+  const int unroll = 2 * p->spg > kFfnPD ? 2 * p->spg : kFfnPD;  // the kernel's slabs per iteration
+  if (F % 128 != 0 || D % 256 != 0 || D % (unroll * 32) != 0 || F % (unroll * 32) != 0) return false;
+  return plan_wide(2 * T, D, F, 256, 32, unroll, 256, &p->down, 128);
+}
+
 // ---- host side ------------------------------------------------------------------------------
 struct MoeLayout {
-  size_t topi, topw, slot_of, perm, tiles, h, o, total;
+  size_t topi, topw, slot_of, perm, tiles, h, o, part, total;
   int bm, max_tiles;
 };
 
-MoeLayout moe_layout(int T, int E, int hidden, int out_cols) {
+// bm: rows per tile-table entry (0: 128 when an expert averages more than 96 rows, else 64).
+MoeLayout moe_layout(int T, int E, int hidden, int out_cols, int bm = 0, size_t part_bytes = 0) {
   MoeLayout L;
-  L.bm = (2 * T) / (E > 0 ? E : 1) > 96 ? 128 : 64;
+  L.bm = bm ? bm : ((2 * T) / (E > 0 ? E : 1) > 96 ? 128 : 64);
   L.max_tiles = (2 * T + L.bm - 1) / L.bm + E;
   size_t o = 0;
   auto take = [&](size_t bytes) {
@@ -340,6 +439,7 @@ MoeLayout moe_layout(int T, int E, int hidden, int out_cols) {
   L.tiles = take((size_t)L.max_tiles * 3 * 4);
   L.h = take((size_t)2 * T * hidden * 2);
   L.o = take((size_t)2 * T * out_cols * 2);
+  L.part = take(part_bytes);
   L.total = o;
   return L;
 }
@@ -378,6 +478,74 @@ void launch_combine(const void* o, const uint16_t* topw, void* y, int T, int N, 
   const size_t n = (size_t)T * N;
   hipLaunchKernelGGL(moe_combine_kernel<BF16>, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st,
                      (const uint16_t*)o, topw, (uint16_t*)y, T, N);
+}
+
+template <bool BF16, int SPG>
+void launch_ffn_wide_spg(const FfnPlan& fp, const MoeLayout& L, const MoeBuffers& mb,
+                         const void* x, const W4WidePolicy<BF16, 256>& gp,
+                         const W4WidePolicy<BF16, 256>& upp, const W4WidePolicy<BF16, 256>& dp,
+                         void* h, void* o, float* part, void* y, int T, int D, int F,
+                         hipStream_t st) {
+  using E = WideHalf<BF16>;
+  // gate/up: rows gathered from x through perm, h written in slot order
+  {
+    using RM = GroupedRows<true, false>;
+    using BP = W4PairPolicy<BF16, 256>;
+    const BP bp{gp, upp};
+    const SiluPairOut<BF16> ep{(uint16_t*)h, F};
+    const int grid = L.max_tiles * (2 * F / 256);
+    hipLaunchKernelGGL((tiled_wide_gemm<E, 128, 4, SPG, BP, SiluPairOut<BF16>, RM, 1, kFfnPD>),
+                       dim3(grid), dim3(256), 0, st, x, bp, ep, (float*)nullptr, 2 * T, 2 * F, D,
+                       1, D / 32, RM{mb.tiles, mb.perm});
+  }
+  // down: h rows in slot order, outputs (or split-K partials) in row 2t + k
+  {
+    using RM = GroupedRows<false, true>;
+    using BP = W4WidePolicy<BF16, 256>;
+    const HalfOut<BF16> ep{(uint16_t*)o, D};
+    const int splits = fp.down.splits;
+    const int grid = L.max_tiles * (D / 256) * splits;
+    hipLaunchKernelGGL((tiled_wide_gemm<E, 128, 4, SPG, BP, HalfOut<BF16>, RM, 1, kFfnPD>),
+                       dim3(grid), dim3(256), 0, st, h, dp, ep, part, 2 * T, D, F, splits,
+                       fp.down.slabs_per_split, RM{mb.tiles, mb.perm});
+    if (splits > 1) {
+      const size_t n4 = (size_t)T * D / 4;
+      hipLaunchKernelGGL((moe_reduce_combine_kernel<BF16>), dim3((unsigned)((n4 + 255) / 256)),
+                         dim3(256), 0, st, part, splits, mb.topw, (uint16_t*)y, T, D);
+    } else {
+      launch_combine<BF16>(o, mb.topw, y, T, D, st);
+    }
+  }
+}
+
+template <bool BF16>
+void launch_ffn_wide(const FfnPlan& fp, const MoeLayout& L, const MoeBuffers& mb, const void* x,
+                     const int32_t* gq_, const void* gs_, const void* gz_, const int32_t* uq_,
+                     const void* us_, const void* uz_, const int32_t* dq_, const void* ds_,
+                     const void* dz_, void* h, void* o, float* part, void* y, int T, int D, int F,
+                     int group, size_t gq, size_t gs, size_t dq, size_t ds, hipStream_t st) {
+  const W4WidePolicy<BF16, 256> gp{(const uint32_t*)gq_, (const uint16_t*)gs_,
+                                   (const uint16_t*)gz_, F, group, gq, gs, 0x000F000Fu};
+  const W4WidePolicy<BF16, 256> upp{(const uint32_t*)uq_, (const uint16_t*)us_,
+                                    (const uint16_t*)uz_, F, group, gq, gs, 0x000F000Fu};
+  const W4WidePolicy<BF16, 256> dp{(const uint32_t*)dq_, (const uint16_t*)ds_,
+                                   (const uint16_t*)dz_, D, group, dq, ds, 0x000F000Fu};
+  switch (fp.spg) {
+    case 1: return launch_ffn_wide_spg<BF16, 1>(fp, L, mb, x, gp, upp, dp, h, o, part, y, T, D, F, st);
+    case 2: return launch_ffn_wide_spg<BF16, 2>(fp, L, mb, x, gp, upp, dp, h, o, part, y, T, D, F, st);
+    case 4: return launch_ffn_wide_spg<BF16, 4>(fp, L, mb, x, gp, upp, dp, h, o, part, y, T, D, F, st);
+    default: return launch_ffn_wide_spg<BF16, 8>(fp, L, mb, x, gp, upp, dp, h, o, part, y, T, D, F, st);
+  }
+}
+
+// FFN layout: 128-row tiles and room for the down projection's split-K partials when the wide
+// path applies (plan_ffn); otherwise the 256 x 128 grouped kernels run.
+MoeLayout ffn_layout(int T, int E, int D, int F, int group, bool* wide, FfnPlan* fp) {
+  *wide = (group == 32 || group == 64 || group == 128 || group == 256) &&
+          plan_ffn(T, D, F, group, fp);
+  if (!*wide) return moe_layout(T, E, F, D);
+  const size_t part = fp->down.splits > 1 ? (size_t)fp->down.splits * 2 * T * D * 4 : 0;
+  return moe_layout(T, E, F, D, 128, part);
 }
 
 bool moe_shape_ok(int T, int E, int K, int N, int group) {
@@ -443,7 +611,16 @@ extern "C" int kbh_qmoe(const void* x, const int8_t* qweight, const void* scales
 
 extern "C" size_t kbh_qmoe_ffn_workspace_bytes(int T, int D, int F, int E) {
   if (T <= 0 || E <= 0) return 0;
-  return kbh::moe_layout(T, E, F, D).total;
+  // The group size is not an argument here: size for the largest layout over the allowed
+  // groups (the split count of the down projection, hence its partials, depends on it).
+  size_t best = 0;
+  for (int group : {32, 64, 128, 256}) {
+    bool wide;
+    kbh::FfnPlan fp;
+    const size_t b = kbh::ffn_layout(T, E, D, F, group, &wide, &fp).total;
+    best = b > best ? b : best;
+  }
+  return best;
 }
 
 extern "C" int kbh_qmoe_ffn(const void* x, const void* router_logits, int logits_dtype,
@@ -465,7 +642,9 @@ extern "C" int kbh_qmoe_ffn(const void* x, const void* router_logits, int logits
                         down_qweight, down_scales, down_zeros, y};
   for (const void* p : ptrs)
     if (!aligned16(p)) return KBH_ERR_ALIGN;
-  const MoeLayout L = moe_layout(T, E, F, D);
+  bool wide;
+  FfnPlan fp;
+  const MoeLayout L = ffn_layout(T, E, D, F, group, &wide, &fp);
   if (workspace_bytes < L.total) return KBH_ERR_WORKSPACE;
   const MoeBuffers mb = moe_buffers(workspace, L);
   hipStream_t st = (hipStream_t)stream;
@@ -476,6 +655,18 @@ extern "C" int kbh_qmoe_ffn(const void* x, const void* router_logits, int logits
   // gate/up: [D -> F] packed along F; down: [F -> D] packed along D
   const size_t gq = (size_t)D * (F / 8), gs = (size_t)(D / group) * F;
   const size_t dq = (size_t)F * (D / 8), ds = (size_t)(F / group) * D;
+  if (wide) {
+    float* part = (float*)((char*)workspace + L.part);
+    if (bf)
+      launch_ffn_wide<true>(fp, L, mb, x, gate_qweight, gate_scales, gate_zeros, up_qweight,
+                            up_scales, up_zeros, down_qweight, down_scales, down_zeros, h, o, part,
+                            y, T, D, F, group, gq, gs, dq, ds, st);
+    else
+      launch_ffn_wide<false>(fp, L, mb, x, gate_qweight, gate_scales, gate_zeros, up_qweight,
+                             up_scales, up_zeros, down_qweight, down_scales, down_zeros, h, o,
+                             part, y, T, D, F, group, gq, gs, dq, ds, st);
+    return launch_status();
+  }
 #define KBH_FFN(BF)                                                                              \
   {                                                                                              \
     const W4SlabPolicy<BF> gp{(const uint32_t*)gate_qweight, (const uint16_t*)gate_scales,       \

@@ -28,6 +28,14 @@
 //
 // Output policy (EP): void emit(int r, int n, E::Part v) const; one output element, and
 //   void emit4(int r, int n, vec4 v) const; four consecutive outputs of one row (n % 4 == 0).
+//   A paired policy (EP::kPaired, one wave column) instead receives emit_pair(r, n, a, b): each
+//   128 virtual columns 128c.. of the tile hold 64 columns of a first matrix, then the same 64
+//   columns of a second one (a paired weight policy fills them), and virtual columns
+//   128c + v, 128c + 64 + v (v < 64) become output column n = n0/2 + 64c + v.
+//
+// Row map (RM): tile(mb) -> {first row, rows, expert}; a_row(tile, r) the x row feeding tile row
+//   r; out_row(tile, r) the output row of tile row r. DenseRows is the plain GEMM; GroupedRows
+//   walks an expert tile table (mixture of experts). A tile with rows == 0 does nothing.
 //
 // Policy interface (BP), for 256 threads and a (E::kSlabK) x TN slab:
 //   struct Raw;  struct Grp;                            per-thread slab data / group constants
@@ -70,6 +78,7 @@ struct WideI8 {
 // fp16/bf16 output of fp32 sums.
 template <bool BF16>
 struct HalfOut {
+  static constexpr bool kPaired = false;
   uint16_t* y;
   int N;
   __device__ void emit(int r, int n, float v) const {
@@ -98,6 +107,39 @@ __device__ __host__ inline int wide_b_offset(int kb, int n) {
   return (kb >> 5) * (TN * 32) + ((kb >> 4) & 1) * (TN * 16) + wide_slot(n) * 16 + (kb & 15);
 }
 
+struct DenseRows {
+  int M;
+  struct Tile {
+    int m0, rows, expert;
+  };
+  __device__ Tile tile(int mb, int TM) const { return Tile{mb * TM, min(TM, M - mb * TM), 0}; }
+  __device__ int a_row(const Tile& ti, int r) const { return ti.m0 + min(r, ti.rows - 1); }
+  __device__ int out_row(const Tile& ti, int r) const { return ti.m0 + r; }
+};
+
+// Tile mb of the table {expert, first slot, rows}; slot s reads x row perm[s] >> 1 (GATHER) or
+// row s, and writes output row perm[s] (PERM_OUT) or row s.
+template <bool GATHER, bool PERM_OUT>
+struct GroupedRows {
+  const int* tiles;
+  const int* perm;
+  struct Tile {
+    int s0, rows, expert;
+  };
+  __device__ Tile tile(int mb, int) const {
+    const int* p = tiles + 3 * mb;
+    return Tile{p[1], p[2], p[0]};
+  }
+  __device__ int a_row(const Tile& ti, int r) const {
+    const int s = ti.s0 + min(r, ti.rows - 1);
+    return GATHER ? (perm[s] >> 1) : s;
+  }
+  __device__ int out_row(const Tile& ti, int r) const {
+    const int s = ti.s0 + r;
+    return PERM_OUT ? perm[s] : s;
+  }
+};
+
 template <int TM, int TN, int WM>
 struct WideShape {
   static constexpr int WN = 4 / WM;
@@ -108,17 +150,26 @@ struct WideShape {
   static constexpr int kMinBlocks = RB * CB <= 8 ? 2 : 1;
 };
 
-template <class E, int TM, int WM, int SPG, class BP, class EP>
-__global__ __launch_bounds__(256, (WideShape<TM, BP::kTN, WM>::kMinBlocks)) void tiled_wide_gemm(
+// M: output rows (the size of a split-K slice); N: output columns of the weight producer (TN
+// per tile; paired producers: twice the real output columns).
+// MINB: workgroups per CU the register allocation must allow (0: the shape's default).
+// PD: prefetch depth in slabs. x fragments and raw weights are requested PD slabs before their
+//   use; loads complete in issue order, so PD is the latency budget of the whole stream.
+template <class E, int TM, int WM, int SPG, class BP, class EP, class RM = DenseRows, int MINB = 0,
+          int PD = 2>
+__global__ __launch_bounds__(256, (MINB ? MINB : WideShape<TM, BP::kTN, WM>::kMinBlocks)) void
+tiled_wide_gemm(
     const void* __restrict__ x, BP bp, EP ep, typename E::Part* __restrict__ ws, int M, int N,
-    int K, int splits, int slabs_per_split) {
+    int K, int splits, int slabs_per_split, RM rm) {
   constexpr int TN = BP::kTN;
   constexpr int SK = E::kSlabK;
   constexpr int EB = WSLAB_BYTES / SK;  // bytes per element
   using Shape = WideShape<TM, TN, WM>;
   constexpr int RB = Shape::RB, CB = Shape::CB, WN = Shape::WN;
   constexpr int SLAB = TN * 64;  // LDS bytes per slab buffer
-  constexpr int U = 2 * SPG;  // slabs per loop iteration (two groups)
+  // Slabs per loop iteration: two groups, and a multiple of the prefetch ring.
+  constexpr int U = 2 * SPG > PD ? 2 * SPG : PD;
+  static_assert(U % PD == 0 && U % (2 * SPG) == 0, "prefetch depth and group parity");
   __shared__ __attribute__((aligned(16))) uint8_t Bs[2][SLAB];
 
   const int t = threadIdx.x;
@@ -130,19 +181,21 @@ __global__ __launch_bounds__(256, (WideShape<TM, BP::kTN, WM>::kMinBlocks)) void
   const int rest = id / NB;
   const int split = rest % splits;
   const int mb = rest / splits;
-  const int m0 = mb * TM, n0 = nb * TN;
+  const int n0 = nb * TN;
   const int kt0 = split * slabs_per_split;
   const int KT = slabs_per_split;
+  const typename RM::Tile ti = rm.tile(mb, TM);
+  if (ti.rows <= 0) return;  // unused tile-table entry (uniform across the workgroup)
+  bp = bp.at_expert(ti.expert);
 
-  // A fragments: lane (r = lane%32, g = lane/32) of row block rb holds row
-  // m0 + wm*TM/WM + 32rb + r, bytes 32*step + 16g .. +16 of the slab's 64-byte K run.
+  // A fragments: lane (r = lane%32, g = lane/32) of row block rb holds tile row
+  // wm*TM/WM + 32rb + r, bytes 32*step + 16g .. +16 of the slab's 64-byte K run.
   const int fr = lane & 31, fg = lane >> 5;
   const uint8_t* xrow[RB];
 #pragma unroll
   for (int rb = 0; rb < RB; ++rb) {
-    const int r = m0 + wm * (TM / WM) + rb * 32 + fr;
-    // rows >= M are never stored
-    xrow[rb] = (const uint8_t*)x + (size_t)(r < M ? r : M - 1) * K * EB + fg * 16;
+    const int r = wm * (TM / WM) + rb * 32 + fr;  // rows past the tile re-read its last row
+    xrow[rb] = (const uint8_t*)x + (size_t)rm.a_row(ti, r) * K * EB + fg * 16;
   }
   struct AStage {
     kbh_u32x4 a[RB][2];
@@ -188,23 +241,23 @@ __global__ __launch_bounds__(256, (WideShape<TM, BP::kTN, WM>::kMinBlocks)) void
         acc[q / CB][q % CB] = E::mma(st.a[q / CB][s], bf[q % CB], acc[q / CB][q % CB]);
   };
 
-  // Prologue: slab 0 in LDS, step-0 fragments of slab 0 in registers, A of slabs 0 and 1, raw
-  // weights of slabs 1 and 2 and the constants of the second group in flight.
-  AStage A[2];
-  typename BP::Raw R[2];
+  // Prologue: slab 0 in LDS, step-0 fragments of slab 0 in registers, A of slabs 0..PD-1, raw
+  // weights of slabs 1..PD and the constants of the second group in flight. Ring slot s % PD
+  // holds the A fragments of slab s and the raw weights of slab s (consumed during slab s - 1).
+  AStage A[PD];
+  typename BP::Raw R[PD];
   typename BP::Grp G[2];  // constants of groups with even / odd index within the K range
   const int last = KT - 1;
   load_b(R[0], 0);
   load_g(G[0], 0);
 #pragma unroll
-  for (int st = 0; st < 2; ++st) {
-    load_a_step(A[0], 0, st);
-    load_a_step(A[1], min(1, last), st);
-  }
+  for (int i = 0; i < PD; ++i)
+#pragma unroll
+    for (int st = 0; st < 2; ++st) load_a_step(A[i], min(i, last), st);
 #pragma unroll
   for (int p = 0; p < BP::kParts; ++p) bp.store_part(R[0], G[0], Bs[0], t, p);
-  load_b(R[1], min(1, last));
-  load_b(R[0], min(2, last));
+#pragma unroll
+  for (int i = 1; i <= PD; ++i) load_b(R[i % PD], min(i, last));
   load_g(G[1], min(SPG, last));
   __syncthreads();
   kbh_u32x4 b0[CB], b1[CB];
@@ -223,25 +276,26 @@ __global__ __launch_bounds__(256, (WideShape<TM, BP::kTN, WM>::kMinBlocks)) void
     for (int u = 0; u < U; ++u) {
       const int s = kt + u;  // slab in registers / LDS buffer u&1
       const int cur = u & 1;
+      const int ra = u % PD, rr = (u + 1) % PD;  // ring slots of slab s (A) and s+1 (raw)
       const bool new_group = (u + 1) % SPG == 0;  // slab s+1 starts a group
       const int gsel = ((u + 1) / SPG) & 1;
       read_b(b1, cur, 1);
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int p = 0; p < NP; ++p) {
-        mma_range(A[cur], 0, b0, p * NMF / NP, (p + 1) * NMF / NP);
+        mma_range(A[ra], 0, b0, p * NMF / NP, (p + 1) * NMF / NP);
         __builtin_amdgcn_sched_barrier(0);
-        bp.store_part(R[1 - cur], G[gsel], Bs[1 - cur], t, p);  // slab s+1 (after last: unused)
+        bp.store_part(R[rr], G[gsel], Bs[1 - cur], t, p);  // slab s+1 (after last: unused)
         __builtin_amdgcn_sched_barrier(0);
       }
       __syncthreads();  // s_barrier alone does not stop MFMAs moving across: fenced both sides
       __builtin_amdgcn_sched_barrier(0);
       read_b(b0, 1 - cur, 0);  // step 0 of slab s+1
-      mma(A[cur], 1, b1);
-      load_a_step(A[cur], min(s + 2, last), 0);
-      load_b(R[1 - cur], min(s + 3, last));
+      mma(A[ra], 1, b1);
+      load_a_step(A[ra], min(s + PD, last), 0);
+      load_b(R[rr], min(s + 1 + PD, last));
       if (new_group) load_g(G[gsel ^ 1], min(s + 1 + SPG, last));
-      load_a_step(A[cur], min(s + 2, last), 1);
+      load_a_step(A[ra], min(s + PD, last), 1);
       __builtin_amdgcn_sched_group_barrier(0x100, CB, 1);
 #pragma unroll
       for (int i = 0; i < NMF; ++i) {
@@ -253,8 +307,25 @@ __global__ __launch_bounds__(256, (WideShape<TM, BP::kTN, WM>::kMinBlocks)) void
   }
 
   // Accumulator element e of tile (i, j): row 8(e/4) + 4(lane/32) + e%4, column lane%32.
-  const int rbase = m0 + wm * (TM / WM) + 4 * fg;
+  const int rbase = wm * (TM / WM) + 4 * fg;
   const int cbase = n0 + wn * 32 * CB + fr;
+  if constexpr (EP::kPaired) {
+    static_assert(WN == 1 && CB % 4 == 0, "paired output needs whole 128-column chunks per wave");
+#pragma unroll
+    for (int i = 0; i < RB; ++i)
+#pragma unroll
+      for (int j = 0; j < CB; ++j) {
+        if ((j & 3) >= 2) continue;  // second-matrix blocks pair with block j - 2
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+          const int r = rbase + 32 * i + 8 * (e >> 2) + (e & 3);
+          if (r < ti.rows)
+            ep.emit_pair(rm.out_row(ti, r), n0 / 2 + 64 * (j >> 2) + 32 * (j & 1) + fr,
+                         acc[i][j][e], acc[i][j + 2][e]);
+        }
+      }
+    return;
+  } else {
   if (splits == 1) {
 #pragma unroll
     for (int i = 0; i < RB; ++i)
@@ -263,7 +334,7 @@ __global__ __launch_bounds__(256, (WideShape<TM, BP::kTN, WM>::kMinBlocks)) void
 #pragma unroll
         for (int e = 0; e < 16; ++e) {
           const int r = rbase + 32 * i + 8 * (e >> 2) + (e & 3);
-          if (r < M) ep.emit(r, cbase + 32 * j, acc[i][j][e]);
+          if (r < ti.rows) ep.emit(rm.out_row(ti, r), cbase + 32 * j, acc[i][j][e]);
         }
     return;
   }
@@ -279,8 +350,9 @@ __global__ __launch_bounds__(256, (WideShape<TM, BP::kTN, WM>::kMinBlocks)) void
 #pragma unroll
       for (int e = 0; e < 16; ++e) {
         const int r = rbase + 32 * i + 8 * (e >> 2) + (e & 3);
-        if (r < M) part[(size_t)r * N + cbase + 32 * j] = acc[i][j][e];
+        if (r < ti.rows) part[(size_t)rm.out_row(ti, r) * N + cbase + 32 * j] = acc[i][j][e];
       }
+  }
 }
 
 // Output = sum over splits of ws[split] (in split order), through the output policy. One thread

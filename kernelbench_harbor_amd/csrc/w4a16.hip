@@ -217,8 +217,10 @@ void dispatch_decode(const DecodePlan& p, const void* x, const int32_t* qw, cons
 // Large-M kernels
 // ======================================================================================
 // Above kWideMinM rows the wide-tile kernel (tiled_wide.h) takes over from the split-K decode
-// kernel: 128 x 128 tiles (two workgroups per CU) up to 128 rows, 256 x 256 tiles above. The
-// older 256 x 128 LDS-staged kernel remains for shapes the wide kernel does not cover.
+// kernel: up to 128 rows, 128 x 256 tiles with one workgroup per CU (128 x 128 tiles, two per
+// CU, when N is not a multiple of 256); 256 x 256 tiles above. The 256-column tiles run with a
+// 4-slab prefetch ring. The older 256 x 128 LDS-staged kernel remains for shapes the wide kernel
+// does not cover.
 constexpr int kWideMinM = 33;
 constexpr int kTiledMinM = 128;
 
@@ -228,13 +230,18 @@ struct W4Wide {
   int spg;  // K slabs (32 rows) per quantization group
 };
 
+// Prefetch depth of a wide W4 launch with tn-column tiles.
+constexpr int w4_wide_pd(int tn) { return tn == 256 ? 4 : 2; }
+
 bool plan_w4_wide(int M, int N, int K, int group, W4Wide* w) {
   if (M < kWideMinM) return false;
   w->spg = group / 32;
   const bool small = M <= 128;
-  w->tn = small ? 128 : 256;
-  if (N % w->tn != 0) return false;
-  return plan_wide(M, N, K, w->tn, 32, 2 * w->spg, small ? 512 : 256, &w->plan);
+  w->tn = (N % 256 == 0) ? 256 : 128;
+  if (!small && w->tn != 256) return false;
+  const int pd = w4_wide_pd(w->tn);
+  const int unroll = 2 * w->spg > pd ? 2 * w->spg : pd;  // the kernel's slabs per iteration
+  return plan_wide(M, N, K, w->tn, 32, unroll, w->tn == 128 ? 512 : 256, &w->plan);
 }
 
 template <bool BF16, int TM, int TN, int SPG>
@@ -243,11 +250,14 @@ void launch_w4_wide(const W4Wide& w, const void* x, const int32_t* qw, const voi
   using E = WideHalf<BF16>;
   using BP = W4WidePolicy<BF16, TN>;
   using EP = HalfOut<BF16>;
+  constexpr int MINB = (TM == 128 && TN == 256) ? 1 : 0;
   const BP bp{(const uint32_t*)qw, (const uint16_t*)s, (const uint16_t*)z, N, group, 0, 0,
               0x000F000Fu};
   const EP ep{(uint16_t*)y, N};
-  hipLaunchKernelGGL((tiled_wide_gemm<E, TM, 4, SPG, BP, EP>), dim3(w.plan.grid), dim3(256), 0, st,
-                     x, bp, ep, scratch, M, N, K, w.plan.splits, w.plan.slabs_per_split);
+  hipLaunchKernelGGL((tiled_wide_gemm<E, TM, 4, SPG, BP, EP, DenseRows, MINB, w4_wide_pd(TN)>),
+                     dim3(w.plan.grid), dim3(256), 0, st,
+                     x, bp, ep, scratch, M, N, K, w.plan.splits, w.plan.slabs_per_split,
+                     DenseRows{M});
   if (w.plan.splits > 1) {
     const size_t n4 = (size_t)M * N / 4;
     hipLaunchKernelGGL((wide_reduce_kernel<E, EP>), dim3((unsigned)((n4 + 255) / 256)), dim3(256),
@@ -271,10 +281,12 @@ template <bool BF16>
 void dispatch_w4_wide(const W4Wide& w, const void* x, const int32_t* qw, const void* s,
                       const void* z, void* y, float* scratch, int M, int N, int K, int group,
                       hipStream_t st) {
-  if (w.tn == 128)
-    dispatch_w4_wide_spg<BF16, 128, 128>(w, x, qw, s, z, y, scratch, M, N, K, group, st);
-  else
+  if (w.plan.tm == 256)
     dispatch_w4_wide_spg<BF16, 256, 256>(w, x, qw, s, z, y, scratch, M, N, K, group, st);
+  else if (w.tn == 256)
+    dispatch_w4_wide_spg<BF16, 128, 256>(w, x, qw, s, z, y, scratch, M, N, K, group, st);
+  else
+    dispatch_w4_wide_spg<BF16, 128, 128>(w, x, qw, s, z, y, scratch, M, N, K, group, st);
 }
 
 }  // namespace

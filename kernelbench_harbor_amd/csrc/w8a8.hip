@@ -302,6 +302,7 @@ struct W8WidePolicy {
     kbh_u32x2 r[8];
   };
   struct Grp {};
+  __device__ W8WidePolicy at_expert(int) const { return *this; }
   __device__ static int cb_of(int t) { return (t & 7) | (((t >> 4) & 3) << 3); }
   __device__ static int rb_of(int t) { return ((t >> 3) & 1) | ((t >> 6) << 1); }
   __device__ void load(Raw& r, int k0, int n0, int t) const {
@@ -333,6 +334,7 @@ struct W8WidePolicy {
 // Output policy: the reference epilogue (fp16) or the raw int32 sums.
 template <bool OUT_I32>
 struct W8Out {
+  static constexpr bool kPaired = false;
   void* out;
   const uint16_t* xs;
   const uint16_t* wsc;
@@ -362,20 +364,25 @@ constexpr int kW8WideMinM = 33;
 
 // 256-row tiles at every M: the int8 slab producer holds 8 rows x 8 columns per thread, which
 // does not fit the register budget of two 128-row workgroups per CU.
+// Prefetch depth 4 (four 64-deep slabs in flight) when the K slabs come in multiples of 4.
+int w8_wide_pd(int K) { return (K / 64) % 4 == 0 ? 4 : 2; }
+
 bool plan_w8_wide(int M, int N, int K, WidePlan* p) {
   if (M < kW8WideMinM || N % 256 != 0) return false;
-  return plan_wide(M, N, K, 256, 64, 2, 256, p, 256);
+  return plan_wide(M, N, K, 256, 64, w8_wide_pd(K), 256, p, 256);
 }
 
-template <bool OUT_I32, int TM>
+template <bool OUT_I32, int TM, int PD>
 void launch_w8_wide(const WidePlan& p, const void* x, const void* w, const void* xs,
                     const void* wsc, void* out, int* scratch, int M, int N, int K,
                     hipStream_t st) {
   using EP = W8Out<OUT_I32>;
   const W8WidePolicy bp{(const int8_t*)w, N};
   const EP ep{out, (const uint16_t*)xs, (const uint16_t*)wsc, N};
-  hipLaunchKernelGGL((tiled_wide_gemm<WideI8, TM, 4, 1, W8WidePolicy, EP>), dim3(p.grid),
-                     dim3(256), 0, st, x, bp, ep, scratch, M, N, K, p.splits, p.slabs_per_split);
+  hipLaunchKernelGGL((tiled_wide_gemm<WideI8, TM, 4, 1, W8WidePolicy, EP, DenseRows, 0, PD>),
+                     dim3(p.grid),
+                     dim3(256), 0, st, x, bp, ep, scratch, M, N, K, p.splits, p.slabs_per_split,
+                     DenseRows{M});
   if (p.splits > 1) {
     const size_t n4 = (size_t)M * N / 4;
     hipLaunchKernelGGL((wide_reduce_kernel<WideI8, EP>), dim3((unsigned)((n4 + 255) / 256)),
@@ -392,7 +399,10 @@ int w8a8_run(const void* x, const void* w, const void* xs, const void* wsc, void
     const size_t need = wide_workspace_bytes(M, N, wp.splits);
     if (need > 0 && (!scratch || scratch_bytes < need)) return KBH_ERR_WORKSPACE;
     if (need > 0 && !aligned16(scratch)) return KBH_ERR_ALIGN;
-    launch_w8_wide<OUT_I32, 256>(wp, x, w, xs, wsc, out, (int*)scratch, M, N, K, st);
+    if (w8_wide_pd(K) == 4)
+      launch_w8_wide<OUT_I32, 256, 4>(wp, x, w, xs, wsc, out, (int*)scratch, M, N, K, st);
+    else
+      launch_w8_wide<OUT_I32, 256, 2>(wp, x, w, xs, wsc, out, (int*)scratch, M, N, K, st);
     return launch_status();
   }
   if (M >= kW8TiledMinM && K % (WBK * WDEPTH) == 0) {
