@@ -57,9 +57,11 @@ int kbh_last_hip_error(void);
  *
  * Requirements: M >= 1, N % 128 == 0, group in {32, 64, 128, 256}, K % group == 0,
  * x/qweight/scales/zeros/y 16-byte aligned.
- * workspace: >= kbh_w4a16_workspace_bytes(M, N, K, group) bytes, zero-filled before its first
- * use; every call leaves it zero-filled again. Calls that share a workspace must be ordered
- * (same stream); concurrent calls on one workspace race.
+ * workspace: >= kbh_w4a16_workspace_bytes(M, N, K, group) bytes (may be 0, then NULL is
+ * accepted) of device memory with no content requirement: the split-K partial sums of the
+ * small-M kernel, one slice per K split, added in split order by a second kernel on the same
+ * stream (results are identical from call to call). Calls that share a workspace must be
+ * ordered (same stream); concurrent calls on one workspace race.
  * scratch: >= kbh_w4a16_scratch_bytes(M, N, K, group) bytes (may be 0, then NULL is accepted)
  * of device memory with no content requirement (split-K partial sums of the large-M kernel);
  * it must not overlap the workspace, and calls that share it must be ordered like workspace.
@@ -123,7 +125,7 @@ int kbh_fp8w_gemm(const void* x, const uint8_t* w_fp8, const void* scales, void*
  *   b [N, K] e4m3fn codes, b_scale [N, K/32] e8m0 codes
  *   y [M, N] out_dtype,  y[m, n] = sum_k a[m,k] 2^(a_scale[m,k/32]-127) b[n,k] 2^(b_scale[n,k/32]-127)
  * Requirements: M >= 1, N % 64 == 0, K % 256 == 0, a/b/y 16-byte and scales 4-byte aligned.
- * workspace: used when K is split across workgroups (small M); same contract as
+ * workspace: used when K is split across workgroups (small M); same contract as for
  * kbh_w4a16_gemm, size from kbh_mxfp8_workspace_bytes().
  */
 size_t kbh_mxfp8_workspace_bytes(int M, int N, int K);
@@ -152,7 +154,7 @@ int kbh_mxfp8_gemm(const uint8_t* a, const uint8_t* a_scale, const uint8_t* b,
  *   down qweight [E, F, D/8] int32, scales/zeros [E, F/group, D];
  *   h = dtype(silu(x @ Wg) * (x @ Wu)), o = dtype(h @ Wd), y[t] = sum_k dtype(o_k * w[t, k]).
  * Requirements: E in [2, 256]; D, N, F multiples of 128; group in {32, 64, 128, 256}.
- * workspace: no zero-fill needed; sizes from the *_workspace_bytes functions.
+ * workspace: no content requirement; sizes from the *_workspace_bytes functions.
  */
 size_t kbh_qmoe_workspace_bytes(int T, int D, int N, int E);
 int kbh_moe_route_top2(const void* router_logits, int logits_dtype, int32_t* topi, void* topw,

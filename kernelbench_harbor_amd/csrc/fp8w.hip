@@ -123,7 +123,7 @@ __global__ __launch_bounds__(kSplitKMaxWaves * 64) void fp8w_decode_kernel(
     }
   }
   const int rows = min(16, M - m0);
-  splitk_reduce<NCS, float>(part, sm, acc, splits, rows, N, m0, n0, [&](int r, int n, float v) {
+  splitk_reduce<NCS, float>(part, sm, acc, split, splits, rows, M, N, m0, n0, [&](int r, int n, float v) {
     y[(size_t)(m0 + r) * N + n0 + n] = f32_to_half_bits<BF16>(v);
   });
 }
@@ -161,6 +161,22 @@ struct FP8SlabPolicy {
 
 constexpr int kFp8TiledMinM = 128;
 
+struct Fp8Plan {
+  int spw, waves, ntiles, mblocks, splits;
+};
+
+// 4-step (128-deep) wave K ranges when they divide K, waves per workgroup and K splits as for the
+// W4 decode kernel.
+bool plan_fp8_decode(int M, int N, int K, Fp8Plan* p) {
+  const int nsteps = K / 32;
+  p->spw = (nsteps % 4 == 0) ? 4 : (nsteps % 2 == 0 ? 2 : 1);
+  p->ntiles = N / 128;
+  p->mblocks = (M + 15) / 16;
+  p->splits = 0;
+  p->waves = splitk_pick_waves(nsteps / p->spw, p->ntiles * p->mblocks, &p->splits);
+  return p->waves > 0;
+}
+
 template <bool BF16>
 int fp8w_run(const void* x, const void* w, const void* scales, void* y, void* workspace,
              size_t workspace_bytes, int M, int N, int K, int block, hipStream_t st) {
@@ -170,14 +186,13 @@ int fp8w_run(const void* x, const void* w, const void* scales, void* y, void* wo
                        dim3(256), 0, st, (const uint16_t*)x, bp, (uint16_t*)y, M, N, K);
     return launch_status();
   }
-  if (!workspace || workspace_bytes < splitk_workspace_bytes(M, N)) return KBH_ERR_WORKSPACE;
-  const int nsteps = K / 32;
-  const int spw = (nsteps % 4 == 0) ? 4 : (nsteps % 2 == 0 ? 2 : 1);
-  const int ntiles = N / 128, mblocks = (M + 15) / 16;
-  int splits = 0;
-  const int waves = splitk_pick_waves(nsteps / spw, ntiles * mblocks, &splits);
-  if (!waves) return KBH_ERR_SHAPE;
-  dim3 grid(ntiles * splits, mblocks);
+  Fp8Plan pl;
+  if (!plan_fp8_decode(M, N, K, &pl)) return KBH_ERR_SHAPE;
+  const int spw = pl.spw, waves = pl.waves, splits = pl.splits;
+  const size_t need = splitk_workspace_bytes(M, N, splits);
+  if (need > 0 && (!workspace || workspace_bytes < need)) return KBH_ERR_WORKSPACE;
+  if (need > 0 && !aligned16(workspace)) return KBH_ERR_ALIGN;
+  dim3 grid(pl.ntiles * splits, pl.mblocks);
   float* acc = (float*)workspace;
 #define KBH_FP8_DEC(SPW_)                                                                        \
   if (spw == SPW_)                                                                               \
@@ -187,8 +202,8 @@ int fp8w_run(const void* x, const void* w, const void* scales, void* y, void* wo
   KBH_FP8_DEC(4) else KBH_FP8_DEC(2) else KBH_FP8_DEC(1)
 #undef KBH_FP8_DEC
   if (splits > 1)
-    hipLaunchKernelGGL((splitk_finalize_half<BF16>), dim3(splitk_finalize_blocks(M, N)), dim3(256),
-                       0, st, acc, (uint16_t*)y, (size_t)M * N / 4);
+    hipLaunchKernelGGL((splitk_sum_half<BF16>), dim3(splitk_sum_blocks(M, N)), dim3(256), 0, st,
+                       acc, (uint16_t*)y, (size_t)M * N / 4, splits);
   return launch_status();
 }
 
@@ -196,9 +211,10 @@ int fp8w_run(const void* x, const void* w, const void* scales, void* y, void* wo
 }  // namespace kbh
 
 extern "C" size_t kbh_fp8w_workspace_bytes(int M, int N, int K, int block) {
-  (void)K;
   (void)block;
-  return kbh::splitk_workspace_bytes(M, N);
+  kbh::Fp8Plan p;
+  if (M < 1 || N < 128 || K < 32 || !kbh::plan_fp8_decode(M, N, K, &p)) return 0;
+  return kbh::splitk_workspace_bytes(M, N, p.splits);
 }
 
 extern "C" int kbh_fp8w_gemm(const void* x, const uint8_t* w_fp8, const void* scales, void* y,

@@ -94,4 +94,27 @@ __device__ inline uint16_t f32_to_half_bits(float f) {
   if constexpr (BF16) return f32_to_bf16_bits(f); else return f32_to_f16_bits(f);
 }
 
+// p[0] + p[stride] + ... + p[(n-1)*stride], added in slice order (n >= 1). The slices were just
+// written by another kernel, so every load is a full memory round trip: the loads of up to 16
+// slices are issued together before their adds.
+template <int C, class V>
+__device__ inline void sum_chunk(V& v, const V* p, size_t stride, int s) {
+  V t[C];
+#pragma unroll
+  for (int j = 0; j < C; ++j) t[j] = __builtin_nontemporal_load(p + (size_t)(s + j) * stride);
+#pragma unroll
+  for (int j = 0; j < C; ++j) v += t[j];
+}
+template <class V>
+__device__ inline V sum_slices(const V* p, size_t stride, int n) {
+  V v = __builtin_nontemporal_load(p);
+  int s = 1;
+  for (; s + 16 <= n; s += 16) sum_chunk<16>(v, p, stride, s);
+  if (s + 8 <= n) { sum_chunk<8>(v, p, stride, s); s += 8; }
+  if (s + 4 <= n) { sum_chunk<4>(v, p, stride, s); s += 4; }
+  if (s + 2 <= n) { sum_chunk<2>(v, p, stride, s); s += 2; }
+  if (s < n) v += __builtin_nontemporal_load(p + (size_t)s * stride);
+  return v;
+}
+
 }  // namespace kbh

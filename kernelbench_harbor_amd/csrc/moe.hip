@@ -379,11 +379,7 @@ __global__ __launch_bounds__(256) void moe_reduce_combine_kernel(
   const size_t slice4 = (size_t)2 * T * N / 4;  // one split's slice, in 4-float units
   const kbh_f32x4* p0 = reinterpret_cast<const kbh_f32x4*>(part + (size_t)(2 * t) * N + n);
   const kbh_f32x4* p1 = reinterpret_cast<const kbh_f32x4*>(part + (size_t)(2 * t + 1) * N + n);
-  kbh_f32x4 a = __builtin_nontemporal_load(p0), b = __builtin_nontemporal_load(p1);
-  for (int sp = 1; sp < splits; ++sp) {
-    a += __builtin_nontemporal_load(p0 + sp * slice4);
-    b += __builtin_nontemporal_load(p1 + sp * slice4);
-  }
+  const kbh_f32x4 a = sum_slices(p0, slice4, splits), b = sum_slices(p1, slice4, splits);
   const float w0 = half_bits_to_f32<BF16>(topw[2 * t]), w1 = half_bits_to_f32<BF16>(topw[2 * t + 1]);
   uint16_t r[4];
 #pragma unroll

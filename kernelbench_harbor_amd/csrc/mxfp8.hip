@@ -14,9 +14,10 @@
 // Kernel: 256 threads (2x2 waves), tile 128 x (64*WNT), K in 128-deep slabs (4 scale blocks)
 // held in a two-slab register ring, two LDS buffers with 144-byte rows (conflict-free 16-byte
 // fragment reads). Each wave computes 64 x (32*WNT) with 2 x WNT MFMA tiles. For small M the K
-// range is split over gridDim.z; partial tiles are summed with fp32 atomics into a workspace and
-// the last workgroup of a tile converts (the arrival protocol of splitk.h).
+// range is split over gridDim.z; each split stores its partial tile into its own fp32 workspace
+// slice and splitk_sum_half (splitk.h) adds the slices in split order and converts.
 #include "kbh_common.h"
+#include "splitk.h"
 
 namespace kbh {
 namespace {
@@ -38,12 +39,11 @@ __device__ inline kbh_f32x16 mfma_mx32(kbh_u32x4 a0, kbh_u32x4 a1, kbh_u32x4 b0,
 template <int WNT, bool BF16>
 __global__ __launch_bounds__(256) void mxfp8_kernel(
     const uint8_t* __restrict__ a, const uint8_t* __restrict__ as, const uint8_t* __restrict__ b,
-    const uint8_t* __restrict__ bs, uint16_t* __restrict__ y, float* __restrict__ acc,
-    int* __restrict__ counters, int M, int N, int K, int slabs_per_split) {
+    const uint8_t* __restrict__ bs, uint16_t* __restrict__ y, float* __restrict__ acc, int M,
+    int N, int K, int slabs_per_split) {
   constexpr int XBN = 64 * WNT;
   __shared__ __attribute__((aligned(16))) uint8_t Al[2][XBM * XLD];
   __shared__ __attribute__((aligned(16))) uint8_t Bl[2][XBN * XLD];
-  __shared__ int s_last;
 
   const int t = threadIdx.x;
   const int lane = t & 63, wave = t >> 6;
@@ -186,24 +186,8 @@ __global__ __launch_bounds__(256) void mxfp8_kernel(
     for_each([&](int i, int j, int e, size_t o) { y[o] = f32_to_half_bits<BF16>(accv[i][j][e]); });
     return;
   }
-  for_each([&](int i, int j, int e, size_t o) {
-    __hip_atomic_fetch_add(&acc[o], accv[i][j][e], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  });
-  __builtin_amdgcn_s_waitcnt(0);
-  __syncthreads();
-  int* counter = &counters[id];
-  if (t == 0) {
-    const int prev = __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    s_last = (prev == splits - 1);
-  }
-  __syncthreads();
-  if (!s_last) return;
-  for_each([&](int, int, int, size_t o) {
-    const float v = __hip_atomic_load(&acc[o], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    __hip_atomic_store(&acc[o], 0.f, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    y[o] = f32_to_half_bits<BF16>(v);
-  });
-  if (t == 0) __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  float* slice = acc + (size_t)split * M * N;
+  for_each([&](int i, int j, int e, size_t o) { slice[o] = accv[i][j][e]; });
 }
 
 struct MXPlan {
@@ -229,16 +213,19 @@ MXPlan plan_mx(int M, int N, int K) {
 
 template <bool BF16>
 int mx_launch(const MXPlan& p, const void* a, const void* as, const void* b, const void* bs,
-              void* y, float* acc, int* counters, int M, int N, int K, hipStream_t st) {
+              void* y, float* acc, int M, int N, int K, hipStream_t st) {
   const dim3 grid(p.tiles, 1, p.splits);
   if (p.wnt == 4)
     hipLaunchKernelGGL((mxfp8_kernel<4, BF16>), grid, dim3(256), 0, st, (const uint8_t*)a,
                        (const uint8_t*)as, (const uint8_t*)b, (const uint8_t*)bs, (uint16_t*)y,
-                       acc, counters, M, N, K, p.slabs_per_split);
+                       acc, M, N, K, p.slabs_per_split);
   else
     hipLaunchKernelGGL((mxfp8_kernel<1, BF16>), grid, dim3(256), 0, st, (const uint8_t*)a,
                        (const uint8_t*)as, (const uint8_t*)b, (const uint8_t*)bs, (uint16_t*)y,
-                       acc, counters, M, N, K, p.slabs_per_split);
+                       acc, M, N, K, p.slabs_per_split);
+  if (p.splits > 1)
+    hipLaunchKernelGGL((splitk_sum_half<BF16>), dim3(splitk_sum_blocks(M, N)), dim3(256), 0, st,
+                       acc, (uint16_t*)y, (size_t)M * N / 4, p.splits);
   return launch_status();
 }
 
@@ -247,9 +234,9 @@ int mx_launch(const MXPlan& p, const void* a, const void* as, const void* b, con
 
 extern "C" size_t kbh_mxfp8_workspace_bytes(int M, int N, int K) {
   using namespace kbh;
-  if (M <= 0 || N <= 0) return 0;
-  const MXPlan p = plan_mx(M, N, K > 0 ? K : XBK);
-  return round_up((size_t)M * (size_t)N * 4u, 256) + round_up((size_t)p.tiles * 4u, 256);
+  if (M <= 0 || N < 64 || K < XBK) return 0;
+  const MXPlan p = plan_mx(M, N, K);
+  return splitk_workspace_bytes(M, N, p.splits);
 }
 
 extern "C" int kbh_mxfp8_gemm(const uint8_t* a, const uint8_t* a_scale, const uint8_t* b,
@@ -266,13 +253,13 @@ extern "C" int kbh_mxfp8_gemm(const uint8_t* a, const uint8_t* a_scale, const ui
     return KBH_ERR_ALIGN;
   const MXPlan p = plan_mx(M, N, K);
   float* acc = nullptr;
-  int* counters = nullptr;
   if (p.splits > 1) {
-    if (!workspace || workspace_bytes < kbh_mxfp8_workspace_bytes(M, N, K)) return KBH_ERR_WORKSPACE;
+    if (!workspace || workspace_bytes < splitk_workspace_bytes(M, N, p.splits))
+      return KBH_ERR_WORKSPACE;
+    if (!aligned16(workspace)) return KBH_ERR_ALIGN;
     acc = (float*)workspace;
-    counters = (int*)((char*)workspace + round_up((size_t)M * (size_t)N * 4u, 256));
   }
   hipStream_t st = (hipStream_t)stream;
-  if (out_dtype == KBH_BF16) return mx_launch<true>(p, a, a_scale, b, b_scale, y, acc, counters, M, N, K, st);
-  return mx_launch<false>(p, a, a_scale, b, b_scale, y, acc, counters, M, N, K, st);
+  if (out_dtype == KBH_BF16) return mx_launch<true>(p, a, a_scale, b, b_scale, y, acc, M, N, K, st);
+  return mx_launch<false>(p, a, a_scale, b, b_scale, y, acc, M, N, K, st);
 }

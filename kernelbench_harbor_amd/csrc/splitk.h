@@ -6,12 +6,12 @@
 // private LDS slices (one 16-byte write per column set and lane; the reads of the summing pass
 // are 16-byte and bank-conflict free; lanes whose rows are all beyond M skip the write), then:
 //  * splits == 1: the workgroup emits its tile directly;
-//  * otherwise it adds its tile into the workspace accumulators with agent-scope atomics
-//    (performed at the device coherence point, so partial sums from workgroups on different
-//    XCDs meet there) and ends. A finalize kernel launched after it on the same stream applies
-//    the epilogue to the sums and clears the accumulators, so the workspace is zero again for
-//    the next call. (An in-kernel last-arriver protocol costs three serialised memory round
-//    trips, far more than the second launch.)
+//  * otherwise it stores its tile, with plain coalesced stores, into slice `split` of the
+//    workspace (acc[split][M][ld]) and ends. A summing kernel launched after it on the same
+//    stream adds the slices in split order and applies the epilogue, so the result does not
+//    depend on workgroup timing and the workspace needs no clearing. (Device-scope atomics
+//    instead cost several microseconds at 16 rows, and an in-kernel last-arriver protocol three
+//    serialised memory round trips; the launch boundary orders the two kernels for free.)
 #pragma once
 
 #include "kbh_common.h"
@@ -28,9 +28,11 @@ struct SplitKSmem {
 
 // V is the 4-element vector of T held per column set (kbh_f32x4 / kbh_i32x4).
 // emit(r, n, v): row r (< rows) of the tile, column n (< 16*NCS), reduced value v (splits == 1).
+// M: rows of one workspace slice; ld: its row stride (the output's N).
 template <int NCS, typename T, typename V, typename Emit>
 __device__ inline void splitk_reduce(const V (&tot)[NCS], SplitKSmem<NCS, T>& sm, T* acc,
-                                     int splits, int rows, int ld, int m0, int n0, Emit emit) {
+                                     int split, int splits, int rows, int M, int ld, int m0,
+                                     int n0, Emit emit) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, waves = blockDim.x >> 6;
   if (4 * (lane >> 4) < rows) {
     T* slice = sm.red + wave * NCS * kSplitKCsStride;
@@ -56,35 +58,35 @@ __device__ inline void splitk_reduce(const V (&tot)[NCS], SplitKSmem<NCS, T>& sm
       if (splits == 1)
         emit(r, n, v[i]);
       else
-        __hip_atomic_fetch_add(&acc[(size_t)(m0 + r) * ld + n0 + n], v[i], __ATOMIC_RELAXED,
-                               __HIP_MEMORY_SCOPE_AGENT);
+        acc[((size_t)split * M + m0 + r) * ld + n0 + n] = v[i];
     }
   }
 }
 
-// Converts the fp32 split-K sums acc[M*N] to fp16/bf16 y and clears them. n4 = M*N/4.
+// Sums the fp32 split-K slices acc[splits][M*N] in split order and converts the sums to
+// fp16/bf16 y. n4 = M*N/4.
 template <bool BF16>
-__global__ __launch_bounds__(256) void splitk_finalize_half(float* __restrict__ acc,
-                                                            uint16_t* __restrict__ y, size_t n4) {
+__global__ __launch_bounds__(256) void splitk_sum_half(const float* __restrict__ acc,
+                                                       uint16_t* __restrict__ y, size_t n4,
+                                                       int splits) {
   const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
   if (i >= n4) return;
-  kbh_f32x4* p = reinterpret_cast<kbh_f32x4*>(acc) + i;
-  const kbh_f32x4 v = *p;
-  *p = kbh_f32x4{0.f, 0.f, 0.f, 0.f};
+  const kbh_f32x4 v = sum_slices(reinterpret_cast<const kbh_f32x4*>(acc) + i, n4, splits);
   kbh_u32x2 o;
   o[0] = (uint32_t)f32_to_half_bits<BF16>(v[0]) | ((uint32_t)f32_to_half_bits<BF16>(v[1]) << 16);
   o[1] = (uint32_t)f32_to_half_bits<BF16>(v[2]) | ((uint32_t)f32_to_half_bits<BF16>(v[3]) << 16);
   *reinterpret_cast<kbh_u32x2*>(y + 4 * i) = o;
 }
 
-inline unsigned splitk_finalize_blocks(int M, int N) {
+inline unsigned splitk_sum_blocks(int M, int N) {
   return (unsigned)(((size_t)M * N / 4 + 255) / 256);
 }
 
-// Workspace of a split-K call: fp32/int32 accumulators [M, N], zero between calls.
-inline size_t splitk_workspace_bytes(int M, int N) {
-  if (M <= 0 || N <= 0) return 0;
-  return round_up((size_t)M * (size_t)N * 4u, 256);
+// Workspace of a split-K call: `splits` slices of fp32/int32 partial sums [M, N] (none
+// unsplit). No content requirement between calls.
+inline size_t splitk_workspace_bytes(int M, int N, int splits) {
+  if (M <= 0 || N <= 0 || splits <= 1) return 0;
+  return round_up((size_t)splits * M * (size_t)N * 4u, 256);
 }
 
 // Picks waves per workgroup (<= kSplitKMaxWaves) so that `units` wave-sized K ranges per column

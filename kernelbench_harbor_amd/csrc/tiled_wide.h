@@ -363,9 +363,7 @@ __global__ __launch_bounds__(256) void wide_reduce_kernel(const typename E::Part
   using P4 = typename E::Part4;
   const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
   if (i >= n4) return;
-  const P4* p = reinterpret_cast<const P4*>(ws) + i;
-  P4 v = __builtin_nontemporal_load(p);
-  for (int sp = 1; sp < splits; ++sp) v += __builtin_nontemporal_load(p + sp * n4);
+  const P4 v = sum_slices(reinterpret_cast<const P4*>(ws) + i, n4, splits);
   const size_t e = 4 * i;
   const int r = (int)(e / (size_t)N);
   ep.emit4(r, (int)(e - (size_t)r * N), v);

@@ -20,8 +20,8 @@
 //      sum_k x_k (q_k - z) s = s * (sum_k x_k (B + f q_k) / f - (B/f + z) * sum_k x_k)
 //    with sum_k x_k from one extra MFMA against a ones fragment.
 //  * The waves of a workgroup (consecutive K ranges of one column tile) reduce through private
-//    LDS slices; workgroups (K splits) add their tiles into the workspace with fp32 atomics, and
-//    a finalize kernel converts the sums to the output dtype and clears the workspace
+//    LDS slices; each workgroup (K split) stores its tile into its own workspace slice, and
+//    splitk_sum_half adds the slices in split order and converts to the output dtype
 //    (splitk.h). Workgroup ids are remapped so that all K splits of a column tile run on one XCD.
 //
 // Larger M (M > 32): tiled_wide_gemm (tiled_wide.h) with W4WidePolicy, which dequantizes each
@@ -70,24 +70,10 @@ __global__ __launch_bounds__(kSplitKMaxWaves * 64) void w4a16_decode_kernel(
   const int st0 = (split * waves + wave) * SPW;  // first 32-row K step of this wave
   const int NP = N >> 3;
 
-  // ---- every load of this wave, up front -----------------------------------------------
-  uint32_t wd[SPW][8][NW];
+  // ---- every load of this wave, up front ----------------------------------------------
+  // x fragments and group constants first: loads complete in issue order, so the MFMAs of
+  // step u can start as soon as step u's weights arrive, while later steps are still in flight.
   kbh_u32x4 af[SPW];
-  const uint32_t* qb = qw + (size_t)(st0 * 32 + 8 * g) * NP + (n0 >> 3) + c * NW;
-#pragma unroll
-  for (int u = 0; u < SPW; ++u) {
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const uint32_t* p = qb + (size_t)(u * 32 + i) * NP;
-      if constexpr (NW == 2) {
-        const kbh_u32x2 v = __builtin_nontemporal_load(reinterpret_cast<const kbh_u32x2*>(p));
-        wd[u][i][0] = v[0];
-        wd[u][i][1] = v[1];
-      } else {
-        wd[u][i][0] = __builtin_nontemporal_load(p);
-      }
-    }
-  }
   const bool xok = m0 + c < M;
   const uint16_t* xb = x + (size_t)(xok ? m0 + c : 0) * K + st0 * 32 + 8 * g;
 #pragma unroll
@@ -105,6 +91,22 @@ __global__ __launch_bounds__(kSplitKMaxWaves * 64) void w4a16_decode_kernel(
       const size_t off = (size_t)gi * N + n0 + 8 * (c * NW + w);
       sv[gq][w] = *reinterpret_cast<const kbh_u32x4*>(scales + off);
       zv[gq][w] = *reinterpret_cast<const kbh_u32x4*>(zeros + off);
+    }
+  }
+  uint32_t wd[SPW][8][NW];
+  const uint32_t* qb = qw + (size_t)(st0 * 32 + 8 * g) * NP + (n0 >> 3) + c * NW;
+#pragma unroll
+  for (int u = 0; u < SPW; ++u) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const uint32_t* p = qb + (size_t)(u * 32 + i) * NP;
+      if constexpr (NW == 2) {
+        const kbh_u32x2 v = __builtin_nontemporal_load(reinterpret_cast<const kbh_u32x2*>(p));
+        wd[u][i][0] = v[0];
+        wd[u][i][1] = v[1];
+      } else {
+        wd[u][i][0] = __builtin_nontemporal_load(p);
+      }
     }
   }
 
@@ -161,7 +163,7 @@ __global__ __launch_bounds__(kSplitKMaxWaves * 64) void w4a16_decode_kernel(
   }
 
   const int rows = min(16, M - m0);
-  splitk_reduce<NCS, float>(tot, sm, acc, splits, rows, N, m0, n0, [&](int r, int n, float v) {
+  splitk_reduce<NCS, float>(tot, sm, acc, split, splits, rows, M, N, m0, n0, [&](int r, int n, float v) {
     y[(size_t)(m0 + r) * N + n0 + n] = f32_to_half_bits<BF16>(v);
   });
 }
@@ -196,8 +198,8 @@ void launch_decode(const DecodePlan& p, const void* x, const int32_t* qw, const 
                      (const uint16_t*)x, (const uint32_t*)qw, (const uint16_t*)s,
                      (const uint16_t*)z, (uint16_t*)y, acc, M, N, K, group, p.splits);
   if (p.splits > 1)
-    hipLaunchKernelGGL((splitk_finalize_half<BF16>), dim3(splitk_finalize_blocks(M, N)), dim3(256),
-                       0, stream, acc, (uint16_t*)y, (size_t)M * N / 4);
+    hipLaunchKernelGGL((splitk_sum_half<BF16>), dim3(splitk_sum_blocks(M, N)), dim3(256), 0,
+                       stream, acc, (uint16_t*)y, (size_t)M * N / 4, p.splits);
 }
 
 template <bool BF16>
@@ -293,9 +295,10 @@ void dispatch_w4_wide(const W4Wide& w, const void* x, const int32_t* qw, const v
 }  // namespace kbh
 
 extern "C" size_t kbh_w4a16_workspace_bytes(int M, int N, int K, int group) {
-  (void)K;
-  (void)group;
-  return kbh::splitk_workspace_bytes(M, N);
+  kbh::DecodePlan p;
+  if (M < 1 || N < 128 || K < 32 || group < 32 || !kbh::plan_decode(M, N, K, group / 32, &p))
+    return 0;
+  return kbh::splitk_workspace_bytes(M, N, p.splits);
 }
 
 extern "C" size_t kbh_w4a16_scratch_bytes(int M, int N, int K, int group) {
@@ -345,11 +348,12 @@ extern "C" int kbh_w4a16_gemm(const void* x, const int32_t* qweight, const void*
     return launch_status();
   }
 
-  const size_t need = kbh_w4a16_workspace_bytes(M, N, K, group);
-  if (!workspace || workspace_bytes < need) return KBH_ERR_WORKSPACE;
-  float* acc = (float*)workspace;
   DecodePlan p;
   if (!plan_decode(M, N, K, group / 32, &p)) return KBH_ERR_SHAPE;
+  const size_t need = splitk_workspace_bytes(M, N, p.splits);
+  if (need > 0 && (!workspace || workspace_bytes < need)) return KBH_ERR_WORKSPACE;
+  if (need > 0 && !aligned16(workspace)) return KBH_ERR_ALIGN;
+  float* acc = (float*)workspace;
   if (bf) dispatch_decode<true>(p, x, qweight, scales, zeros, y, acc, M, N, K, group, st);
   else dispatch_decode<false>(p, x, qweight, scales, zeros, y, acc, M, N, K, group, st);
   return launch_status();

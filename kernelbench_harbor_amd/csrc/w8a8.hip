@@ -10,10 +10,11 @@
 //
 // w8a8_decode_kernel (small M): a wave owns 128 columns (dwordx2 per lane per row) and SPW steps
 // of 64 k; all loads up front; 16x16x64 int8 MFMAs; int32 partial tiles reduced through private
-// LDS slices, then across K-split workgroups with int32 atomics (exact, order-independent); the
-// last workgroup of a tile applies the epilogue and clears the workspace.
-// w8a8_tiled_kernel (larger M): 256x128 tile, 64-deep K slabs in a register ring, the weight
-// slab transposed into LDS k-major per column, 2x2 waves of 128x64 with 32x32x32 int8 MFMAs.
+// LDS slices, then each K-split workgroup stores its tile into its own workspace slice and
+// w8a8_finalize adds the slices (exact) and applies the epilogue (splitk.h).
+// Larger M: tiled_wide_gemm (tiled_wide.h) with W8WidePolicy; w8a8_tiled_kernel (256x128 tile,
+// 64-deep K slabs in a register ring, the weight slab transposed into LDS k-major per column,
+// 2x2 waves of 128x64 with 32x32x32 int8 MFMAs) for shapes the wide kernel does not cover.
 #include "kbh_common.h"
 #include "splitk.h"
 #include "tiled_wide.h"
@@ -115,25 +116,24 @@ __global__ __launch_bounds__(kSplitKMaxWaves * 64) void w8a8_decode_kernel(
 
   // Lane column c owns output columns n0 + 8c + cs.
   const int rows = min(16, M - m0);
-  splitk_reduce<NCS, int>(accv, sm, acc, splits, rows, N, m0, n0, [&](int r, int n, int v) {
+  splitk_reduce<NCS, int>(accv, sm, acc, split, splits, rows, M, N, m0, n0, [&](int r, int n, int v) {
     const size_t o = (size_t)(m0 + r) * N + n0 + n;
     if constexpr (OUT_I32) reinterpret_cast<int*>(out)[o] = v;
     else reinterpret_cast<uint16_t*>(out)[o] = w8a8_epilogue(v, xs[m0 + r], wsc[n0 + n]);
   });
 }
 
-// Applies the epilogue to the int32 split-K sums acc[M*N] (exact integers) and clears them: 4
+// Sums the int32 split-K slices acc[splits][M*N] (exact integers) and applies the epilogue: 4
 // consecutive outputs of one row per thread (N % 4 == 0), n4 = M*N/4.
 template <bool OUT_I32>
-__global__ __launch_bounds__(256) void w8a8_finalize(int* __restrict__ acc,
+__global__ __launch_bounds__(256) void w8a8_finalize(const int* __restrict__ acc,
                                                      const uint16_t* __restrict__ xs,
                                                      const uint16_t* __restrict__ wsc,
-                                                     void* __restrict__ out, int N, size_t n4) {
+                                                     void* __restrict__ out, int N, size_t n4,
+                                                     int splits) {
   const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
   if (i >= n4) return;
-  kbh_i32x4* p = reinterpret_cast<kbh_i32x4*>(acc) + i;
-  const kbh_i32x4 v = *p;
-  *p = kbh_i32x4{0, 0, 0, 0};
+  const kbh_i32x4 v = sum_slices(reinterpret_cast<const kbh_i32x4*>(acc) + i, n4, splits);
   if constexpr (OUT_I32) {
     reinterpret_cast<kbh_i32x4*>(out)[i] = v;
   } else {
@@ -412,11 +412,12 @@ int w8a8_run(const void* x, const void* w, const void* xs, const void* wsc, void
                        (const uint16_t*)wsc, out, M, N, K);
     return launch_status();
   }
-  const size_t need = kbh_w8a8_workspace_bytes(M, N, K);
-  if (!workspace || workspace_bytes < need) return KBH_ERR_WORKSPACE;
-  int* acc = (int*)workspace;
   W8Plan p;
   if (!plan_w8_decode(M, N, K, &p)) return KBH_ERR_SHAPE;
+  const size_t need = splitk_workspace_bytes(M, N, p.splits);
+  if (need > 0 && (!workspace || workspace_bytes < need)) return KBH_ERR_WORKSPACE;
+  if (need > 0 && !aligned16(workspace)) return KBH_ERR_ALIGN;
+  int* acc = (int*)workspace;
   dim3 grid(p.ntiles * p.splits, p.mblocks);
   if (p.spw == 2)
     hipLaunchKernelGGL((w8a8_decode_kernel<2, OUT_I32>), grid, dim3(p.waves * 64), 0, st,
@@ -427,9 +428,9 @@ int w8a8_run(const void* x, const void* w, const void* xs, const void* wsc, void
                        (const int8_t*)x, (const int8_t*)w, (const uint16_t*)xs,
                        (const uint16_t*)wsc, out, acc, M, N, K, p.splits);
   if (p.splits > 1)
-    hipLaunchKernelGGL((w8a8_finalize<OUT_I32>), dim3(splitk_finalize_blocks(M, N)), dim3(256), 0,
-                       st, acc, (const uint16_t*)xs, (const uint16_t*)wsc, out, N,
-                       (size_t)M * N / 4);
+    hipLaunchKernelGGL((w8a8_finalize<OUT_I32>), dim3(splitk_sum_blocks(M, N)), dim3(256), 0, st,
+                       acc, (const uint16_t*)xs, (const uint16_t*)wsc, out, N, (size_t)M * N / 4,
+                       p.splits);
   return launch_status();
 }
 
@@ -445,8 +446,9 @@ int w8a8_check(const void* x, const void* w, const void* xs, const void* wsc, co
 }  // namespace kbh
 
 extern "C" size_t kbh_w8a8_workspace_bytes(int M, int N, int K) {
-  (void)K;
-  return kbh::splitk_workspace_bytes(M, N);
+  kbh::W8Plan p;
+  if (M < 1 || N < 128 || K < 64 || !kbh::plan_w8_decode(M, N, K, &p)) return 0;
+  return kbh::splitk_workspace_bytes(M, N, p.splits);
 }
 
 extern "C" size_t kbh_w8a8_scratch_bytes(int M, int N, int K) {

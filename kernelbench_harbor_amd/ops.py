@@ -16,15 +16,11 @@ _DT_CODE = {torch.float16: _lib.KBH_F16, torch.bfloat16: _lib.KBH_BF16}
 
 
 class _WorkspacePool:
-    """Device buffers per (device, stream), grown on demand.
+    """Device buffers per (device, stream), grown on demand. The kernels put no requirement on
+    their content, so one buffer serves every call ordered on the same stream; the two pools
+    below exist because an op may need a workspace and a scratch buffer that do not overlap."""
 
-    zeroed=True: zero-filled workspace; the kernels leave it zero-filled after every call, so
-    one buffer serves every call ordered on the same stream. zeroed=False: scratch with no
-    content requirement (never shared with the zero-filled pool).
-    """
-
-    def __init__(self, zeroed: bool):
-        self._zeroed = zeroed
+    def __init__(self):
         self._bufs: dict[tuple[int, int], torch.Tensor] = {}
         self._lock = threading.Lock()
 
@@ -34,14 +30,13 @@ class _WorkspacePool:
         with self._lock:
             buf = self._bufs.get(key)
             if buf is None or buf.numel() < nbytes:
-                alloc = torch.zeros if self._zeroed else torch.empty
-                buf = alloc(max(nbytes, 256), dtype=torch.uint8, device=device)
+                buf = torch.empty(max(nbytes, 256), dtype=torch.uint8, device=device)
                 self._bufs[key] = buf
             return buf
 
 
-workspaces = _WorkspacePool(zeroed=True)
-scratches = _WorkspacePool(zeroed=False)
+workspaces = _WorkspacePool()
+scratches = _WorkspacePool()
 
 
 def _require(cond: bool, msg: str) -> None:

@@ -3,7 +3,7 @@ import numpy as np
 import pytest
 import torch
 
-from kernelbench_harbor_amd import W4A16Model, inputs, ops
+from kernelbench_harbor_amd import W4A16Model, _lib, inputs, ops
 from kernelbench_harbor_amd.harness import compare
 from oracle import w4a16 as ow
 
@@ -108,15 +108,17 @@ def test_w4a16_full_size_prefill(dev):
     assert cmp.ok, cmp
 
 
-def test_w4a16_workspace_left_clean_and_repeatable(dev):
+def test_w4a16_split_k_deterministic_with_garbage_workspace(dev):
+    """The split-K decode sums its partial slices in a fixed order and reads nothing it did not
+    write: a workspace full of 0xFF bytes (NaN patterns) gives the same bits as before."""
     M, K, N = 16, 14336, 4096
+    assert _lib.load().kbh_w4a16_workspace_bytes(M, N, K, 128) > 0   # the split-K path
     x, qw, s, z = [t.to(dev) for t in inputs.w4a16(M, K, N, seed=3)]
     y1 = ops.w4a16_gemm(x, qw, s, z)
+    ops.workspaces.get(0, x.device).fill_(255)
     y2 = ops.w4a16_gemm(x, qw, s, z)
-    torch.cuda.synchronize()
-    ws = ops.workspaces.get(0, x.device)
-    assert int(ws.count_nonzero()) == 0
-    assert compare(y2, y1.float()).max_abs_frac < 1e-3
+    assert torch.equal(y1, y2)
+    assert compare(y1, _gt(x.cpu(), qw.cpu(), s.cpu(), z.cpu())).ok
 
 
 def test_w4a16_batched_leading_dims(dev):
