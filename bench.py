@@ -45,10 +45,10 @@ def w4a16_bytes(M, K=K_DIM, N=N_DIM, G=GROUP):
 
 
 # HBM bytes per kbh_w4a16_gemm call at the sweep's two regimes, from rocprofv3 PMC runs:
-# FETCH_SIZE scaled by 2.0 (a plain 256 MiB device copy reads as 131085.3 KiB) plus WRITE_SIZE
-# (exact on the same copy), summed over the call's launches (GEMM + split-K finalize/reduce).
+# FETCH_SIZE scaled by 2.0 (a plain 256 MiB device copy reads as 131085.4 KiB) plus WRITE_SIZE
+# (exact on the same copy), summed over the call's launches (GEMM + split-K slice sum).
 # Keyed by M; other M report null.
-W4A16_PMC_TRAFFIC = {16: 39_911_116, 2048: 466_557_595}
+W4A16_PMC_TRAFFIC = {16: 43_613_798, 2048: 466_669_568}
 
 
 def gemm_flops(M, N=N_DIM, K=K_DIM):
