@@ -396,19 +396,22 @@ __global__ __launch_bounds__(256) void moe_reduce_combine_kernel(
   *reinterpret_cast<kbh_u32x2*>(y + e) = o;
 }
 
-// FFN plan: 128 x 256 expert tiles, one workgroup per CU with a 4-slab prefetch ring; gate/up
-// unsplit (about 2T/128 x 2F/256 workgroups), down split over K until the estimated
-// 2T/128 x D/256 tiles fill the CUs.
+// FFN plan: TM x 256 expert tiles (TM = 256 rows when experts average at least 192 routed rows,
+// else 128: at ~128 rows per expert, 256-row tiles measured 20% slower despite fewer tiles), one
+// workgroup per CU with a 4-slab prefetch ring; gate/up unsplit (about
+// 2T/TM x 2F/256 workgroups), down split over K until the estimated 2T/TM x D/256 tiles fill
+// the CUs.
 constexpr int kFfnPD = 4;
 struct FfnPlan {
-  int spg;
+  int spg, tm;
   WidePlan down;
 };
-bool plan_ffn(int T, int D, int F, int group, FfnPlan* p) {
+bool plan_ffn(int T, int E, int D, int F, int group, FfnPlan* p) {
   p->spg = group / 32;
+  p->tm = (2 * T) / (E > 0 ? E : 1) >= 192 ? 256 : 128;
   const int unroll = 2 * p->spg > kFfnPD ? 2 * p->spg : kFfnPD;  // the kernel's slabs per iteration
   if (F % 128 != 0 || D % 256 != 0 || D % (unroll * 32) != 0 || F % (unroll * 32) != 0) return false;
-  return plan_wide(2 * T, D, F, 256, 32, unroll, 256, &p->down, 128);
+  return plan_wide(2 * T, D, F, 256, 32, unroll, 256, &p->down, p->tm == 256 ? 256 : 128);
 }
 
 // ---- host side ------------------------------------------------------------------------------
@@ -476,7 +479,7 @@ void launch_combine(const void* o, const uint16_t* topw, void* y, int T, int N, 
                      (const uint16_t*)o, topw, (uint16_t*)y, T, N);
 }
 
-template <bool BF16, int SPG>
+template <bool BF16, int TM, int SPG>
 void launch_ffn_wide_spg(const FfnPlan& fp, const MoeLayout& L, const MoeBuffers& mb,
                          const void* x, const W4WidePolicy<BF16, 256>& gp,
                          const W4WidePolicy<BF16, 256>& upp, const W4WidePolicy<BF16, 256>& dp,
@@ -490,7 +493,7 @@ void launch_ffn_wide_spg(const FfnPlan& fp, const MoeLayout& L, const MoeBuffers
     const BP bp{gp, upp};
     const SiluPairOut<BF16> ep{(uint16_t*)h, F};
     const int grid = L.max_tiles * (2 * F / 256);
-    hipLaunchKernelGGL((tiled_wide_gemm<E, 128, 4, SPG, BP, SiluPairOut<BF16>, RM, 1, kFfnPD>),
+    hipLaunchKernelGGL((tiled_wide_gemm<E, TM, 4, SPG, BP, SiluPairOut<BF16>, RM, 1, kFfnPD>),
                        dim3(grid), dim3(256), 0, st, x, bp, ep, (float*)nullptr, 2 * T, 2 * F, D,
                        1, D / 32, RM{mb.tiles, mb.perm});
   }
@@ -501,7 +504,7 @@ void launch_ffn_wide_spg(const FfnPlan& fp, const MoeLayout& L, const MoeBuffers
     const HalfOut<BF16> ep{(uint16_t*)o, D};
     const int splits = fp.down.splits;
     const int grid = L.max_tiles * (D / 256) * splits;
-    hipLaunchKernelGGL((tiled_wide_gemm<E, 128, 4, SPG, BP, HalfOut<BF16>, RM, 1, kFfnPD>),
+    hipLaunchKernelGGL((tiled_wide_gemm<E, TM, 4, SPG, BP, HalfOut<BF16>, RM, 1, kFfnPD>),
                        dim3(grid), dim3(256), 0, st, h, dp, ep, part, 2 * T, D, F, splits,
                        fp.down.slabs_per_split, RM{mb.tiles, mb.perm});
     if (splits > 1) {
@@ -526,22 +529,33 @@ void launch_ffn_wide(const FfnPlan& fp, const MoeLayout& L, const MoeBuffers& mb
                                     (const uint16_t*)uz_, F, group, gq, gs, 0x000F000Fu};
   const W4WidePolicy<BF16, 256> dp{(const uint32_t*)dq_, (const uint16_t*)ds_,
                                    (const uint16_t*)dz_, D, group, dq, ds, 0x000F000Fu};
-  switch (fp.spg) {
-    case 1: return launch_ffn_wide_spg<BF16, 1>(fp, L, mb, x, gp, upp, dp, h, o, part, y, T, D, F, st);
-    case 2: return launch_ffn_wide_spg<BF16, 2>(fp, L, mb, x, gp, upp, dp, h, o, part, y, T, D, F, st);
-    case 4: return launch_ffn_wide_spg<BF16, 4>(fp, L, mb, x, gp, upp, dp, h, o, part, y, T, D, F, st);
-    default: return launch_ffn_wide_spg<BF16, 8>(fp, L, mb, x, gp, upp, dp, h, o, part, y, T, D, F, st);
+#define KBH_FFN(TM_, SPG_) \
+  return launch_ffn_wide_spg<BF16, TM_, SPG_>(fp, L, mb, x, gp, upp, dp, h, o, part, y, T, D, F, st)
+  if (fp.tm == 256) {
+    switch (fp.spg) {
+      case 1: KBH_FFN(256, 1);
+      case 2: KBH_FFN(256, 2);
+      case 4: KBH_FFN(256, 4);
+      default: KBH_FFN(256, 8);
+    }
   }
+  switch (fp.spg) {
+    case 1: KBH_FFN(128, 1);
+    case 2: KBH_FFN(128, 2);
+    case 4: KBH_FFN(128, 4);
+    default: KBH_FFN(128, 8);
+  }
+#undef KBH_FFN
 }
 
-// FFN layout: 128-row tiles and room for the down projection's split-K partials when the wide
+// FFN layout: TM-row tiles (the plan's) and room for the down projection's split-K partials when the wide
 // path applies (plan_ffn); otherwise the 256 x 128 grouped kernels run.
 MoeLayout ffn_layout(int T, int E, int D, int F, int group, bool* wide, FfnPlan* fp) {
   *wide = (group == 32 || group == 64 || group == 128 || group == 256) &&
-          plan_ffn(T, D, F, group, fp);
+          plan_ffn(T, E, D, F, group, fp);
   if (!*wide) return moe_layout(T, E, F, D);
   const size_t part = fp->down.splits > 1 ? (size_t)fp->down.splits * 2 * T * D * 4 : 0;
-  return moe_layout(T, E, F, D, 128, part);
+  return moe_layout(T, E, F, D, fp->tm, part);
 }
 
 bool moe_shape_ok(int T, int E, int K, int N, int group) {

@@ -72,6 +72,9 @@ FFN_CASES = [
     (64, 256, 512, 4, torch.float16),
     (128, 512, 1024, 8, torch.float16),
     (96, 512, 384, 8, torch.bfloat16),
+    # >= 192 routed rows per expert on average: 256-row expert tiles
+    (400, 256, 256, 4, torch.float16),
+    (512, 512, 512, 4, torch.bfloat16),
 ]
 
 
