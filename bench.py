@@ -169,6 +169,66 @@ def record(name, ts, batched, by, fl, peak, **extra):
     return out
 
 
+# ---- the reference's task grid ---------------------------------------------------------------
+# The task lists of generate_tasks.py:268-275 (linear shapes), 390-394 (qMoE) and 481-490 (W4A16
+# layers), with the families' grid axes (generate_tasks.py:535-544, 561-580, 617-626).
+GRID_LAYERS = [("llama3_8b_gate", 4096, 14336), ("llama3_8b_down", 14336, 4096),
+               ("llama3_70b_gate", 8192, 28672), ("llama3_70b_down", 28672, 8192),
+               ("qwen2_7b_gate", 3584, 18944), ("qwen2_7b_down", 18944, 3584),
+               ("qwen2_72b_gate", 8192, 29568), ("qwen2_72b_down", 29568, 8192)]
+GRID_LINEAR = [("llama3_8b_qkv", 4096, 6144), ("llama3_8b_o", 4096, 4096),
+               ("llama3_8b_gate", 4096, 14336), ("llama3_8b_down", 14336, 4096),
+               ("qwen2_7b_gate", 3584, 18944), ("qwen2_72b_down", 29568, 8192)]
+GRID_QMOE = [("deepseek_moe", 2048, 64, 1408), ("mixtral", 4096, 8, 14336),
+             ("qwen_moe", 2048, 60, 1408)]
+
+
+def w4a16_bytes(M, K, N, G):
+    return K * N // 2 + 2 * (K // G) * N * 2 + 2 * M * K + 2 * M * N
+
+
+def run_grid(torch, dev, inputs, ops):
+    """Times every task of the grid (M=16 unless the task says otherwise; T=256 for the qMoE)
+    on rotated HBM-cold inputs; one record per task."""
+    recs = []
+    f16, bf16 = torch.float16, torch.bfloat16
+
+    def one(name, make, fn, by, fl, peak, n_sets_bytes, **extra):
+        sets = rotation(make, n_sets_bytes)
+        ts, bm = time_config(torch, fn, sets, 10, 20)
+        recs.append(record(name, ts, bm, by, fl, peak, **extra))
+        del sets
+        torch.cuda.empty_cache()
+        print(f"[grid] {name}: {recs[-1]['us_batched']} us, frac {recs[-1]['roofline_frac']}",
+              file=sys.stderr, flush=True)
+
+    for (n, K, N) in GRID_LAYERS:
+        for g, dt in ((64, f16), (128, f16), (128, bf16)):
+            by = w4a16_bytes(16, K, N, g)
+            one(f"w4a16 {n} g{g} {str(dt)[6:]}",
+                lambda: [t.to(dev) for t in inputs.w4a16(16, K, N, g, dt, seed=1)],
+                ops.w4a16_gemm, by, 2 * 16 * N * K, PEAK["f16"], by, M=16, K=K, N=N)
+    for (n, K, N) in GRID_LINEAR:
+        for M in (16, 64, 256):
+            by = w8a8_bytes(M, K, N)
+            one(f"w8a8 {n} M={M}",
+                lambda: [t.to(dev) for t in inputs.w8a8(M, K, N, seed=1, dist="reference")],
+                ops.w8a8_gemm, by, 2 * M * N * K, PEAK["i8"], by, M=M, K=K, N=N)
+    for (n, K, N) in GRID_LINEAR:
+        for b, dt in ((32, f16), (128, f16), (32, bf16)):
+            by = fp8w_bytes(16, K, N, b)
+            one(f"fp8w {n} b{b} {str(dt)[6:]}",
+                lambda: [t.to(dev) for t in inputs.fp8w(16, K, N, b, dt, seed=1)],
+                ops.fp8w_gemm, by, 2 * 16 * N * K, PEAK["f16"], by, M=16, K=K, N=N)
+    for (n, D, E, N) in GRID_QMOE:
+        for dt in (f16, bf16):
+            by = qmoe_bytes(256, D, N, E)
+            one(f"qmoe {n} {str(dt)[6:]}",
+                lambda: [t.to(dev) for t in inputs.qmoe(256, D, E, N, dt, seed=1)],
+                ops.qmoe, by, qmoe_flops(256, D, N), PEAK["f16"], by, T=256, D=D, E=E, N=N)
+    return recs
+
+
 # ---- CPU baseline ----------------------------------------------------------------------------
 def cpu_baseline(sample_m, seed=0):
     """Times the numpy oracle (oracle/w4a16.py, fp32 ground-truth path) on the host cores."""
@@ -208,6 +268,9 @@ def main():
     ap.add_argument("--m", type=str, default=",".join(map(str, SWEEP_M)))
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-configs", action="store_true", help="only the W4A16 sweep")
+    ap.add_argument("--grid", action="store_true",
+                    help="only time the reference's task grid (all W4A16/W8A8/FP8/qMoE tasks at "
+                         "their real shapes) and print one JSON line of per-task records")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                     help="only run 5 device copies of MIB MiB (calibrates rocprofv3 FETCH_SIZE/"
                          "WRITE_SIZE against a kernel of known traffic) and exit")
@@ -234,6 +297,11 @@ def main():
             dst.copy_(src)
         torch.cuda.synchronize()
         print(json.dumps({"copy_probe_bytes": n, "copies": 5}))
+        return
+    if args.grid:
+        recs = run_grid(torch, dev, inputs, ops)
+        print(json.dumps({"grid": recs, "n_gpus": 1, "data": "synthetic (seeded; the reference "
+                          "task distributions; inputs rotated to stay HBM-cold)"}))
         return
     ms = [int(v) for v in args.m.split(",") if v]
 
