@@ -43,10 +43,8 @@ __device__ inline kbh_u32x2 fp8x4_dequant(uint32_t v, uint16_t s) {
     const float sf = f16_bits_to_f32(s);
     const f2_t lo = __builtin_amdgcn_cvt_pk_f32_fp8(v, false);
     const f2_t hi = __builtin_amdgcn_cvt_pk_f32_fp8(v, true);
-    return kbh_u32x2{(uint32_t)f32_to_bf16_bits(keep_f32(lo[0] * sf)) |
-                         ((uint32_t)f32_to_bf16_bits(keep_f32(lo[1] * sf)) << 16),
-                     (uint32_t)f32_to_bf16_bits(keep_f32(hi[0] * sf)) |
-                         ((uint32_t)f32_to_bf16_bits(keep_f32(hi[1] * sf)) << 16)};
+    return kbh_u32x2{f32x2_to_bf16x2_bits(keep_f32(lo[0] * sf), keep_f32(lo[1] * sf)),
+                     f32x2_to_bf16x2_bits(keep_f32(hi[0] * sf), keep_f32(hi[1] * sf))};
   } else {
     const _Float16 sh = __builtin_bit_cast(_Float16, s);
     const h2_t lo = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(v, 1.0f, false) * h2_t{sh, sh};

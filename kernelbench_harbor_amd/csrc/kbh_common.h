@@ -81,13 +81,16 @@ __device__ inline float keep_f32(float v) {
   return v;
 }
 
-// fp32 -> fp16 / bf16 with round-to-nearest-even (NaN is kept quiet).
+// fp32 -> fp16 / bf16 with round-to-nearest-even (NaN is kept quiet); both are hardware
+// conversions on gfx950 (v_cvt_f16_f32, v_cvt_pk_bf16_f32; two neighbouring bf16 conversions
+// become one packed instruction).
 __device__ inline uint16_t f32_to_f16_bits(float f) { return __builtin_bit_cast(uint16_t, (_Float16)f); }
-__device__ inline uint16_t f32_to_bf16_bits(float f) {
-  uint32_t u = __builtin_bit_cast(uint32_t, f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return (uint16_t)(u >> 16);
+__device__ inline uint16_t f32_to_bf16_bits(float f) { return __builtin_bit_cast(uint16_t, (__bf16)f); }
+// Two fp32 values to one dword of bf16 (lo in bits 0-15), one v_cvt_pk_bf16_f32.
+__device__ inline uint32_t f32x2_to_bf16x2_bits(float lo, float hi) {
+  typedef float f2 __attribute__((ext_vector_type(2)));
+  typedef __bf16 b2 __attribute__((ext_vector_type(2)));
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f2{lo, hi}, b2));
 }
 template <bool BF16>
 __device__ inline uint16_t f32_to_half_bits(float f) {

@@ -51,12 +51,11 @@ __device__ inline void dequant_2x8(uint32_t w0, uint32_t w1, kbh_u32x4 sv, kbh_u
         // q - z is exact in fp32 and rounds once to bf16; times s is exact in fp32 and rounds.
         const float s = bf16_bits_to_f32(sb);
         const float z = bf16_bits_to_f32(zb);
-        const __bf16 dl = (__bf16)((bf16_bits_to_f32((uint16_t)(h & 0xffffu)) - 128.0f) - z);
-        const __bf16 dh = (__bf16)((bf16_bits_to_f32((uint16_t)(h >> 16)) - 128.0f) - z);
-        const __bf16 el = (__bf16)((float)dl * s);
-        const __bf16 eh = (__bf16)((float)dh * s);
-        out[col] = (uint32_t)__builtin_bit_cast(uint16_t, el) |
-                   ((uint32_t)__builtin_bit_cast(uint16_t, eh) << 16);
+        const uint32_t d =
+            f32x2_to_bf16x2_bits((bf16_bits_to_f32((uint16_t)(h & 0xffffu)) - 128.0f) - z,
+                                 (bf16_bits_to_f32((uint16_t)(h >> 16)) - 128.0f) - z);
+        out[col] = f32x2_to_bf16x2_bits(__builtin_bit_cast(float, d << 16) * s,
+                                        __builtin_bit_cast(float, d & 0xffff0000u) * s);
       } else {
         typedef _Float16 h2 __attribute__((ext_vector_type(2)));
         const _Float16 sc = __builtin_bit_cast(_Float16, sb);
@@ -172,12 +171,9 @@ struct W4WidePolicy {
     if constexpr (BF16) {
       // q - z is exact in fp32 and rounds once to bf16; times s is exact in fp32 and rounds once.
       const float z = bf16_bits_to_f32(zb), s = bf16_bits_to_f32(sb);
-      const __bf16 d0 = (__bf16)((float)(m & 0xffu) - z);
-      const __bf16 d1 = (__bf16)((float)(m >> 16) - z);
-      const __bf16 e0 = (__bf16)((float)d0 * s);
-      const __bf16 e1 = (__bf16)((float)d1 * s);
-      return (uint32_t)__builtin_bit_cast(uint16_t, e0) |
-             ((uint32_t)__builtin_bit_cast(uint16_t, e1) << 16);
+      const uint32_t d = f32x2_to_bf16x2_bits((float)(m & 0xffu) - z, (float)(m >> 16) - z);
+      return f32x2_to_bf16x2_bits(__builtin_bit_cast(float, d << 16) * s,
+                                  __builtin_bit_cast(float, d & 0xffff0000u) * s);
     } else {
       typedef _Float16 h2 __attribute__((ext_vector_type(2)));
       const _Float16 z = __builtin_bit_cast(_Float16, zb), sc = __builtin_bit_cast(_Float16, sb);
