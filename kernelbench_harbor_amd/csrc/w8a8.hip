@@ -367,9 +367,10 @@ constexpr int kW8WideMinM = 33;
 // Prefetch depth 4 (four 64-deep slabs in flight) when the K slabs come in multiples of 4.
 int w8_wide_pd(int K) { return (K / 64) % 4 == 0 ? 4 : 2; }
 
+// 128-row tiles (one workgroup per CU) up to 128 rows, 256-row tiles above.
 bool plan_w8_wide(int M, int N, int K, WidePlan* p) {
   if (M < kW8WideMinM || N % 256 != 0) return false;
-  return plan_wide(M, N, K, 256, 64, w8_wide_pd(K), 256, p, 256);
+  return plan_wide(M, N, K, 256, 64, w8_wide_pd(K), 256, p, 128);
 }
 
 template <bool OUT_I32, int TM, int PD>
@@ -379,7 +380,8 @@ void launch_w8_wide(const WidePlan& p, const void* x, const void* w, const void*
   using EP = W8Out<OUT_I32>;
   const W8WidePolicy bp{(const int8_t*)w, N};
   const EP ep{out, (const uint16_t*)xs, (const uint16_t*)wsc, N};
-  hipLaunchKernelGGL((tiled_wide_gemm<WideI8, TM, 4, 1, W8WidePolicy, EP, DenseRows, 0, PD>),
+  constexpr int MINB = TM == 128 ? 1 : 0;
+  hipLaunchKernelGGL((tiled_wide_gemm<WideI8, TM, 4, 1, W8WidePolicy, EP, DenseRows, MINB, PD>),
                      dim3(p.grid),
                      dim3(256), 0, st, x, bp, ep, scratch, M, N, K, p.splits, p.slabs_per_split,
                      DenseRows{M});
@@ -399,10 +401,14 @@ int w8a8_run(const void* x, const void* w, const void* xs, const void* wsc, void
     const size_t need = wide_workspace_bytes(M, N, wp.splits);
     if (need > 0 && (!scratch || scratch_bytes < need)) return KBH_ERR_WORKSPACE;
     if (need > 0 && !aligned16(scratch)) return KBH_ERR_ALIGN;
-    if (w8_wide_pd(K) == 4)
-      launch_w8_wide<OUT_I32, 256, 4>(wp, x, w, xs, wsc, out, (int*)scratch, M, N, K, st);
-    else
-      launch_w8_wide<OUT_I32, 256, 2>(wp, x, w, xs, wsc, out, (int*)scratch, M, N, K, st);
+    const bool pd4 = w8_wide_pd(K) == 4;
+    if (wp.tm == 128) {
+      if (pd4) launch_w8_wide<OUT_I32, 128, 4>(wp, x, w, xs, wsc, out, (int*)scratch, M, N, K, st);
+      else launch_w8_wide<OUT_I32, 128, 2>(wp, x, w, xs, wsc, out, (int*)scratch, M, N, K, st);
+    } else {
+      if (pd4) launch_w8_wide<OUT_I32, 256, 4>(wp, x, w, xs, wsc, out, (int*)scratch, M, N, K, st);
+      else launch_w8_wide<OUT_I32, 256, 2>(wp, x, w, xs, wsc, out, (int*)scratch, M, N, K, st);
+    }
     return launch_status();
   }
   if (M >= kW8TiledMinM && K % (WBK * WDEPTH) == 0) {
