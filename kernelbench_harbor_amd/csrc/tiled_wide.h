@@ -378,31 +378,46 @@ struct WidePlan {
   int grid;
 };
 
-// Picks the tile height (256 rows, or tm_small up to 128 rows) and the split count. `slots` is
-// the number of workgroups the GPU runs
-// at once (256 CUs x workgroups per CU). A split count is valid when it divides the K slabs into
-// ranges of at least 8 slabs that are a multiple of `unroll`; among those, the plan minimises
-// (waves of workgroups) x (slabs per workgroup), preferring fewer splits on a tie.
+// Picks the tile height and the split count. Up to 128 rows the tiles are tm_small rows high;
+// above, 256 rows, or (choose_tm) tm_small rows when the cost estimate favours them, i.e. when
+// 256-row tiles would leave CUs idle. `slots` is the number of workgroups the GPU runs at once
+// (256 CUs x workgroups per CU). A split count is valid when it divides the K slabs into ranges
+// of at least 8 slabs that are a multiple of `unroll`; among those, the plan minimises (waves of
+// workgroups) x (slabs per workgroup), preferring fewer splits on a tie.
 inline bool plan_wide(int M, int N, int K, int tn, int slab_k, int unroll, int slots,
-                      WidePlan* p, int tm_small = 128) {
+                      WidePlan* p, int tm_small = 128, bool choose_tm = false) {
   if (N % tn != 0 || K % (unroll * slab_k) != 0 || M < 1) return false;
   const int KT = K / slab_k;
-  p->tm = M > 128 ? 256 : tm_small;
-  const int tiles = ((M + p->tm - 1) / p->tm) * (N / tn);
-  long best = -1;
-  for (int s = 1; s <= KT / unroll; ++s) {
-    if (KT % s != 0) continue;
-    const int spp = KT / s;
-    if (spp % unroll != 0 || (spp < 8 && s > 1)) continue;
-    const long waves = ((long)tiles * s + slots - 1) / slots;
-    const long cost = waves * spp;
-    if (best < 0 || cost < best) {
-      best = cost;
-      p->splits = s;
-      p->slabs_per_split = spp;
+  // Plan for tile height tm; returns the estimated time in units of a third of a 128-row slab
+  // (a 256-row slab measures about 4/3 of a 128-row one).
+  auto plan_tm = [&](int tm, WidePlan* q) {
+    q->tm = tm;
+    const int tiles = ((M + tm - 1) / tm) * (N / tn);
+    long best = -1;
+    for (int s = 1; s <= KT / unroll; ++s) {
+      if (KT % s != 0) continue;
+      const int spp = KT / s;
+      if (spp % unroll != 0 || (spp < 8 && s > 1)) continue;
+      const long waves = ((long)tiles * s + slots - 1) / slots;
+      const long cost = waves * spp;
+      if (best < 0 || cost < best) {
+        best = cost;
+        q->splits = s;
+        q->slabs_per_split = spp;
+      }
     }
+    q->grid = tiles * q->splits;
+    return best * (tm == 256 ? 4 : 3);
+  };
+  if (M <= 128) {
+    plan_tm(tm_small, p);
+    return true;
   }
-  p->grid = tiles * p->splits;
+  const long c256 = plan_tm(256, p);
+  if (choose_tm && tm_small != 256) {
+    WidePlan q;
+    if (plan_tm(tm_small, &q) < c256) *p = q;
+  }
   return true;
 }
 

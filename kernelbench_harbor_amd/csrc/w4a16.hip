@@ -243,7 +243,8 @@ bool plan_w4_wide(int M, int N, int K, int group, W4Wide* w) {
   if (!small && w->tn != 256) return false;
   const int pd = w4_wide_pd(w->tn);
   const int unroll = 2 * w->spg > pd ? 2 * w->spg : pd;  // the kernel's slabs per iteration
-  return plan_wide(M, N, K, w->tn, 32, unroll, w->tn == 128 ? 512 : 256, &w->plan);
+  return plan_wide(M, N, K, w->tn, 32, unroll, w->tn == 128 ? 512 : 256, &w->plan, 128,
+                   w->tn == 256);
 }
 
 template <bool BF16, int TM, int TN, int SPG>

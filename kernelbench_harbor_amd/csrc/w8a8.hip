@@ -367,10 +367,11 @@ constexpr int kW8WideMinM = 33;
 // Prefetch depth 4 (four 64-deep slabs in flight) when the K slabs come in multiples of 4.
 int w8_wide_pd(int K) { return (K / 64) % 4 == 0 ? 4 : 2; }
 
-// 128-row tiles (one workgroup per CU) up to 128 rows, 256-row tiles above.
+// 128-row tiles (one workgroup per CU) up to 128 rows; above, 256-row tiles unless they would
+// leave CUs idle (plan_wide's choose_tm).
 bool plan_w8_wide(int M, int N, int K, WidePlan* p) {
   if (M < kW8WideMinM || N % 256 != 0) return false;
-  return plan_wide(M, N, K, 256, 64, w8_wide_pd(K), 256, p, 128);
+  return plan_wide(M, N, K, 256, 64, w8_wide_pd(K), 256, p, 128, true);
 }
 
 template <bool OUT_I32, int TM, int PD>
