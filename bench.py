@@ -183,10 +183,6 @@ GRID_QMOE = [("deepseek_moe", 2048, 64, 1408), ("mixtral", 4096, 8, 14336),
              ("qwen_moe", 2048, 60, 1408)]
 
 
-def w4a16_bytes(M, K, N, G):
-    return K * N // 2 + 2 * (K // G) * N * 2 + 2 * M * K + 2 * M * N
-
-
 def run_grid(torch, dev, inputs, ops):
     """Times every task of the grid (M=16 unless the task says otherwise; T=256 for the qMoE)
     on rotated HBM-cold inputs; one record per task."""
