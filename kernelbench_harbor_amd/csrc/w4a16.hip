@@ -176,14 +176,16 @@ struct DecodePlan {
 // divide evenly and the grid is close to one workgroup per CU (256).
 bool plan_decode(int M, int N, int K, int group_steps_, DecodePlan* p) {
   const int nsteps = K / 32;
-  p->nw = (N % 256 == 0) ? 2 : 1;
-  p->ntiles = N / (128 * p->nw);
-  p->mblocks = (M + 15) / 16;
   p->spw = (nsteps % 4 == 0) ? 4 : (nsteps % 2 == 0 ? 2 : 1);
   // Wave ranges start at multiples of SPW steps, so they stay inside one group when the group
   // spans a multiple of SPW steps; otherwise the group (1 or 2 steps) divides SPW.
   const int gsteps = group_steps_;
   p->spg = (gsteps % p->spw == 0) ? p->spw : gsteps;
+  // 256 columns per wave, except with four groups per wave (32-row groups): their constants on
+  // top of 256 columns' accumulators would spill.
+  p->nw = (N % 256 == 0 && 2 * p->spg >= p->spw) ? 2 : 1;
+  p->ntiles = N / (128 * p->nw);
+  p->mblocks = (M + 15) / 16;
   const int units = nsteps / p->spw;  // wave-sized K units per column tile
   p->waves = splitk_pick_waves(units, p->ntiles * p->mblocks, &p->splits);
   return p->waves > 0;
@@ -209,7 +211,7 @@ void dispatch_decode(const DecodePlan& p, const void* x, const int32_t* qw, cons
 #define KBH_DEC(NW_, SPW_, SPG_)                                                                 \
   if (p.nw == NW_ && p.spw == SPW_ && p.spg == SPG_)                                             \
     return launch_decode<NW_, SPW_, SPG_, BF16>(p, x, qw, s, z, y, acc, M, N, K, group, st);
-  KBH_DEC(2, 4, 4) KBH_DEC(2, 4, 2) KBH_DEC(2, 4, 1) KBH_DEC(2, 2, 2) KBH_DEC(2, 2, 1)
+  KBH_DEC(2, 4, 4) KBH_DEC(2, 4, 2) KBH_DEC(2, 2, 2) KBH_DEC(2, 2, 1)
   KBH_DEC(2, 1, 1) KBH_DEC(1, 4, 4) KBH_DEC(1, 4, 2) KBH_DEC(1, 4, 1) KBH_DEC(1, 2, 2)
   KBH_DEC(1, 2, 1) KBH_DEC(1, 1, 1)
 #undef KBH_DEC
