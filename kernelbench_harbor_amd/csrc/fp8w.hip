@@ -87,10 +87,14 @@ __global__ __launch_bounds__(kSplitKMaxWaves * 64) void fp8w_decode_kernel(
   const uint16_t* xb = x + (size_t)(xok ? m0 + c : 0) * K + st0 * 32 + 8 * g;
 #pragma unroll
   for (int u = 0; u < SPW; ++u) {
-    const kbh_u32x4 v = *reinterpret_cast<const kbh_u32x4*>(xb + u * 32);
-    af[u] = xok ? v : kbh_u32x4{0u, 0u, 0u, 0u};
+    af[u] = *reinterpret_cast<const kbh_u32x4*>(xb + u * 32);
     sv[u] = *reinterpret_cast<const kbh_u32x4*>(scales + (size_t)(((st0 + u) * 32) / block) * N + n0 + 8 * c);
   }
+  // All loads are issued before any use (a consumer between them stalls the stream).
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int u = 0; u < SPW; ++u)
+    if (!xok) af[u] = kbh_u32x4{0u, 0u, 0u, 0u};  // rows past M contribute zero
 
   kbh_f32x4 part[NCS];
 #pragma unroll
@@ -200,8 +204,8 @@ int fp8w_run(const void* x, const void* w, const void* scales, void* y, void* wo
   KBH_FP8_DEC(4) else KBH_FP8_DEC(2) else KBH_FP8_DEC(1)
 #undef KBH_FP8_DEC
   if (splits > 1)
-    hipLaunchKernelGGL((splitk_sum_half<BF16>), dim3(splitk_sum_blocks(M, N)), dim3(256), 0, st,
-                       acc, (uint16_t*)y, (size_t)M * N / 4, splits);
+    launch_splitk_sum(reinterpret_cast<const kbh_f32x4*>(acc), HalfOut<BF16>{(uint16_t*)y, N}, M, N,
+                      pl.ntiles, 128, splits, st);
   return launch_status();
 }
 

@@ -38,6 +38,15 @@ __device__ inline int xcd_remap(int bid, int nblocks) {
   return (bid & 7) * (nblocks >> 3) + (bid >> 3);
 }
 
+// Buffer resource over [p, p + bytes) (bytes clamped to 4 GiB - 1) for raw buffer loads: offsets
+// at or past the end read as zero. Word 3 is the gfx9 raw-buffer format (32-bit data, no swizzle).
+__device__ inline __amdgpu_buffer_rsrc_t make_rsrc(const void* p, size_t bytes) {
+  const int n = bytes >= 0xffffffffu ? -1 : (int)bytes;
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), 0, n, 0x00020000);
+}
+// Cache policy of streaming loads (read once): the nt bit.
+constexpr int kBufNT = 2;
+
 // 16x16x32 MFMA, fp16 or bf16 operands (8 values per lane, packed in 4 dwords), fp32 accumulate.
 // Lane l holds A[row l%16][k 8(l/16)..+8] and B[k 8(l/16)..+8][col l%16]; C lane l holds
 // C[4(l/16)+i][l%16], i = 0..3.
@@ -96,6 +105,24 @@ template <bool BF16>
 __device__ inline uint16_t f32_to_half_bits(float f) {
   if constexpr (BF16) return f32_to_bf16_bits(f); else return f32_to_f16_bits(f);
 }
+
+// Output policy: fp16/bf16 output of fp32 sums (emit: one element; emit4: four consecutive
+// elements of a row, n % 4 == 0).
+template <bool BF16>
+struct HalfOut {
+  static constexpr bool kPaired = false;
+  uint16_t* y;
+  int N;
+  __device__ void emit(int r, int n, float v) const {
+    y[(size_t)r * N + n] = f32_to_half_bits<BF16>(v);
+  }
+  __device__ void emit4(int r, int n, kbh_f32x4 v) const {
+    kbh_u32x2 o;
+    o[0] = (uint32_t)f32_to_half_bits<BF16>(v[0]) | ((uint32_t)f32_to_half_bits<BF16>(v[1]) << 16);
+    o[1] = (uint32_t)f32_to_half_bits<BF16>(v[2]) | ((uint32_t)f32_to_half_bits<BF16>(v[3]) << 16);
+    *reinterpret_cast<kbh_u32x2*>(y + (size_t)r * N + n) = o;
+  }
+};
 
 // p[0] + p[stride] + ... + p[(n-1)*stride], added in slice order (n >= 1). The slices were just
 // written by another kernel, so every load is a full memory round trip: the loads of up to 16

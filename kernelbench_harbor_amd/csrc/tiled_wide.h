@@ -75,23 +75,6 @@ struct WideI8 {
   }
 };
 
-// fp16/bf16 output of fp32 sums.
-template <bool BF16>
-struct HalfOut {
-  static constexpr bool kPaired = false;
-  uint16_t* y;
-  int N;
-  __device__ void emit(int r, int n, float v) const {
-    y[(size_t)r * N + n] = f32_to_half_bits<BF16>(v);
-  }
-  __device__ void emit4(int r, int n, kbh_f32x4 v) const {
-    kbh_u32x2 o;
-    o[0] = (uint32_t)f32_to_half_bits<BF16>(v[0]) | ((uint32_t)f32_to_half_bits<BF16>(v[1]) << 16);
-    o[1] = (uint32_t)f32_to_half_bits<BF16>(v[2]) | ((uint32_t)f32_to_half_bits<BF16>(v[3]) << 16);
-    *reinterpret_cast<kbh_u32x2*>(y + (size_t)r * N + n) = o;
-  }
-};
-
 // Column slot within a slab: columns are permuted within groups of 8 (slot = 8q + ((n ^ f(q)) &
 // 7), q = n/8, f(q) = q ^ (q >> 3)) so that producer writes, which step through packed words 8
 // columns apart, spread over all LDS banks.

@@ -21,8 +21,9 @@
 //    with sum_k x_k from one extra MFMA against a ones fragment.
 //  * The waves of a workgroup (consecutive K ranges of one column tile) reduce through private
 //    LDS slices; each workgroup (K split) stores its tile into its own workspace slice, and
-//    splitk_sum_half adds the slices in split order and converts to the output dtype
-//    (splitk.h). Workgroup ids are remapped so that all K splits of a column tile run on one XCD.
+//    splitk_sum_kernel, run on the XCDs that wrote them, adds the slices in split order and
+//    converts to the output dtype (splitk.h). Workgroup ids are remapped so that all K splits
+//    of a column tile run on one XCD.
 //
 // Larger M (M > 32): tiled_wide_gemm (tiled_wide.h) with W4WidePolicy, which dequantizes each
 // packed 32 x TN weight slab once per workgroup into LDS with the exact reference arithmetic
@@ -59,7 +60,7 @@ __global__ __launch_bounds__(kSplitKMaxWaves * 64) void w4a16_decode_kernel(
 
   const int waves = blockDim.x >> 6;
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform: SGPR addressing
   const int c = lane & 15;
   const int g = lane >> 4;
   const int id = xcd_remap(blockIdx.x, gridDim.x);
@@ -77,10 +78,7 @@ __global__ __launch_bounds__(kSplitKMaxWaves * 64) void w4a16_decode_kernel(
   const bool xok = m0 + c < M;
   const uint16_t* xb = x + (size_t)(xok ? m0 + c : 0) * K + st0 * 32 + 8 * g;
 #pragma unroll
-  for (int u = 0; u < SPW; ++u) {
-    const kbh_u32x4 v = *reinterpret_cast<const kbh_u32x4*>(xb + u * 32);
-    af[u] = xok ? v : kbh_u32x4{0u, 0u, 0u, 0u};
-  }
+  for (int u = 0; u < SPW; ++u) af[u] = *reinterpret_cast<const kbh_u32x4*>(xb + u * 32);
   constexpr int NG = SPW / SPG;  // quantization groups touched by this wave
   kbh_u32x4 sv[NG][NW], zv[NG][NW];
 #pragma unroll
@@ -93,25 +91,43 @@ __global__ __launch_bounds__(kSplitKMaxWaves * 64) void w4a16_decode_kernel(
       zv[gq][w] = *reinterpret_cast<const kbh_u32x4*>(zeros + off);
     }
   }
+  __builtin_amdgcn_sched_barrier(0);  // keeps the group constants ahead of the weight stream
   uint32_t wd[SPW][8][NW];
-  const uint32_t* qb = qw + (size_t)(st0 * 32 + 8 * g) * NP + (n0 >> 3) + c * NW;
+  // Buffer loads from the wave's first row: the row offset is an SGPR (soffset) and the lane
+  // offset one VGPR, so no load needs per-lane 64-bit address arithmetic (global loads got a
+  // v_lshl_add_u64 chain). Reads past the matrix would return zero (range-checked resource).
+  const size_t qbase = (size_t)st0 * 32 * NP + (n0 >> 3);
+  const __amdgpu_buffer_rsrc_t qres = make_rsrc(qw + qbase, ((size_t)K * NP - qbase) * 4);
+  const uint32_t qlane = (uint32_t)(8 * g * NP + c * NW) * 4u;
 #pragma unroll
   for (int u = 0; u < SPW; ++u) {
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-      const uint32_t* p = qb + (size_t)(u * 32 + i) * NP;
+      const int soff = (u * 32 + i) * NP * 4;
       if constexpr (NW == 2) {
-        const kbh_u32x2 v = __builtin_nontemporal_load(reinterpret_cast<const kbh_u32x2*>(p));
+        const kbh_u32x2 v = __builtin_amdgcn_raw_buffer_load_b64(qres, qlane, soff, kBufNT);
         wd[u][i][0] = v[0];
         wd[u][i][1] = v[1];
       } else {
-        wd[u][i][0] = __builtin_nontemporal_load(p);
+        wd[u][i][0] = __builtin_amdgcn_raw_buffer_load_b32(qres, qlane, soff, kBufNT);
       }
     }
   }
+  // Nothing may use a loaded value before the last load is issued: a consumer scheduled between
+  // the loads makes the wave wait one memory latency with part of its stream not yet requested.
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int u = 0; u < SPW; ++u)
+    if (!xok) af[u] = kbh_u32x4{0u, 0u, 0u, 0u};  // rows past M contribute zero
 
   const uint32_t one = BF16 ? kOneBF16 : kOneF16;
   const kbh_u32x4 ones = {one, one, one, one};
+  // The nibble masks in SGPRs and the magic exponent in a VGPR: (P & mask) | magic is then one
+  // v_and_or_b32 (a VOP3 here takes no literal and reads at most one SGPR); with literals the
+  // compiler emits a v_and_b32 and a v_or_b32 per B dword.
+  uint32_t mlo = 0x000F000Fu, mhi = 0x00F000F0u, magic = MAGIC;
+  asm volatile("" : "+s"(mlo), "+s"(mhi));
+  asm volatile("" : "+v"(magic));
   kbh_f32x4 tot[NCS], part[NCS], xs = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int cs = 0; cs < NCS; ++cs) {
@@ -129,8 +145,8 @@ __global__ __launch_bounds__(kSplitKMaxWaves * 64) void w4a16_decode_kernel(
 #pragma unroll
         for (int p = 0; p < 4; ++p) {
           const uint32_t P = pair_bytes_rt(wd[u][2 * p][w], wd[u][2 * p + 1][w], j);
-          blo[p] = (P & 0x000F000Fu) | MAGIC;
-          bhi[p] = BF16 ? (((P >> 4) & 0x000F000Fu) | MAGIC) : ((P & 0x00F000F0u) | MAGIC);
+          blo[p] = (P & mlo) | magic;
+          bhi[p] = BF16 ? (((P >> 4) & mlo) | magic) : ((P & mhi) | magic);
         }
         part[w * 8 + 2 * j] = mfma16x16x32<BF16>(af[u], blo, part[w * 8 + 2 * j]);
         part[w * 8 + 2 * j + 1] = mfma16x16x32<BF16>(af[u], bhi, part[w * 8 + 2 * j + 1]);
@@ -162,6 +178,10 @@ __global__ __launch_bounds__(kSplitKMaxWaves * 64) void w4a16_decode_kernel(
     }
   }
 
+  // The fold's only use is inside splitk_reduce's row-guarded branch; without this the compiler
+  // sinks the fold, and the group-constant loads with it, behind that branch and the last weight.
+#pragma unroll
+  for (int cs = 0; cs < NCS; ++cs) asm volatile("" : "+v"(tot[cs]));
   const int rows = min(16, M - m0);
   splitk_reduce<NCS, float>(tot, sm, acc, split, splits, rows, M, N, m0, n0, [&](int r, int n, float v) {
     y[(size_t)(m0 + r) * N + n0 + n] = f32_to_half_bits<BF16>(v);
@@ -200,8 +220,8 @@ void launch_decode(const DecodePlan& p, const void* x, const int32_t* qw, const 
                      (const uint16_t*)x, (const uint32_t*)qw, (const uint16_t*)s,
                      (const uint16_t*)z, (uint16_t*)y, acc, M, N, K, group, p.splits);
   if (p.splits > 1)
-    hipLaunchKernelGGL((splitk_sum_half<BF16>), dim3(splitk_sum_blocks(M, N)), dim3(256), 0,
-                       stream, acc, (uint16_t*)y, (size_t)M * N / 4, p.splits);
+    launch_splitk_sum(reinterpret_cast<const kbh_f32x4*>(acc), HalfOut<BF16>{(uint16_t*)y, N}, M, N,
+                      p.ntiles, 128 * NW, p.splits, stream);
 }
 
 template <bool BF16>

@@ -11,7 +11,7 @@
 // w8a8_decode_kernel (small M): a wave owns 128 columns (dwordx2 per lane per row) and SPW steps
 // of 64 k; all loads up front; 16x16x64 int8 MFMAs; int32 partial tiles reduced through private
 // LDS slices, then each K-split workgroup stores its tile into its own workspace slice and
-// w8a8_finalize adds the slices (exact) and applies the epilogue (splitk.h).
+// splitk_sum_kernel adds the slices (exact) and applies the epilogue (splitk.h).
 // Larger M: tiled_wide_gemm (tiled_wide.h) with W8WidePolicy; w8a8_tiled_kernel (256x128 tile,
 // 64-deep K slabs in a register ring, the weight slab transposed into LDS k-major per column,
 // 2x2 waves of 128x64 with 32x32x32 int8 MFMAs) for shapes the wide kernel does not cover.
@@ -84,10 +84,12 @@ __global__ __launch_bounds__(kSplitKMaxWaves * 64) void w8a8_decode_kernel(
   const bool xok = m0 + c < M;
   const int8_t* xb = x + (size_t)(xok ? m0 + c : 0) * K + st0 * 64 + 16 * g;
 #pragma unroll
-  for (int u = 0; u < SPW; ++u) {
-    const kbh_u32x4 v = *reinterpret_cast<const kbh_u32x4*>(xb + u * 64);
-    af[u] = xok ? v : kbh_u32x4{0u, 0u, 0u, 0u};
-  }
+  for (int u = 0; u < SPW; ++u) af[u] = *reinterpret_cast<const kbh_u32x4*>(xb + u * 64);
+  // All loads are issued before any use (a consumer between them stalls the stream).
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int u = 0; u < SPW; ++u)
+    if (!xok) af[u] = kbh_u32x4{0u, 0u, 0u, 0u};  // rows past M contribute zero
 
   kbh_i32x4 accv[NCS];
 #pragma unroll
@@ -121,31 +123,6 @@ __global__ __launch_bounds__(kSplitKMaxWaves * 64) void w8a8_decode_kernel(
     if constexpr (OUT_I32) reinterpret_cast<int*>(out)[o] = v;
     else reinterpret_cast<uint16_t*>(out)[o] = w8a8_epilogue(v, xs[m0 + r], wsc[n0 + n]);
   });
-}
-
-// Sums the int32 split-K slices acc[splits][M*N] (exact integers) and applies the epilogue: 4
-// consecutive outputs of one row per thread (N % 4 == 0), n4 = M*N/4.
-template <bool OUT_I32>
-__global__ __launch_bounds__(256) void w8a8_finalize(const int* __restrict__ acc,
-                                                     const uint16_t* __restrict__ xs,
-                                                     const uint16_t* __restrict__ wsc,
-                                                     void* __restrict__ out, int N, size_t n4,
-                                                     int splits) {
-  const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
-  if (i >= n4) return;
-  const kbh_i32x4 v = sum_slices(reinterpret_cast<const kbh_i32x4*>(acc) + i, n4, splits);
-  if constexpr (OUT_I32) {
-    reinterpret_cast<kbh_i32x4*>(out)[i] = v;
-  } else {
-    const size_t e = 4 * i;
-    const int r = (int)(e / (size_t)N), n = (int)(e - (size_t)r * N);
-    kbh_u32x2 o;
-    o[0] = (uint32_t)w8a8_epilogue(v[0], xs[r], wsc[n]) |
-           ((uint32_t)w8a8_epilogue(v[1], xs[r], wsc[n + 1]) << 16);
-    o[1] = (uint32_t)w8a8_epilogue(v[2], xs[r], wsc[n + 2]) |
-           ((uint32_t)w8a8_epilogue(v[3], xs[r], wsc[n + 3]) << 16);
-    reinterpret_cast<kbh_u32x2*>(out)[i] = o;
-  }
 }
 
 struct W8Plan {
@@ -435,9 +412,9 @@ int w8a8_run(const void* x, const void* w, const void* xs, const void* wsc, void
                        (const int8_t*)x, (const int8_t*)w, (const uint16_t*)xs,
                        (const uint16_t*)wsc, out, acc, M, N, K, p.splits);
   if (p.splits > 1)
-    hipLaunchKernelGGL((w8a8_finalize<OUT_I32>), dim3(splitk_sum_blocks(M, N)), dim3(256), 0, st,
-                       acc, (const uint16_t*)xs, (const uint16_t*)wsc, out, N, (size_t)M * N / 4,
-                       p.splits);
+    launch_splitk_sum(reinterpret_cast<const kbh_i32x4*>(acc),
+                      W8Out<OUT_I32>{out, (const uint16_t*)xs, (const uint16_t*)wsc, N}, M, N,
+                      p.ntiles, 128, p.splits, st);
   return launch_status();
 }
 
