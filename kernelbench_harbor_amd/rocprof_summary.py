@@ -43,7 +43,16 @@ def main() -> None:
     print("|---|---|---|---|---|---|---|---|")
     for r in rows:
         short = r["kernel"].replace("(anonymous namespace)::", "").replace("void ", "")
-        short = short.split("(")[0]
+        # drop the argument list: the last top-level "(...)" (template arguments may hold
+        # parentheses, as in "float __vector(4)")
+        depth, cut = 0, len(short)
+        for i, ch in enumerate(short):
+            depth += ch == "<"
+            depth -= ch == ">"
+            if ch == "(" and depth == 0:
+                cut = i
+                break
+        short = short[:cut].rstrip()
         print(f"| `{short}` | {r['grid_threads'][0]}x{r['grid_threads'][1]} | {r['workgroup']} | "
               f"{r['calls']} | {r['avg_us']:.2f} | {r['median_us']:.2f} | {r['min_us']:.2f} | "
               f"{r['max_us']:.2f} |")
