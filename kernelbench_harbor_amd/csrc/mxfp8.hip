@@ -13,7 +13,9 @@
 //
 // Kernel: 256 threads (2x2 waves), tile 128 x (64*WNT), K in 128-deep slabs (4 scale blocks)
 // held in a two-slab register ring, two LDS buffers with 144-byte rows (conflict-free 16-byte
-// fragment reads). Each wave computes 64 x (32*WNT) with 2 x WNT MFMA tiles. For small M the K
+// fragment reads). Each wave computes 64 x (32*WNT) with 2 x WNT MFMA tiles; per slab the LDS
+// stores of the next slab, the fragment reads of the next K step and the global loads are
+// interleaved with the MFMAs (one barrier per slab). For small M the K
 // range is split over gridDim.z; each split stores its partial tile into its own fp32 workspace
 // slice and splitk_sum_half (splitk.h) adds the slices in split order and converts.
 #include "kbh_common.h"
@@ -44,6 +46,9 @@ __global__ __launch_bounds__(256) void mxfp8_kernel(
   constexpr int XBN = 64 * WNT;
   __shared__ __attribute__((aligned(16))) uint8_t Al[2][XBM * XLD];
   __shared__ __attribute__((aligned(16))) uint8_t Bl[2][XBN * XLD];
+  // e8m0 scale dwords of the slab (4 blocks of 32 along K per row): A rows, then B rows (and
+  // 128 unused dwords that waves 2-3 write so the store needs no branch).
+  __shared__ uint32_t Sl[2][XBM + XBN + XBM];
 
   const int t = threadIdx.x;
   const int lane = t & 63, wave = t >> 6;
@@ -57,54 +62,72 @@ __global__ __launch_bounds__(256) void mxfp8_kernel(
   const int kt_begin = split * slabs_per_split;
   const int KT = slabs_per_split;
 
-  // global -> register mapping: 16-byte chunk t%8 of rows t/8 + 32i
+  // global -> register mapping: 16-byte chunk t%8 of rows t/8 + 32i. Buffer loads: one VGPR
+  // offset per matrix plus the uniform row/k offset in an SGPR; A rows past M (offsets past
+  // the end of a) read as zero and are never stored.
   const int ch = t & 7, rr = t >> 3;
-  const uint8_t* arow[4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int r = m0 + rr + 32 * i;
-    arow[i] = a + (size_t)(r < M ? r : M - 1) * K + ch * 16;  // rows >= M are never stored
-  }
-  const uint8_t* brow[WNT * 2];
-#pragma unroll
-  for (int i = 0; i < 2 * WNT; ++i) brow[i] = b + (size_t)(n0 + rr + 32 * i) * K + ch * 16;
-  // scale rows of this lane: A row tiles i < 2, B column tiles j < WNT
   const int fr = lane & 31, fg = lane >> 5;
-  const uint8_t* asrow[2];
-#pragma unroll
-  for (int i = 0; i < 2; ++i) {
-    const int r = m0 + wm * 64 + i * 32 + fr;
-    asrow[i] = as + (size_t)(r < M ? r : M - 1) * KS;
-  }
-  const uint8_t* bsrow[WNT];
-#pragma unroll
-  for (int j = 0; j < WNT; ++j) bsrow[j] = bs + (size_t)(n0 + wn * 32 * WNT + j * 32 + fr) * KS;
+  const __amdgpu_buffer_rsrc_t ra = make_rsrc(a, (size_t)M * K);
+  const __amdgpu_buffer_rsrc_t rb = make_rsrc(b, (size_t)N * K);
+  // Scale rows of the slab: waves 0-1 (t < 128) load A row t and B row 128 + t (read only for
+  // 256-row B tiles), waves 2-3 load B row t - 128 (and an unused dword). The choice of matrix
+  // is uniform per wave, so it selects the buffer resource and the loop body has no branch.
+  const bool sa_wave = __builtin_amdgcn_readfirstlane(t) < XBM;
+  const __amdgpu_buffer_rsrc_t rs0 =
+      make_rsrc(sa_wave ? (const void*)as : (const void*)bs, (size_t)(sa_wave ? M : N) * KS);
+  const __amdgpu_buffer_rsrc_t rsb = make_rsrc(bs, (size_t)N * KS);  // rows past N read as 0
+  const uint32_t va = (uint32_t)((m0 + rr) * K + ch * 16);
+  const uint32_t vb = (uint32_t)((n0 + rr) * K + ch * 16);
+  const uint32_t vs0 = sa_wave ? (uint32_t)((m0 + t) * KS) : (uint32_t)((n0 + t - XBM) * KS);
+  const uint32_t vs1 = (uint32_t)((n0 + XBM + t) * KS);
 
   struct Slab {
     kbh_u32x4 a[4];
     kbh_u32x4 b[2 * WNT];
+    uint32_t s[2];
+  };
+  struct Scales {
     uint32_t sa[2];
     uint32_t sb[WNT];
   };
+  struct Frags {
+    kbh_u32x4 a0[2], a1[2], b0[WNT], b1[WNT];
+  };
   auto load = [&](Slab& sl, int kt) {
     const int k0 = (kt_begin + kt) * XBK;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) sl.a[i] = *reinterpret_cast<const kbh_u32x4*>(arow[i] + k0);
-#pragma unroll
-    for (int i = 0; i < 2 * WNT; ++i)
-      sl.b[i] = __builtin_nontemporal_load(reinterpret_cast<const kbh_u32x4*>(brow[i] + k0));
-#pragma unroll
-    for (int i = 0; i < 2; ++i) sl.sa[i] = *reinterpret_cast<const uint32_t*>(asrow[i] + k0 / 32);
-#pragma unroll
-    for (int j = 0; j < WNT; ++j) sl.sb[j] = *reinterpret_cast<const uint32_t*>(bsrow[j] + k0 / 32);
-  };
-  auto store = [&](const Slab& sl, int buf) {
+    // the scale dwords first: the oldest loads of the group, so waiting for them does not wait
+    // for the A/B data issued after them
+    sl.s[0] = __builtin_amdgcn_raw_buffer_load_b32(rs0, vs0, k0 / 32, 0);
+    if constexpr (XBN > XBM) sl.s[1] = __builtin_amdgcn_raw_buffer_load_b32(rsb, vs1, k0 / 32, 0);
 #pragma unroll
     for (int i = 0; i < 4; ++i)
-      *reinterpret_cast<kbh_u32x4*>(&Al[buf][(rr + 32 * i) * XLD + ch * 16]) = sl.a[i];
+      sl.a[i] = __builtin_bit_cast(kbh_u32x4, __builtin_amdgcn_raw_buffer_load_b128(ra, va, 32 * i * K + k0, 0));
 #pragma unroll
     for (int i = 0; i < 2 * WNT; ++i)
-      *reinterpret_cast<kbh_u32x4*>(&Bl[buf][(rr + 32 * i) * XLD + ch * 16]) = sl.b[i];
+      sl.b[i] = __builtin_bit_cast(kbh_u32x4, __builtin_amdgcn_raw_buffer_load_b128(rb, vb, 32 * i * K + k0, kBufNT));
+  };
+  // LDS stores of a slab in 4 parts (A chunks, then B chunks), interleaved with MFMAs.
+  constexpr int NCH = 4 + 2 * WNT;  // 16-byte chunks per thread
+  auto store_part = [&](const Slab& sl, int buf, int p) {
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) {
+      if (c * 4 / NCH != p) continue;
+      if (c < 4)
+        *reinterpret_cast<kbh_u32x4*>(&Al[buf][(rr + 32 * c) * XLD + ch * 16]) = sl.a[c];
+      else
+        *reinterpret_cast<kbh_u32x4*>(&Bl[buf][(rr + 32 * (c - 4)) * XLD + ch * 16]) = sl.b[c - 4];
+    }
+    if (p == 3) {
+      Sl[buf][t] = sl.s[0];  // A row t, or B row t - 128 at index 128 + (t - 128)
+      if constexpr (XBN > XBM) Sl[buf][2 * XBM + t] = sl.s[1];  // B row 128 + t (t < 128)
+    }
+  };
+  // This wave's scale dwords of the slab in LDS buffer buf.
+  auto read_scales = [&](Scales& sc, int buf) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i) sc.sa[i] = Sl[buf][wm * 64 + i * 32 + fr];
+#pragma unroll
+    for (int j = 0; j < WNT; ++j) sc.sb[j] = Sl[buf][XBM + wn * 32 * WNT + j * 32 + fr];
   };
 
   kbh_f32x16 accv[2][WNT];
@@ -115,57 +138,81 @@ __global__ __launch_bounds__(256) void mxfp8_kernel(
 #pragma unroll
       for (int e = 0; e < 16; ++e) accv[i][j][e] = 0.f;
 
-  // One 64-deep K step (kk = 0, 1 within the slab). Scale byte 2*kk + g of the slab's dword.
-  auto mma_k64 = [&](int buf, int kk, const Slab& sl) {
+  // Fragments of one 64-deep K step (kk = 0, 1 within the slab) from LDS buffer buf.
+  auto read_frags = [&](Frags& f, int buf, int kk) {
     const uint8_t* Ab = &Al[buf][(wm * 64 + fr) * XLD + kk * 64 + 16 * fg];
     const uint8_t* Bb = &Bl[buf][(wn * 32 * WNT + fr) * XLD + kk * 64 + 16 * fg];
-    kbh_u32x4 a0[2], a1[2], b0[WNT], b1[WNT];
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
-      a0[i] = *reinterpret_cast<const kbh_u32x4*>(Ab + i * 32 * XLD);
-      a1[i] = *reinterpret_cast<const kbh_u32x4*>(Ab + i * 32 * XLD + 32);
+      f.a0[i] = *reinterpret_cast<const kbh_u32x4*>(Ab + i * 32 * XLD);
+      f.a1[i] = *reinterpret_cast<const kbh_u32x4*>(Ab + i * 32 * XLD + 32);
     }
 #pragma unroll
     for (int j = 0; j < WNT; ++j) {
-      b0[j] = *reinterpret_cast<const kbh_u32x4*>(Bb + j * 32 * XLD);
-      b1[j] = *reinterpret_cast<const kbh_u32x4*>(Bb + j * 32 * XLD + 32);
+      f.b0[j] = *reinterpret_cast<const kbh_u32x4*>(Bb + j * 32 * XLD);
+      f.b1[j] = *reinterpret_cast<const kbh_u32x4*>(Bb + j * 32 * XLD + 32);
     }
+  };
+  // MFMAs q in [lo, hi) of step kk (q = i * WNT + j); scale byte 2*kk + g of the slab's dword.
+  auto mma_range = [&](const Frags& f, int kk, const Scales& sc, int lo, int hi) {
     const int sh = 8 * (2 * kk + fg);
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const int sa = (int)((sl.sa[i] >> sh) & 0xffu);
-#pragma unroll
-      for (int j = 0; j < WNT; ++j) {
-        const int sb = (int)((sl.sb[j] >> sh) & 0xffu);
-        accv[i][j] = mfma_mx32(a0[i], a1[i], b0[j], b1[j], accv[i][j], sa, sb);
-      }
+    for (int q = 0; q < 2 * WNT; ++q) {
+      if (q < lo || q >= hi) continue;
+      const int i = q / WNT, j = q % WNT;
+      const int sa = (int)((sc.sa[i] >> sh) & 0xffu);
+      const int sb = (int)((sc.sb[j] >> sh) & 0xffu);
+      accv[i][j] = mfma_mx32(f.a0[i], f.a1[i], f.b0[j], f.b1[j], accv[i][j], sa, sb);
     }
   };
 
-  // Ring of XDEPTH slabs; the scales of slab kt stay in `cur` while its data sits in LDS.
+  // Ring of XDEPTH slabs in registers (slab s is loaded two iterations before it is stored to
+  // LDS); LDS buffer s & 1 holds slab s. Per slab: step-1 fragments are read, the step-0 MFMAs
+  // run interleaved with the LDS stores of slab s+1, one barrier, then the step-0 fragments of
+  // slab s+1 are read while the step-1 MFMAs run interleaved with the global loads of slab s+3.
   Slab ring[XDEPTH];
-  Slab cur;
+  Frags f0, f1;
 #pragma unroll
   for (int d = 0; d < XDEPTH; ++d) load(ring[d], min(d, KT - 1));
-  store(ring[0], 0);
-  cur = ring[0];
+#pragma unroll
+  for (int p = 0; p < 4; ++p) store_part(ring[0], 0, p);
   load(ring[0], min(XDEPTH, KT - 1));
   __syncthreads();
+  Scales scur;
+  read_scales(scur, 0);
+  read_frags(f0, 0, 0);
+  constexpr int NMF = 2 * WNT;  // MFMAs per step
   for (int kt0 = 0; kt0 < KT; kt0 += XDEPTH) {
 #pragma unroll
     for (int d = 0; d < XDEPTH; ++d) {
       // KT is a multiple of XDEPTH: no branch here (see tiled_f16.h on wait counts).
       const int kt = kt0 + d;
+      const int cur = kt & 1;
       const int nxt = (d + 1) % XDEPTH;
-      mma_k64(kt & 1, 0, cur);
-      store(ring[nxt], (kt + 1) & 1);  // after the last slab: unused buffer
-      mma_k64(kt & 1, 1, cur);
-      cur.sa[0] = ring[nxt].sa[0];
-      cur.sa[1] = ring[nxt].sa[1];
+      read_frags(f1, cur, 1);
+      __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-      for (int j = 0; j < WNT; ++j) cur.sb[j] = ring[nxt].sb[j];
-      load(ring[nxt], min(kt + 1 + XDEPTH, KT - 1));
+      for (int p = 0; p < 4; ++p) {
+        mma_range(f0, 0, scur, p * NMF / 4, (p + 1) * NMF / 4);
+        __builtin_amdgcn_sched_barrier(0);
+        store_part(ring[nxt], 1 - cur, p);  // slab kt+1 (after the last: unused buffer)
+        __builtin_amdgcn_sched_barrier(0);
+      }
       __syncthreads();
+      __builtin_amdgcn_sched_barrier(0);
+      Scales snext;
+      read_scales(snext, 1 - cur);  // slab kt+1
+      read_frags(f0, 1 - cur, 0);   // step 0 of slab kt+1
+      mma_range(f1, 1, scur, 0, NMF);
+      load(ring[nxt], min(kt + 1 + XDEPTH, KT - 1));
+#pragma unroll
+      for (int q = 0; q < NMF; ++q) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);  // one MFMA
+        __builtin_amdgcn_sched_group_barrier(0x020, 2, 1);  // two VMEM reads
+        __builtin_amdgcn_sched_group_barrier(0x100, 2, 1);  // two LDS reads
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      scur = snext;
     }
   }
 
@@ -248,6 +295,8 @@ extern "C" int kbh_mxfp8_gemm(const uint8_t* a, const uint8_t* a_scale, const ui
   if (out_dtype != KBH_F16 && out_dtype != KBH_BF16) return KBH_ERR_DTYPE;
   if (M < 1 || N < 64 || (N % 64) != 0 || K < XBK * XDEPTH || (K % (XBK * XDEPTH)) != 0)
     return KBH_ERR_SHAPE;
+  // The kernel addresses a and b with 32-bit buffer offsets.
+  if ((size_t)M * K >= 0x80000000u || (size_t)N * K >= 0x80000000u) return KBH_ERR_SHAPE;
   if (!aligned16(a) || !aligned16(b) || !aligned16(y) || (reinterpret_cast<uintptr_t>(a_scale) & 3) ||
       (reinterpret_cast<uintptr_t>(b_scale) & 3))
     return KBH_ERR_ALIGN;
