@@ -278,9 +278,12 @@ __global__ __launch_bounds__(256) void moe_gemm_kernel(const uint16_t* __restric
       const int kt = kt0 + d;
       const int nxt = (d + 1) % TDEPTH;
       mma(kt & 1);
-      store(ring[nxt], (kt + 1) & 1);  // after the last slab: unused buffer
+      __builtin_amdgcn_sched_barrier(0);  // phases in order (see tiled_f16.h)
+      store(ring[nxt], (kt + 1) & 1);     // after the last slab: unused buffer
+      __builtin_amdgcn_sched_barrier(0);
       load(ring[nxt], min(kt + 1 + TDEPTH, KT - 1));
       __syncthreads();
+      __builtin_amdgcn_sched_barrier(0);
     }
   }
 

@@ -106,12 +106,20 @@ __global__ __launch_bounds__(256) void tiled_f16_gemm(const uint16_t* __restrict
       const int kt = kt0 + d;
       const int nxt = (d + 1) % TDEPTH;  // ring stage of slab kt+1
       // After the last slab the other buffer is written but never read.
+      // Scheduling fences keep each slab's phases in this order: unfenced, the scheduler
+      // hoists the stores (and the weight producer's VALU) of all TDEPTH unrolled slabs to the
+      // top of the loop, which waits for the most recent loads and drains the prefetch ring.
       mma_k16(kt & 1, 0);
+      __builtin_amdgcn_sched_barrier(0);
       store_a(ring[nxt], (kt + 1) & 1);
+      __builtin_amdgcn_sched_barrier(0);
       mma_k16(kt & 1, 1);
+      __builtin_amdgcn_sched_barrier(0);
       bp.store(ring[nxt].b, Bs[(kt + 1) & 1], t);
+      __builtin_amdgcn_sched_barrier(0);
       load(ring[nxt], min(kt + 1 + TDEPTH, KT - 1));
       __syncthreads();
+      __builtin_amdgcn_sched_barrier(0);
     }
   }
 
