@@ -241,8 +241,9 @@ void dispatch_decode(const DecodePlan& p, const void* x, const int32_t* qw, cons
 // Large-M kernels
 // ======================================================================================
 // Above kWideMinM rows the wide-tile kernel (tiled_wide.h) takes over from the split-K decode
-// kernel: up to 128 rows, 128 x 256 tiles with one workgroup per CU (128 x 128 tiles, two per
-// CU, when N is not a multiple of 256); 256 x 256 tiles above. The 256-column tiles run with a
+// kernel: up to 64 rows, 64 x 256 tiles with two workgroups per CU; up to 128 rows, 128 x 256
+// tiles with one workgroup per CU (128 x 128 tiles, two per CU, when N is not a multiple of
+// 256); 256 x 256 tiles above. The 256-column tiles run with a
 // 4-slab prefetch ring. The older 256 x 128 LDS-staged kernel remains for shapes the wide kernel
 // does not cover.
 constexpr int kWideMinM = 33;
@@ -265,8 +266,11 @@ bool plan_w4_wide(int M, int N, int K, int group, W4Wide* w) {
   if (!small && w->tn != 256) return false;
   const int pd = w4_wide_pd(w->tn);
   const int unroll = 2 * w->spg > pd ? 2 * w->spg : pd;  // the kernel's slabs per iteration
-  return plan_wide(M, N, K, w->tn, 32, unroll, w->tn == 128 ? 512 : 256, &w->plan, 128,
-                   w->tn == 256);
+  // Up to 64 rows with 256-column tiles: 64 x 256 tiles (2 x 2 waves of 32 x 128, two
+  // workgroups per CU); a 128-row tile would spend half its MFMAs and A loads on padding.
+  const bool rows64 = M <= 64 && w->tn == 256;
+  return plan_wide(M, N, K, w->tn, 32, unroll, (w->tn == 128 || rows64) ? 512 : 256, &w->plan,
+                   rows64 ? 64 : 128, w->tn == 256);
 }
 
 template <bool BF16, int TM, int TN, int SPG>
@@ -276,10 +280,11 @@ void launch_w4_wide(const W4Wide& w, const void* x, const int32_t* qw, const voi
   using BP = W4WidePolicy<BF16, TN>;
   using EP = HalfOut<BF16>;
   constexpr int MINB = (TM == 128 && TN == 256) ? 1 : 0;
+  constexpr int WM = TM == 64 ? 2 : 4;  // waves along M
   const BP bp{(const uint32_t*)qw, (const uint16_t*)s, (const uint16_t*)z, N, group, 0, 0,
               0x000F000Fu};
   const EP ep{(uint16_t*)y, N};
-  hipLaunchKernelGGL((tiled_wide_gemm<E, TM, 4, SPG, BP, EP, DenseRows, MINB, w4_wide_pd(TN)>),
+  hipLaunchKernelGGL((tiled_wide_gemm<E, TM, WM, SPG, BP, EP, DenseRows, MINB, w4_wide_pd(TN)>),
                      dim3(w.plan.grid), dim3(256), 0, st,
                      x, bp, ep, scratch, M, N, K, w.plan.splits, w.plan.slabs_per_split,
                      DenseRows{M});
@@ -308,6 +313,8 @@ void dispatch_w4_wide(const W4Wide& w, const void* x, const int32_t* qw, const v
                       hipStream_t st) {
   if (w.plan.tm == 256)
     dispatch_w4_wide_spg<BF16, 256, 256>(w, x, qw, s, z, y, scratch, M, N, K, group, st);
+  else if (w.plan.tm == 64)
+    dispatch_w4_wide_spg<BF16, 64, 256>(w, x, qw, s, z, y, scratch, M, N, K, group, st);
   else if (w.tn == 256)
     dispatch_w4_wide_spg<BF16, 128, 256>(w, x, qw, s, z, y, scratch, M, N, K, group, st);
   else
