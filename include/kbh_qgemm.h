@@ -124,7 +124,8 @@ int kbh_fp8w_gemm(const void* x, const uint8_t* w_fp8, const void* scales, void*
  *   a [M, K] e4m3fn codes, a_scale [M, K/32] e8m0 codes
  *   b [N, K] e4m3fn codes, b_scale [N, K/32] e8m0 codes
  *   y [M, N] out_dtype,  y[m, n] = sum_k a[m,k] 2^(a_scale[m,k/32]-127) b[n,k] 2^(b_scale[n,k/32]-127)
- * Requirements: M >= 1, N % 64 == 0, K % 256 == 0, a/b/y 16-byte and scales 4-byte aligned.
+ * Requirements: M >= 1, N % 64 == 0, K % 256 == 0, M*K and N*K below 2^31 (32-bit buffer
+ * offsets), a/b/y 16-byte and scales 4-byte aligned.
  * workspace: used when K is split across workgroups (small M); same contract as for
  * kbh_w4a16_gemm, size from kbh_mxfp8_workspace_bytes().
  */

@@ -59,6 +59,11 @@ def test_host_checks_run_without_gpu():
     need = lib.kbh_w8a8_scratch_bytes(512, 4096, 14336)
     assert need >= 512 * 4096 * 4 * 2
     assert lib.kbh_w8a8_gemm(p, p, p, p, p, p, 1 << 20, p, need - 1, 512, 4096, 14336, None) == _lib.KBH_ERR_WORKSPACE
+    # MXFP8: K % 256, N % 64, and the 32-bit operand offsets (M*K, N*K < 2^31)
+    assert lib.kbh_mxfp8_gemm(p, p, p, p, p, p, 1 << 20, 128, 4096, 14300, 0, None) == _lib.KBH_ERR_SHAPE
+    assert lib.kbh_mxfp8_gemm(p, p, p, p, p, p, 1 << 20, 128, 4000, 14336, 0, None) == _lib.KBH_ERR_SHAPE
+    assert lib.kbh_mxfp8_gemm(p, p, p, p, p, p, 1 << 20, 1 << 18, 4096, 8192, 0, None) == _lib.KBH_ERR_SHAPE
+    assert lib.kbh_mxfp8_gemm(p, p, p, p, p, p, 1 << 20, 128, 1 << 18, 8192, 0, None) == _lib.KBH_ERR_SHAPE
 
 
 def test_workspace_sizes():
