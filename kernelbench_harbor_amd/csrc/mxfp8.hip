@@ -54,8 +54,17 @@ __global__ __launch_bounds__(256) void mxfp8_kernel(
   const int lane = t & 63, wave = t >> 6;
   const int wm = wave >> 1, wn = wave & 1;
   const int ntn = N / XBN;
+  // Tile order: groups of up to 8 row blocks, rows fastest within a group, so the 32 tiles an
+  // XCD runs (consecutive ids after xcd_remap) form an 8 x 4 block that shares A rows and B
+  // columns in its L2 (row-major order would give each XCD 2 x 16 tiles and make every XCD
+  // stream all of B).
   const int id = xcd_remap(blockIdx.x, gridDim.x);
-  const int mb = id / ntn, nb = id - mb * ntn;
+  const int nmb = gridDim.x / ntn;
+  const int gm0 = nmb < 8 ? nmb : 8;
+  const int grp = id / (gm0 * ntn), first_m = grp * gm0;
+  const int gm = nmb - first_m < gm0 ? nmb - first_m : gm0;
+  const int r_in = id - grp * gm0 * ntn;
+  const int mb = first_m + r_in % gm, nb = r_in / gm;
   const int m0 = mb * XBM, n0 = nb * XBN;
   const int splits = gridDim.z, split = blockIdx.z;
   const int KS = K / 32;  // scale columns
