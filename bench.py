@@ -7,7 +7,8 @@ FLOPs of a step / wall time of a step (TFLOP/s).
 
 Also measured (reported under "configs", not part of `value`): W8A8 at M in {16, 512}, MXFP8 at
 M in {128, 2048}, the top-2 W4A16 MoE SiLU FFN (T=512, Mixtral layer), the reference qMoE op
-(T=256) and the reference FP8 weight-only op (M=16).
+(T=256), the reference FP8 weight-only op (M=16) and the reference fused SiLU + FP8 quantisation
+(T=512, H=14336).
 
 Inputs are synthetic (seeded, BASELINE distributions) and resident in HBM before timing. Each
 configuration rotates over enough input copies (> 2x the 256 MB Infinity Cache) that every call
@@ -82,6 +83,15 @@ def qmoe_bytes(T=256, D=4096, N=14336, E=8, G=GROUP):
 
 def qmoe_flops(T=256, D=4096, N=14336):
     return 2 * T * 2 * D * N
+
+
+def silu_fp8_bytes(T=512, H=14336):
+    """gate and up (fp16/bf16) read once, the fp32 dequantised output written once."""
+    return T * 2 * H * 2 + T * H * 4
+
+
+def silu_fp8_flops(T=512, H=14336):
+    return 0   # elementwise: no MFMA term; the bound is HBM
 
 
 def roofline(seconds, by, fl, peak):
@@ -181,6 +191,7 @@ GRID_LINEAR = [("llama3_8b_qkv", 4096, 6144), ("llama3_8b_o", 4096, 4096),
                ("qwen2_7b_gate", 3584, 18944), ("qwen2_72b_down", 29568, 8192)]
 GRID_QMOE = [("deepseek_moe", 2048, 64, 1408), ("mixtral", 4096, 8, 14336),
              ("qwen_moe", 2048, 60, 1408)]
+GRID_SILU = [("deepseek_moe", 1408), ("qwen_moe", 2560), ("mixtral", 14336)]   # generate_tasks.py:351-355
 
 
 def run_grid(torch, dev, inputs, ops):
@@ -222,6 +233,12 @@ def run_grid(torch, dev, inputs, ops):
             one(f"qmoe {n} {str(dt)[6:]}",
                 lambda: [t.to(dev) for t in inputs.qmoe(256, D, E, N, dt, seed=1)],
                 ops.qmoe, by, qmoe_flops(256, D, N), PEAK["f16"], by, T=256, D=D, E=E, N=N)
+    for (n, H) in GRID_SILU:
+        for T, dt in ((256, f16), (512, f16), (512, bf16)):
+            by = silu_fp8_bytes(T, H)
+            one(f"silu_fp8 {n} T={T} {str(dt)[6:]}",
+                lambda: [t.to(dev) for t in inputs.silu_fp8(T, H, dt, seed=1)],
+                ops.silu_fp8_quant, by, 0, PEAK["f16"], by, T=T, H=H)
     return recs
 
 
@@ -390,6 +407,13 @@ def main():
         ts, bm = time_config(torch, ops.qmoe_ffn, s_, 10, 10)
         configs.append(record("qmoe_ffn T=512 D=4096 F=14336 E=8 top2", ts, bm, ffn_bytes(),
                               ffn_flops(), PEAK["f16"], T=512))
+        del s_
+        torch.cuda.empty_cache()
+        s_ = rotation(lambda: [t.to(dev) for t in inputs.silu_fp8(512, 14336, torch.float16, 0)],
+                      silu_fp8_bytes())
+        ts, bm = time_config(torch, ops.silu_fp8_quant, s_, it, bt)
+        configs.append(record("silu_fp8 (reference op) T=512 H=14336 g128", ts, bm,
+                              silu_fp8_bytes(), 0, PEAK["f16"], T=512, H=14336))
         del s_
         torch.cuda.empty_cache()
         s_ = [[t.to(dev) for t in inputs.qmoe(seed=0)]]       # 470 MB of weights

@@ -172,6 +172,24 @@ int kbh_qmoe_ffn(const void* x, const void* router_logits, int logits_dtype,
                  void* y, void* workspace, size_t workspace_bytes, int T, int D, int F, int E,
                  int group, int dtype, void* stream);
 
+/* ---------------------------------------------------------------------------------------
+ * Fused SiLU x up with per-group dynamic FP8 (e4m3fn) quantisation.
+ * Replaces tasks/fused_silu_fp8/fused_silu_fp8__mixtral__T512__fp16/environment/reference.py:13-23
+ * (Model.forward(y)); template generate_tasks.py:321-348.
+ *
+ *   y [T, 2H] dtype = concat(gate, up) along columns
+ *   act = fp32(silu(fp32(gate)) * fp32(up)); per row and per `group` consecutive columns:
+ *   scale = max(amax(|act|) / 448, 1e-12); q = e4m3fn_rne(clamp(act / scale, -448, 448))
+ *   out      [T, H] float32 = fp32(q) * scale   (the reference's output)
+ *   q_codes  [T, H] e4m3fn codes, or NULL       (optional: the FP8 GEMM operand)
+ *   q_scales [T, H/group] float32, or NULL      (optional: its per-group scales)
+ * A NaN anywhere in a group makes its scale and every output of the group NaN, as in torch.
+ * Requirements: T >= 0, group in {32, 64, 128}, H % group == 0, y/out 16-byte aligned, q_codes
+ * 8-byte and q_scales 4-byte aligned. No workspace.
+ */
+int kbh_silu_fp8_quant(const void* y, float* out, uint8_t* q_codes, float* q_scales, int T, int H,
+                       int group, int dtype, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -148,3 +148,9 @@ def qmoe_ffn(T: int = 512, D: int = 4096, F: int = 14336, E: int = 8, group: int
         z = torch.randint(0, 16, (E, K // group, Nc), generator=g).to(dtype)
         return [q, s, z]
     return [x, logits] + w4(D, F) + w4(D, F) + w4(F, D)
+
+
+def silu_fp8(T: int = 512, H: int = 14336, dtype: torch.dtype = torch.float16, seed: int = 0):
+    """[y]: y [T, 2H] ~ N(0, 1) in dtype, as tasks/fused_silu_fp8/*/environment/reference.py:25-28."""
+    g = _gen(seed)
+    return [torch.randn(T, 2 * H, generator=g).to(dtype)]

@@ -79,3 +79,14 @@ class QMoEFFNModel(nn.Module):
                 up_scales, up_zeros, down_qweight, down_scales, down_zeros):
         return ops.qmoe_ffn(x, router_logits, gate_qweight, gate_scales, gate_zeros, up_qweight,
                             up_scales, up_zeros, down_qweight, down_scales, down_zeros)
+
+
+class FusedSiluFP8Model(nn.Module):
+    """Fused SiLU x up + per-group (128) dynamic FP8 quantisation, returned dequantised.
+
+    Reference: tasks/fused_silu_fp8/*/environment/reference.py:13-23,
+    forward(y [T, 2H] fp16/bf16) -> [T, H] float32.
+    """
+
+    def forward(self, y):
+        return ops.silu_fp8_quant(y, 128)

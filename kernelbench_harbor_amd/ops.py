@@ -330,3 +330,39 @@ def qmoe_ffn(x, router_logits, gate_qweight, gate_scales, gate_zeros, up_qweight
                           _DT_CODE[x.dtype], _stream_ptr(dev))
     _lib.check(st, "kbh_qmoe_ffn")
     return y
+
+
+def silu_fp8_quant(y: torch.Tensor, group: int = 128, return_codes: bool = False):
+    """Fused SiLU x up with per-group dynamic e4m3fn quantisation, returned dequantised.
+
+    Follows tasks/fused_silu_fp8/fused_silu_fp8__mixtral__T512__fp16/environment/reference.py:13-23:
+    y [T, 2H] = concat(gate, up); act = silu(fp32 gate) * fp32 up; per `group` columns
+    scale = max(amax|act| / 448, 1e-12), q = e4m3fn(clamp(act / scale, +-448));
+    returns fp32(q) * scale as float32 [T, H]. With ``return_codes`` also returns the codes
+    (torch.float8_e4m3fn [T, H]) and the scales (float32 [T, H / group]).
+    """
+    _require(y.dtype in _DT_CODE, f"y must be float16 or bfloat16, got {y.dtype}")
+    _require(y.dim() == 2, f"y must be 2-D [T, 2H], got {tuple(y.shape)}")
+    T, H2 = y.shape
+    _require(H2 % 2 == 0, f"y's last dim {H2} must be even (gate and up halves)")
+    H = H2 // 2
+    _require(group in (32, 64, 128), f"group must be 32, 64 or 128, got {group}")
+    # the reference's reshape(T, H // GROUP, GROUP) raises for any other H
+    _require(H % group == 0, f"H={H} must be a multiple of the group size {group}")
+    dev = _check_device(y)
+    out = torch.empty((T, H), dtype=torch.float32, device=dev)
+    codes = scales = None
+    if return_codes:
+        codes = torch.empty((T, H), dtype=torch.uint8, device=dev)
+        scales = torch.empty((T, H // group), dtype=torch.float32, device=dev)
+    if T > 0 and H > 0:
+        lib = _lib.load()
+        yc = y.contiguous()
+        st = lib.kbh_silu_fp8_quant(yc.data_ptr(), out.data_ptr(),
+                                    codes.data_ptr() if return_codes else None,
+                                    scales.data_ptr() if return_codes else None,
+                                    T, H, group, _DT_CODE[y.dtype], _stream_ptr(dev))
+        _lib.check(st, "kbh_silu_fp8_quant")
+    if return_codes:
+        return out, codes.view(torch.float8_e4m3fn), scales
+    return out

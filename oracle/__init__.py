@@ -24,4 +24,9 @@ modules' op sequences on small seeded inputs; the reference itself ships none):
   qmoe          top-2 closed form w1 = 1/(1+exp(l2-l1)), dense-vs-sparse equivalence on tiny
                 shapes, brute-force loops.
   qmoe_ffn      brute-force per-token loops on tiny shapes; SiLU closed form.
+  silu_fp8      golden vectors (torch CPU ops of the reference sequence); silu(x) = x exactly
+                for x >= 17 (e^-x < 2^-24), so act is exact there; the group's absmax element
+                quantises to +-448; power-of-two scales make act/scale exact, so crafted values
+                on and between e4m3 grid points (ties) pin the RNE codes; |out - act| within
+                half an e4m3 step of each group.
 """

@@ -11,11 +11,16 @@ move with the installed torch. The sequences follow:
   FP8     tasks/fp8_microscale/<task>/environment/reference.py:9-12
   MXFP8   generate_tasks.py:337-342 (amax/448, e4m3fn cast) with a power-of-two block scale
   qMoE    tasks/fused_qmoe/<task>/environment/reference.py:14-21
+  SiLU-FP8 tasks/fused_silu_fp8/<task>/environment/reference.py:13-23
+
+`python tests/golden/make_golden.py [name ...]` rewrites only the named files (default: all);
+each file draws from its own seeded generator, so one can be rewritten without the others.
 """
 from __future__ import annotations
 
 import json
 import os
+import sys
 
 import numpy as np
 import torch
@@ -97,21 +102,57 @@ def qmoe_route(g):
     return dict(logits=_np(logits), topi=_np(topi), topw=_np(w))
 
 
+def silu_fp8(g):
+    """Two rows each in fp16 and bf16 (H = 256, group 128) at several magnitudes, one fp16 row of
+    zeros (amax 0: scale clamps to 1e-12, codes 0) and one with large gates (silu(x) = x)."""
+    import torch.nn.functional as F
+    T, H, G = 6, 256, 128
+    mag = torch.tensor([1.0, 0.01, 30.0, 1.0, 0.0, 1.0]).unsqueeze(1)
+    y = torch.randn(T, 2 * H, generator=g) * mag
+    y[5, :H] = torch.rand(H, generator=g) * 64 + 20
+    out = {}
+    for name, dt in (("f16", torch.float16), ("bf16", torch.bfloat16)):
+        yt = y.to(dt)
+        gate, up = yt[:, :H], yt[:, H:]
+        act = F.silu(gate.float()) * up.float()
+        a = act.reshape(T, H // G, G)
+        scale = (a.abs().amax(dim=-1, keepdim=True) / 448.0).clamp(min=1e-12)
+        q = (a / scale).clamp(-448.0, 448.0).to(torch.float8_e4m3fn)
+        deq = (q.float() * scale).reshape(T, H)
+        out.update({f"y_{name}": _np(yt.float()), f"act_{name}": _np(act),
+                    f"codes_{name}": _np(q.view(torch.uint8).reshape(T, H)),
+                    f"scales_{name}": _np(scale.reshape(T, H // G)), f"out_{name}": _np(deq)})
+    return out
+
+
 def e4m3fn_table():
     v = torch.arange(256, dtype=torch.uint8).view(torch.float8_e4m3fn).float()
     return ["nan" if np.isnan(a) else float(a).hex() for a in v.tolist()]
 
 
-def main():
-    g = torch.Generator().manual_seed(20240611)
-    for name, fn in (("w4a16", w4a16), ("w8a8", w8a8), ("fp8w", fp8w), ("mxfp8", mxfp8),
-                     ("qmoe_route", qmoe_route)):
-        np.savez(os.path.join(HERE, f"{name}.npz"), **fn(g))
-    with open(os.path.join(HERE, "e4m3fn_table.json"), "w") as f:
-        json.dump({"source": "torch.float8_e4m3fn -> float32, codes 0..255",
-                   "values": e4m3fn_table()}, f, indent=0)
-        f.write("\n")
+SEEDS = {"w4a16": 20240611, "silu_fp8": 20240612}
+SETS = (("w4a16", w4a16), ("w8a8", w8a8), ("fp8w", fp8w), ("mxfp8", mxfp8),
+        ("qmoe_route", qmoe_route))
+
+
+def main(names=()):
+    names = set(names) or {n for n, _ in SETS} | {"silu_fp8", "e4m3fn_table"}
+    # The first five sets share one generator, drawn in this order (as first written).
+    if names & {n for n, _ in SETS}:
+        g = torch.Generator().manual_seed(SEEDS["w4a16"])
+        for name, fn in SETS:
+            d = fn(g)
+            if name in names:
+                np.savez(os.path.join(HERE, f"{name}.npz"), **d)
+    if "silu_fp8" in names:
+        g = torch.Generator().manual_seed(SEEDS["silu_fp8"])
+        np.savez(os.path.join(HERE, "silu_fp8.npz"), **silu_fp8(g))
+    if "e4m3fn_table" in names:
+        with open(os.path.join(HERE, "e4m3fn_table.json"), "w") as f:
+            json.dump({"source": "torch.float8_e4m3fn -> float32, codes 0..255",
+                       "values": e4m3fn_table()}, f, indent=0)
+            f.write("\n")
 
 
 if __name__ == "__main__":
-    main()
+    main(sys.argv[1:])

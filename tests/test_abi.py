@@ -65,6 +65,15 @@ def test_host_checks_run_without_gpu():
     assert lib.kbh_mxfp8_gemm(p, p, p, p, p, p, 1 << 20, 1 << 18, 4096, 8192, 0, None) == _lib.KBH_ERR_SHAPE
     assert lib.kbh_mxfp8_gemm(p, p, p, p, p, p, 1 << 20, 128, 1 << 18, 8192, 0, None) == _lib.KBH_ERR_SHAPE
 
+    # fused SiLU + FP8 quantisation: group, divisibility, dtype, alignment; T = 0 is a no-op
+    assert lib.kbh_silu_fp8_quant(None, p, None, None, 4, 256, 128, 0, None) == _lib.KBH_ERR_NULL
+    assert lib.kbh_silu_fp8_quant(p, p, None, None, 4, 256, 100, 0, None) == _lib.KBH_ERR_SHAPE
+    assert lib.kbh_silu_fp8_quant(p, p, None, None, 4, 320, 128, 0, None) == _lib.KBH_ERR_SHAPE
+    assert lib.kbh_silu_fp8_quant(p, p, None, None, 4, 256, 128, 5, None) == _lib.KBH_ERR_DTYPE
+    assert lib.kbh_silu_fp8_quant(p, ctypes.c_void_p(20), None, None, 4, 256, 128, 0, None) == _lib.KBH_ERR_ALIGN
+    assert lib.kbh_silu_fp8_quant(p, p, ctypes.c_void_p(20), None, 4, 256, 128, 0, None) == _lib.KBH_ERR_ALIGN
+    assert lib.kbh_silu_fp8_quant(p, p, None, None, 0, 256, 128, 0, None) == _lib.KBH_OK
+
 
 def test_workspace_sizes():
     lib = _lib.load()

@@ -72,3 +72,17 @@ def test_static_check_rules():
     assert not ok
     ok, why = harness.static_check("import torch\n")
     assert not ok and "HIP library" in why
+
+
+def test_silu_fp8_rejects_bad_inputs():
+    y = torch.zeros(4, 512, dtype=torch.float16)
+    with pytest.raises(ValueError, match="float16 or bfloat16"):
+        ops.silu_fp8_quant(y.float())
+    with pytest.raises(ValueError, match="2-D"):
+        ops.silu_fp8_quant(y[0])
+    with pytest.raises(ValueError, match="multiple of the group"):
+        ops.silu_fp8_quant(torch.zeros(4, 2 * 200, dtype=torch.float16))
+    with pytest.raises(ValueError, match="group must be"):
+        ops.silu_fp8_quant(y, 100)
+    with pytest.raises(ValueError, match="HIP device"):
+        ops.silu_fp8_quant(y)
