@@ -173,6 +173,30 @@ int kbh_qmoe_ffn(const void* x, const void* router_logits, int logits_dtype,
                  int group, int dtype, void* stream);
 
 /* ---------------------------------------------------------------------------------------
+ * Top-k mixture of experts with fp16/bf16 expert weights.
+ * Replaces tasks/moe/moe_top2__mixtral_8x7b__T16__fp16/environment/reference.py:10-17
+ * (Model.forward(x, w, router_logits)); template generate_tasks.py:162-186 (top-k in
+ * {2, 6, 8}, generate_tasks.py:189-195).
+ *
+ *   x [T, D] dtype; w [E, D, H] dtype; router_logits [T, E] (logits_dtype: 0 fp16, 1 bf16, 2 fp32)
+ *   probs = softmax(fp32 logits); topi, topv = topk(probs) (descending; lower index first on a
+ *   tie); wk = dtype(topv / sum(topv));  y [T, H] dtype,
+ *   y[t] = dtype(sum_j fp32(dtype(dtype(x[t] @ w[topi[t, j]]) * wk[t, j])))
+ * Only the routed (token, expert) pairs are computed (the reference evaluates every expert).
+ * kbh_moe_route_topk runs the routing alone: topi [T, topk] int32, topw [T, topk] dtype.
+ * Requirements: E in [2, 256], 1 <= topk <= min(8, E), D a multiple of 128, H a multiple of 128,
+ * x/w/y 16-byte aligned. workspace >= kbh_moe_workspace_bytes(T, D, H, E, topk), no content
+ * requirement.
+ */
+size_t kbh_moe_workspace_bytes(int T, int D, int H, int E, int topk);
+int kbh_moe_route_topk(const void* router_logits, int logits_dtype, int32_t* topi, void* topw,
+                       void* workspace, size_t workspace_bytes, int T, int E, int topk, int dtype,
+                       void* stream);
+int kbh_moe(const void* x, const void* w, const void* router_logits, int logits_dtype, void* y,
+            void* workspace, size_t workspace_bytes, int T, int D, int H, int E, int topk,
+            int dtype, void* stream);
+
+/* ---------------------------------------------------------------------------------------
  * Fused SiLU x up with per-group dynamic FP8 (e4m3fn) quantisation.
  * Replaces tasks/fused_silu_fp8/fused_silu_fp8__mixtral__T512__fp16/environment/reference.py:13-23
  * (Model.forward(y)); template generate_tasks.py:321-348.

@@ -53,6 +53,9 @@ SIGNATURES = {
     "kbh_qmoe_ffn_workspace_bytes": (_sz, [_i, _i, _i, _i]),
     "kbh_qmoe_ffn": (_i, [_vp, _vp, _i] + [_vp] * 9 + [_vp, _vp, _sz, _i, _i, _i, _i, _i, _i, _vp]),
     "kbh_silu_fp8_quant": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp]),
+    "kbh_moe_workspace_bytes": (_sz, [_i, _i, _i, _i, _i]),
+    "kbh_moe_route_topk": (_i, [_vp, _i, _vp, _vp, _vp, _sz, _i, _i, _i, _i, _vp]),
+    "kbh_moe": (_i, [_vp, _vp, _vp, _i, _vp, _vp, _sz, _i, _i, _i, _i, _i, _i, _vp]),
 }
 
 

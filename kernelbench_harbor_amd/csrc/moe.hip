@@ -112,6 +112,136 @@ __global__ __launch_bounds__(1024) void moe_route_kernel(const void* __restrict_
   }
 }
 
+// Top-k routing (k <= kMoeMaxTopk) for the fp16/bf16-weight MoE (tasks/moe/<task>/environment/
+// reference.py:11-13): probs = softmax(fp32 logits), the k largest in descending order (the lower
+// expert index first among equal logits: an expert only displaces strictly smaller entries),
+// weights p_j / sum_j p_j (summed in k order) rounded to the activation dtype. Slots, permutation
+// (perm[slot] = k t + j) and tile table as moe_route_kernel. Indices start as 0..k-1 so that
+// every id is in range whatever the logits hold (NaN, -inf).
+constexpr int kMoeMaxTopk = 8;
+template <int LDT>
+__global__ __launch_bounds__(1024) void moe_route_topk_kernel(const void* __restrict__ logits,
+                                                              int T, int E, int K, int out_bf16,
+                                                              MoeBuffers mb, int max_tiles, int bm) {
+  __shared__ int cnt[kMoeMaxExperts];
+  __shared__ int off[kMoeMaxExperts];
+  __shared__ int tbase[kMoeMaxExperts + 1];
+  for (int e = threadIdx.x; e < E; e += blockDim.x) cnt[e] = 0;
+  __syncthreads();
+  for (int t = threadIdx.x; t < T; t += blockDim.x) {
+    const size_t row = (size_t)t * E;
+    float lv[kMoeMaxTopk];
+    int li[kMoeMaxTopk];
+#pragma unroll
+    for (int j = 0; j < kMoeMaxTopk; ++j) {
+      lv[j] = -INFINITY;
+      li[j] = j < K ? j : 0;
+    }
+    float mx = -INFINITY;
+    for (int e = 0; e < E; ++e) {
+      const float v = logit_at<LDT>(logits, row + e);
+      mx = fmaxf(mx, v);
+      if (!(v > lv[K - 1])) continue;
+      // insertion into the descending list: entries below position p shift down by one
+      int p = K - 1;
+#pragma unroll
+      for (int j = kMoeMaxTopk - 1; j > 0; --j) {
+        if (j < K && j <= p && v > lv[j - 1]) {
+          lv[j] = lv[j - 1];
+          li[j] = li[j - 1];
+          p = j - 1;
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < kMoeMaxTopk; ++j)
+        if (j == p) { lv[j] = v; li[j] = e; }
+    }
+    float sum = 0.f;
+    for (int e = 0; e < E; ++e) sum += expf(logit_at<LDT>(logits, row + e) - mx);
+    float pk[kMoeMaxTopk], ps = 0.f;
+#pragma unroll
+    for (int j = 0; j < kMoeMaxTopk; ++j) {
+      if (j < K) {
+        pk[j] = keep_f32(expf(logit_at<LDT>(logits, row + li[j]) - mx) / sum);
+        ps = keep_f32(ps + pk[j]);
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < kMoeMaxTopk; ++j) {
+      if (j < K) {
+        const float w = keep_f32(pk[j] / ps);
+        const int e = min(max(li[j], 0), E - 1);
+        mb.topi[K * t + j] = e;
+        mb.topw[K * t + j] = out_bf16 ? f32_to_bf16_bits(w) : f32_to_f16_bits(w);
+        mb.slot_of[K * t + j] = atomicAdd(&cnt[e], 1);
+      }
+    }
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    int o = 0, tb = 0;
+    for (int e = 0; e < E; ++e) {
+      off[e] = o;
+      tbase[e] = tb;
+      o += cnt[e];
+      tb += (cnt[e] + bm - 1) / bm;
+    }
+    tbase[E] = tb;
+  }
+  __syncthreads();
+  for (int i = threadIdx.x; i < K * T; i += blockDim.x)
+    mb.perm[off[mb.topi[i]] + mb.slot_of[i]] = i;
+  for (int e = threadIdx.x; e < E; e += blockDim.x) {
+    for (int j = 0; j < tbase[e + 1] - tbase[e]; ++j) {
+      int* tl = &mb.tiles[3 * (tbase[e] + j)];
+      tl[0] = e;
+      tl[1] = off[e] + j * bm;
+      tl[2] = min(bm, cnt[e] - j * bm);
+    }
+  }
+  for (int i = tbase[E] + threadIdx.x; i < max_tiles; i += blockDim.x) {
+    mb.tiles[3 * i] = 0;
+    mb.tiles[3 * i + 1] = 0;
+    mb.tiles[3 * i + 2] = 0;
+  }
+}
+
+// Slab producer for fp16/bf16 weights [E][K][N] (N contiguous), used as they are: each thread
+// loads 4 rows x 4 columns (8 bytes per row; a row of the 128-column slab is 256 contiguous
+// bytes across 32 threads) and writes the 4x4 block transposed, Bs[n * TLD + k], as four 8-byte
+// LDS stores (two v_perm_b32 per column).
+struct F16SlabPolicy {
+  const uint16_t* w;
+  int N;
+  size_t w_stride;
+  __device__ F16SlabPolicy at_expert(int e) const {
+    F16SlabPolicy p = *this;
+    p.w += (size_t)e * w_stride;
+    return p;
+  }
+  struct Regs {
+    kbh_u32x2 r[4];
+  };
+  __device__ void load(Regs& r, int k0, int n0, int t) const {
+    const int cq = t & 31, rq = t >> 5;
+    const uint16_t* p = w + (size_t)(k0 + 4 * rq) * N + n0 + 4 * cq;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      r.r[i] = __builtin_nontemporal_load(reinterpret_cast<const kbh_u32x2*>(p + (size_t)i * N));
+  }
+  __device__ void store(const Regs& r, uint16_t* Bs, int t) const {
+    const int cq = t & 31, rq = t >> 5;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const uint32_t sel = (j & 1) ? 0x07060302u : 0x05040100u;  // high or low halves
+      kbh_u32x2 out;
+      out[0] = __builtin_amdgcn_perm(r.r[1][j >> 1], r.r[0][j >> 1], sel);
+      out[1] = __builtin_amdgcn_perm(r.r[3][j >> 1], r.r[2][j >> 1], sel);
+      *reinterpret_cast<kbh_u32x2*>(&Bs[(4 * cq + j) * TLD + 4 * rq]) = out;
+    }
+  }
+};
+
 // Slab producer for int8-stored weights [E][K][N] (N contiguous) with scales [E][K/G][N] in the
 // activation dtype: W = dtype(dtype(q) * s), one rounding (q is exact in either dtype).
 template <bool BF16>
@@ -189,7 +319,7 @@ __global__ __launch_bounds__(256) void moe_gemm_kernel(const uint16_t* __restric
                                                        const int* __restrict__ perm,
                                                        const int* __restrict__ tiles, BP bp,
                                                        BP bp2, uint16_t* __restrict__ out,
-                                                       int ldo, int N, int K) {
+                                                       int ldo, int N, int K, int topk) {
   constexpr int BN = 128;
   constexpr int WM = BM / 64, WN = 4 / WM;  // waves along M and N
   constexpr int WNT = BN / WN / 32;         // 32-column MFMA tiles per wave
@@ -214,7 +344,7 @@ __global__ __launch_bounds__(256) void moe_gemm_kernel(const uint16_t* __restric
   for (int i = 0; i < AL; ++i) {
     const int r = min(a_row + 64 * i, rows - 1);  // rows past the tile repeat the last one
     const int s = s0 + r;
-    const int src = GATHER ? (perm[s] >> 1) : s;
+    const int src = GATHER ? (perm[s] / topk) : s;  // perm[s] = topk * token + k
     arow[i] = A + (size_t)src * lda + a_ch * 8;
   }
   struct Slab {
@@ -321,6 +451,35 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(const uint16_t* __rest
   y[i] = f32_to_half_bits<BF16>(keep_f32(p0 + p1));
 }
 
+// y[t][n] = dtype(sum_j fp32(dtype(o[k t + j][n] * w[k t + j]))), j = 0..k-1 in order: the
+// reference's (sel * topv).sum(dim=1) in the activation dtype (tasks/moe/<task>/environment/
+// reference.py:16-17). Four columns per thread.
+template <bool BF16>
+__global__ __launch_bounds__(256) void moe_combine_k_kernel(const uint16_t* __restrict__ o,
+                                                            const uint16_t* __restrict__ topw,
+                                                            uint16_t* __restrict__ y, int T, int N,
+                                                            int K) {
+  const size_t i4 = ((size_t)blockIdx.x * blockDim.x + threadIdx.x) * 4;
+  if (i4 >= (size_t)T * N) return;
+  const size_t t = i4 / N, n = i4 - t * N;
+  float acc[4] = {0.f, 0.f, 0.f, 0.f};
+  for (int j = 0; j < K; ++j) {
+    const size_t r = (size_t)K * t + j;
+    const float w = half_bits_to_f32<BF16>(topw[r]);
+    const kbh_u32x2 v = *reinterpret_cast<const kbh_u32x2*>(o + r * N + n);
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const uint16_t h = (uint16_t)(v[c >> 1] >> (16 * (c & 1)));
+      acc[c] = keep_f32(acc[c] + half_bits_to_f32<BF16>(
+                                     f32_to_half_bits<BF16>(keep_f32(half_bits_to_f32<BF16>(h) * w))));
+    }
+  }
+  kbh_u32x2 out;
+  out[0] = (uint32_t)f32_to_half_bits<BF16>(acc[0]) | ((uint32_t)f32_to_half_bits<BF16>(acc[1]) << 16);
+  out[1] = (uint32_t)f32_to_half_bits<BF16>(acc[2]) | ((uint32_t)f32_to_half_bits<BF16>(acc[3]) << 16);
+  *reinterpret_cast<kbh_u32x2*>(y + i4) = out;
+}
+
 // ---- SiLU FFN on the wide-tile kernel -------------------------------------------------------
 
 // Gate and up weights as one virtual TN-column slab: in each 16-word chunk c of the tile, packed
@@ -420,27 +579,31 @@ bool plan_ffn(int T, int E, int D, int F, int group, FfnPlan* p) {
 // ---- host side ------------------------------------------------------------------------------
 struct MoeLayout {
   size_t topi, topw, slot_of, perm, tiles, h, o, part, total;
-  int bm, max_tiles;
+  int bm, max_tiles, topk;
 };
 
-// bm: rows per tile-table entry (0: 128 when an expert averages more than 96 rows, else 64).
-MoeLayout moe_layout(int T, int E, int hidden, int out_cols, int bm = 0, size_t part_bytes = 0) {
+// Slots: topk per token (slot order grouped by expert). bm: rows per tile-table entry (0: 128
+// when an expert averages more than 96 rows, else 64).
+MoeLayout moe_layout(int T, int E, int hidden, int out_cols, int bm = 0, size_t part_bytes = 0,
+                     int topk = 2) {
   MoeLayout L;
-  L.bm = bm ? bm : ((2 * T) / (E > 0 ? E : 1) > 96 ? 128 : 64);
-  L.max_tiles = (2 * T + L.bm - 1) / L.bm + E;
+  const size_t S = (size_t)topk * T;
+  L.topk = topk;
+  L.bm = bm ? bm : ((int)S / (E > 0 ? E : 1) > 96 ? 128 : 64);
+  L.max_tiles = (int)((S + L.bm - 1) / L.bm) + E;
   size_t o = 0;
   auto take = [&](size_t bytes) {
     const size_t at = o;
     o += round_up(bytes, 256);
     return at;
   };
-  L.topi = take((size_t)2 * T * 4);
-  L.topw = take((size_t)2 * T * 2);
-  L.slot_of = take((size_t)2 * T * 4);
-  L.perm = take((size_t)2 * T * 4);
+  L.topi = take(S * 4);
+  L.topw = take(S * 2);
+  L.slot_of = take(S * 4);
+  L.perm = take(S * 4);
   L.tiles = take((size_t)L.max_tiles * 3 * 4);
-  L.h = take((size_t)2 * T * hidden * 2);
-  L.o = take((size_t)2 * T * out_cols * 2);
+  L.h = take(S * hidden * 2);
+  L.o = take(S * out_cols * 2);
   L.part = take(part_bytes);
   L.total = o;
   return L;
@@ -463,16 +626,30 @@ void launch_route(const void* logits, int logits_dtype, int T, int E, bool bf16,
     hipLaunchKernelGGL(moe_route_kernel<2>, g, b, 0, st, logits, T, E, (int)bf16, mb, L.max_tiles, L.bm);
 }
 
+void launch_route_topk(const void* logits, int logits_dtype, int T, int E, bool bf16,
+                       const MoeBuffers& mb, const MoeLayout& L, hipStream_t st) {
+  const dim3 g(1), b(1024);
+  const int K = L.topk;
+  if (logits_dtype == 0)
+    hipLaunchKernelGGL(moe_route_topk_kernel<0>, g, b, 0, st, logits, T, E, K, (int)bf16, mb, L.max_tiles, L.bm);
+  else if (logits_dtype == 1)
+    hipLaunchKernelGGL(moe_route_topk_kernel<1>, g, b, 0, st, logits, T, E, K, (int)bf16, mb, L.max_tiles, L.bm);
+  else
+    hipLaunchKernelGGL(moe_route_topk_kernel<2>, g, b, 0, st, logits, T, E, K, (int)bf16, mb, L.max_tiles, L.bm);
+}
+
 template <bool BF16, class BP, bool GATHER, bool GATED, bool OUT_PERM>
 void launch_moe_gemm(const MoeLayout& L, const void* A, int lda, const MoeBuffers& mb, const BP& bp,
                      const BP& bp2, void* out, int ldo, int N, int K, hipStream_t st) {
   const dim3 grid(N / 128, L.max_tiles);
   if (L.bm == 64)
     hipLaunchKernelGGL((moe_gemm_kernel<BF16, 64, BP, GATHER, GATED, OUT_PERM>), grid, dim3(256), 0,
-                       st, (const uint16_t*)A, lda, mb.perm, mb.tiles, bp, bp2, (uint16_t*)out, ldo, N, K);
+                       st, (const uint16_t*)A, lda, mb.perm, mb.tiles, bp, bp2, (uint16_t*)out, ldo, N,
+                       K, L.topk);
   else
     hipLaunchKernelGGL((moe_gemm_kernel<BF16, 128, BP, GATHER, GATED, OUT_PERM>), grid, dim3(256), 0,
-                       st, (const uint16_t*)A, lda, mb.perm, mb.tiles, bp, bp2, (uint16_t*)out, ldo, N, K);
+                       st, (const uint16_t*)A, lda, mb.perm, mb.tiles, bp, bp2, (uint16_t*)out, ldo, N,
+                       K, L.topk);
 }
 
 template <bool BF16>
@@ -694,5 +871,60 @@ extern "C" int kbh_qmoe_ffn(const void* x, const void* router_logits, int logits
   }
   if (bf) KBH_FFN(true) else KBH_FFN(false)
 #undef KBH_FFN
+  return launch_status();
+}
+
+extern "C" size_t kbh_moe_workspace_bytes(int T, int D, int H, int E, int topk) {
+  (void)D;
+  if (T <= 0 || E <= 0 || topk < 1 || topk > kbh::kMoeMaxTopk) return 0;
+  return kbh::moe_layout(T, E, 0, H, 0, 0, topk).total;
+}
+
+extern "C" int kbh_moe_route_topk(const void* router_logits, int logits_dtype, int32_t* topi,
+                                  void* topw, void* workspace, size_t workspace_bytes, int T,
+                                  int E, int topk, int dtype, void* stream) {
+  using namespace kbh;
+  if (!router_logits || !topi || !topw || !workspace) return KBH_ERR_NULL;
+  if (logits_dtype < 0 || logits_dtype > 2 || (dtype != KBH_F16 && dtype != KBH_BF16)) return KBH_ERR_DTYPE;
+  if (T < 1 || E < 2 || E > kMoeMaxExperts || topk < 1 || topk > kMoeMaxTopk || topk > E)
+    return KBH_ERR_SHAPE;
+  const MoeLayout L = moe_layout(T, E, 0, 0, 0, 0, topk);
+  if (workspace_bytes < L.total) return KBH_ERR_WORKSPACE;
+  MoeBuffers mb = moe_buffers(workspace, L);
+  mb.topi = topi;
+  mb.topw = (uint16_t*)topw;
+  launch_route_topk(router_logits, logits_dtype, T, E, dtype == KBH_BF16, mb, L, (hipStream_t)stream);
+  return launch_status();
+}
+
+extern "C" int kbh_moe(const void* x, const void* w, const void* router_logits, int logits_dtype,
+                       void* y, void* workspace, size_t workspace_bytes, int T, int D, int H, int E,
+                       int topk, int dtype, void* stream) {
+  using namespace kbh;
+  if (!x || !w || !router_logits || !y || !workspace) return KBH_ERR_NULL;
+  if (dtype != KBH_F16 && dtype != KBH_BF16) return KBH_ERR_DTYPE;
+  if (logits_dtype < 0 || logits_dtype > 2) return KBH_ERR_DTYPE;
+  if (!moe_shape_ok(T, E, D, H, 128) || topk < 1 || topk > kMoeMaxTopk || topk > E)
+    return KBH_ERR_SHAPE;
+  if (!aligned16(x) || !aligned16(w) || !aligned16(y)) return KBH_ERR_ALIGN;
+  const MoeLayout L = moe_layout(T, E, 0, H, 0, 0, topk);
+  if (workspace_bytes < L.total) return KBH_ERR_WORKSPACE;
+  const MoeBuffers mb = moe_buffers(workspace, L);
+  hipStream_t st = (hipStream_t)stream;
+  void* o = (char*)workspace + L.o;
+  const bool bf = dtype == KBH_BF16;
+  launch_route_topk(router_logits, logits_dtype, T, E, bf, mb, L, st);
+  const F16SlabPolicy bp{(const uint16_t*)w, H, (size_t)D * H};
+  const size_t n4 = (size_t)T * H / 4;
+  const dim3 cgrid((unsigned)((n4 + 255) / 256));
+  if (bf) {
+    launch_moe_gemm<true, F16SlabPolicy, true, false, true>(L, x, D, mb, bp, bp, o, H, H, D, st);
+    hipLaunchKernelGGL(moe_combine_k_kernel<true>, cgrid, dim3(256), 0, st, (const uint16_t*)o,
+                       mb.topw, (uint16_t*)y, T, H, topk);
+  } else {
+    launch_moe_gemm<false, F16SlabPolicy, true, false, true>(L, x, D, mb, bp, bp, o, H, H, D, st);
+    hipLaunchKernelGGL(moe_combine_k_kernel<false>, cgrid, dim3(256), 0, st, (const uint16_t*)o,
+                       mb.topw, (uint16_t*)y, T, H, topk);
+  }
   return launch_status();
 }

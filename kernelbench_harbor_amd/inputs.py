@@ -154,3 +154,30 @@ def silu_fp8(T: int = 512, H: int = 14336, dtype: torch.dtype = torch.float16, s
     """[y]: y [T, 2H] ~ N(0, 1) in dtype, as tasks/fused_silu_fp8/*/environment/reference.py:25-28."""
     g = _gen(seed)
     return [torch.randn(T, 2 * H, generator=g).to(dtype)]
+
+
+def _topk_distinct_logits(T: int, E: int, k: int, g: torch.Generator,
+                          dtype: torch.dtype) -> torch.Tensor:
+    """N(0,1) router logits in `dtype` whose k+1 largest per row are distinct (rows with a tie
+    there are re-drawn), so the top-k selection and its order do not depend on tie-breaking."""
+    lg = torch.randn(T, E, generator=g).to(dtype)
+    m = min(k + 1, E)
+    while True:
+        top = lg.float().topk(m, dim=-1).values
+        bad = (top[:, :-1] <= top[:, 1:]).any(dim=-1) if m > 1 else torch.zeros(T, dtype=torch.bool)
+        n = int(bad.sum())
+        if n == 0:
+            return lg
+        lg[bad] = torch.randn(n, E, generator=g).to(dtype)
+
+
+def moe(T: int = 16, D: int = 4096, E: int = 8, H: int = 14336, topk: int = 2,
+        dtype: torch.dtype = torch.float16, seed: int = 0):
+    """[x, w, router_logits] with the distributions of the reference moe task
+    (tasks/moe/*/environment/reference.py:19-24): x N(0,1), w N(0,1)*0.02, logits N(0,1), all in
+    dtype (logits re-drawn per row where the top-(k+1) would tie)."""
+    g = _gen(seed)
+    x = torch.randn(T, D, generator=g).to(dtype)
+    w = (torch.randn(E, D, H, generator=g) * 0.02).to(dtype)
+    logits = _topk_distinct_logits(T, E, topk, g, dtype)
+    return [x, w, logits]

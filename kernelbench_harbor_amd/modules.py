@@ -90,3 +90,25 @@ class FusedSiluFP8Model(nn.Module):
 
     def forward(self, y):
         return ops.silu_fp8_quant(y, 128)
+
+
+class MoEModel(nn.Module):
+    """Top-k mixture of experts with fp16/bf16 expert weights (sparse dispatch).
+
+    Reference: tasks/moe/*/environment/reference.py:10-17, whose TOPK is a module constant
+    (generate_tasks.py:189-195: 2, 6 or 8): forward(x [T,D], w [E,D,H], router_logits [T,E])
+    -> [T, H] x.dtype. Subclasses fix TOPK for the top-6 and top-8 tasks.
+    """
+
+    TOPK = 2
+
+    def forward(self, x, w, router_logits):
+        return ops.moe(x, w, router_logits, self.TOPK)
+
+
+class MoETop6Model(MoEModel):
+    TOPK = 6
+
+
+class MoETop8Model(MoEModel):
+    TOPK = 8

@@ -366,3 +366,55 @@ def silu_fp8_quant(y: torch.Tensor, group: int = 128, return_codes: bool = False
     if return_codes:
         return out, codes.view(torch.float8_e4m3fn), scales
     return out
+
+
+def moe_route_topk(router_logits: torch.Tensor, topk: int, dtype: torch.dtype = torch.float16):
+    """(topi [T, topk] int32, topw [T, topk] dtype): softmax(fp32 logits), top-k in descending
+    order (lower index first on a tie), weights renormalised and rounded to dtype
+    (tasks/moe/*/environment/reference.py:11-13)."""
+    _require(dtype in _DT_CODE, f"dtype must be float16 or bfloat16, got {dtype}")
+    T = router_logits.shape[0]
+    E = _check_logits(router_logits, T)
+    _require(1 <= topk <= min(8, E), f"topk must be in [1, min(8, E={E})], got {topk}")
+    dev = _check_device(router_logits)
+    topi = torch.empty((T, topk), dtype=torch.int32, device=dev)
+    topw = torch.empty((T, topk), dtype=dtype, device=dev)
+    if T == 0:
+        return topi, topw
+    lib = _lib.load()
+    ws = scratches.get(lib.kbh_moe_workspace_bytes(T, 0, 0, E, topk), dev)
+    st = lib.kbh_moe_route_topk(router_logits.contiguous().data_ptr(),
+                                _LOGIT_CODE[router_logits.dtype], topi.data_ptr(), topw.data_ptr(),
+                                ws.data_ptr(), ws.numel(), T, E, topk, _DT_CODE[dtype],
+                                _stream_ptr(dev))
+    _lib.check(st, "kbh_moe_route_topk")
+    return topi, topw
+
+
+def moe(x: torch.Tensor, w: torch.Tensor, router_logits: torch.Tensor, topk: int) -> torch.Tensor:
+    """Top-k MoE with fp16/bf16 experts: y[t] = sum_j w_j * (x[t] @ w[e_j]), sparse dispatch.
+
+    Follows tasks/moe/moe_top2__mixtral_8x7b__T16__fp16/environment/reference.py:10-17: x [T, D],
+    w [E, D, H] in x.dtype, router_logits [T, E]; each expert output and each weighted product
+    rounded to x.dtype, the k products summed in fp32 and rounded once."""
+    _require(x.dtype in _DT_CODE and x.dim() == 2, "x must be a float16/bfloat16 [T, D] tensor")
+    T, D = x.shape
+    E = _check_logits(router_logits, T)
+    _require(w.dtype == x.dtype and w.dim() == 3 and w.shape[:2] == (E, D),
+             f"w must be x.dtype [{E}, {D}, H], got {w.dtype} {tuple(w.shape)}")
+    H = w.shape[2]
+    _require(1 <= topk <= min(8, E), f"topk must be in [1, min(8, E={E})], got {topk}")
+    _require(D % 128 == 0 and D >= 128, f"D={D} must be a positive multiple of 128")
+    _require(H % 128 == 0 and H >= 128, f"H={H} must be a positive multiple of 128")
+    dev = _check_device(x, w, router_logits)
+    y = torch.empty((T, H), dtype=x.dtype, device=dev)
+    if T == 0:
+        return y
+    lib = _lib.load()
+    ws = scratches.get(lib.kbh_moe_workspace_bytes(T, D, H, E, topk), dev)
+    xc, wc = x.contiguous(), w.contiguous()
+    st = lib.kbh_moe(xc.data_ptr(), wc.data_ptr(), router_logits.contiguous().data_ptr(),
+                     _LOGIT_CODE[router_logits.dtype], y.data_ptr(), ws.data_ptr(), ws.numel(),
+                     T, D, H, E, topk, _DT_CODE[x.dtype], _stream_ptr(dev))
+    _lib.check(st, "kbh_moe")
+    return y

@@ -12,6 +12,7 @@ move with the installed torch. The sequences follow:
   MXFP8   generate_tasks.py:337-342 (amax/448, e4m3fn cast) with a power-of-two block scale
   qMoE    tasks/fused_qmoe/<task>/environment/reference.py:14-21
   SiLU-FP8 tasks/fused_silu_fp8/<task>/environment/reference.py:13-23
+  MoE     tasks/moe/<task>/environment/reference.py:10-17 (top-2 and top-6)
 
 `python tests/golden/make_golden.py [name ...]` rewrites only the named files (default: all);
 each file draws from its own seeded generator, so one can be rewritten without the others.
@@ -125,18 +126,40 @@ def silu_fp8(g):
     return out
 
 
+def moe(g):
+    """Top-k fp16 MoE at T=6, D=64, E=8, H=16 for k = 2 and 6: the reference's op sequence in
+    fp16 (native path) and on fp32-upcast inputs (the grader's ground truth)."""
+    T, D, E, H = 6, 64, 8, 16
+    x = torch.randn(T, D, generator=g).half()
+    w = (torch.randn(E, D, H, generator=g) * 0.02).half()
+    lg = torch.randn(T, E, generator=g).half()
+    out = {"x": _np(x.float()), "w": _np(w.float()), "logits": _np(lg.float())}
+    for k in (2, 6):
+        for tag, (xx, ww, ll) in (("f16", (x, w, lg)), ("gt", (x.float(), w.float(), lg.float()))):
+            probs = torch.softmax(ll.float(), dim=-1)
+            topv, topi = probs.topk(k, dim=-1)
+            topv = (topv / topv.sum(dim=-1, keepdim=True)).to(xx.dtype)
+            all_out = torch.einsum("td,edh->teh", xx, ww)
+            sel = torch.gather(all_out, 1, topi.unsqueeze(-1).expand(-1, -1, H))
+            y = (sel * topv.unsqueeze(-1)).sum(dim=1)
+            out[f"y_{tag}_k{k}"] = _np(y.float())
+            out[f"topi_k{k}"] = _np(topi)
+            out[f"topw_{tag}_k{k}"] = _np(topv.float())
+    return out
+
+
 def e4m3fn_table():
     v = torch.arange(256, dtype=torch.uint8).view(torch.float8_e4m3fn).float()
     return ["nan" if np.isnan(a) else float(a).hex() for a in v.tolist()]
 
 
-SEEDS = {"w4a16": 20240611, "silu_fp8": 20240612}
+SEEDS = {"w4a16": 20240611, "silu_fp8": 20240612, "moe": 20240613}
 SETS = (("w4a16", w4a16), ("w8a8", w8a8), ("fp8w", fp8w), ("mxfp8", mxfp8),
         ("qmoe_route", qmoe_route))
 
 
 def main(names=()):
-    names = set(names) or {n for n, _ in SETS} | {"silu_fp8", "e4m3fn_table"}
+    names = set(names) or {n for n, _ in SETS} | {"silu_fp8", "moe", "e4m3fn_table"}
     # The first five sets share one generator, drawn in this order (as first written).
     if names & {n for n, _ in SETS}:
         g = torch.Generator().manual_seed(SEEDS["w4a16"])
@@ -147,6 +170,9 @@ def main(names=()):
     if "silu_fp8" in names:
         g = torch.Generator().manual_seed(SEEDS["silu_fp8"])
         np.savez(os.path.join(HERE, "silu_fp8.npz"), **silu_fp8(g))
+    if "moe" in names:
+        g = torch.Generator().manual_seed(SEEDS["moe"])
+        np.savez(os.path.join(HERE, "moe.npz"), **moe(g))
     if "e4m3fn_table" in names:
         with open(os.path.join(HERE, "e4m3fn_table.json"), "w") as f:
             json.dump({"source": "torch.float8_e4m3fn -> float32, codes 0..255",

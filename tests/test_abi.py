@@ -73,6 +73,17 @@ def test_host_checks_run_without_gpu():
     assert lib.kbh_silu_fp8_quant(p, ctypes.c_void_p(20), None, None, 4, 256, 128, 0, None) == _lib.KBH_ERR_ALIGN
     assert lib.kbh_silu_fp8_quant(p, p, ctypes.c_void_p(20), None, 4, 256, 128, 0, None) == _lib.KBH_ERR_ALIGN
     assert lib.kbh_silu_fp8_quant(p, p, None, None, 0, 256, 128, 0, None) == _lib.KBH_OK
+    # top-k MoE: k range, D / H divisibility, workspace size
+    need = lib.kbh_moe_workspace_bytes(16, 4096, 14336, 8, 2)
+    assert need >= 2 * 16 * 14336 * 2 and lib.kbh_moe_workspace_bytes(16, 4096, 14336, 8, 9) == 0
+    assert lib.kbh_moe(p, p, p, 0, p, p, need, 16, 4096, 14336, 8, 9, 0, None) == _lib.KBH_ERR_SHAPE
+    assert lib.kbh_moe(p, p, p, 0, p, p, need, 16, 4096, 14336, 8, 0, 0, None) == _lib.KBH_ERR_SHAPE
+    assert lib.kbh_moe(p, p, p, 0, p, p, need, 16, 4000, 14336, 8, 2, 0, None) == _lib.KBH_ERR_SHAPE
+    assert lib.kbh_moe(p, p, p, 0, p, p, need, 16, 4096, 14300, 8, 2, 0, None) == _lib.KBH_ERR_SHAPE
+    assert lib.kbh_moe(p, p, p, 0, p, p, need - 1, 16, 4096, 14336, 8, 2, 0, None) == _lib.KBH_ERR_WORKSPACE
+    assert lib.kbh_moe(p, p, p, 3, p, p, need, 16, 4096, 14336, 8, 2, 0, None) == _lib.KBH_ERR_DTYPE
+    assert lib.kbh_moe(None, p, p, 0, p, p, need, 16, 4096, 14336, 8, 2, 0, None) == _lib.KBH_ERR_NULL
+    assert lib.kbh_moe_route_topk(p, 0, p, p, p, need, 16, 4, 6, 0, None) == _lib.KBH_ERR_SHAPE
 
 
 def test_workspace_sizes():

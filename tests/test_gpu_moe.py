@@ -1,0 +1,107 @@
+"""GPU parity of the top-k fp16/bf16 MoE (kbh_moe, kbh_moe_route_topk) against the CPU oracle
+(oracle/moe.py): routing ids exactly, weights within one ulp; outputs to the BASELINE tolerance
+against the fp32 ground truth; one-hot activations bit-exact against the oracle's native-dtype
+path; and every task of the reference generator's moe family at its real shape
+(generate_tasks.py:189-195, 552-553: five layers x T in {16, 128, 512} fp16 plus T=512 bf16),
+checked on the first and last 256 output columns."""
+import functools
+
+import numpy as np
+import pytest
+import torch
+
+from kernelbench_harbor_amd import MoEModel, MoETop6Model, MoETop8Model, inputs, ops
+from kernelbench_harbor_amd.harness import compare
+from oracle import moe as om
+
+pytestmark = pytest.mark.gpu
+
+
+def _f(t):
+    return t.float().numpy()
+
+
+@pytest.mark.parametrize("E,k", [(8, 2), (64, 6), (128, 8), (8, 8), (60, 1)])
+@pytest.mark.parametrize("ldt", [torch.float16, torch.float32])
+def test_route_topk(dev, E, k, ldt):
+    g = torch.Generator().manual_seed(E + k)
+    lg = inputs._topk_distinct_logits(333, E, k, g, ldt)
+    topi, topw = ops.moe_route_topk(lg.to(dev), k, torch.float16)
+    oi, ow = om.route_topk(_f(lg), k, "f16")
+    assert np.array_equal(topi.cpu().numpy(), oi)
+    assert np.abs(topw.float().cpu().numpy() - ow).max() <= 2 ** -11   # at most one fp16 ulp
+
+
+CASES = [
+    # T, D, E, H, k, dtype
+    (16, 256, 8, 256, 2, torch.float16),
+    (37, 512, 64, 384, 6, torch.float16),
+    (100, 256, 128, 128, 8, torch.bfloat16),
+    (300, 512, 8, 256, 2, torch.bfloat16),
+    (1, 128, 4, 128, 1, torch.float16),
+    (250, 384, 16, 640, 8, torch.float16),   # > 96 rows per expert: 128-row tiles
+]
+
+
+@pytest.mark.parametrize("T,D,E,H,k,dtype", CASES)
+def test_moe_parity(dev, T, D, E, H, k, dtype):
+    print(f"[moe] T={T} D={D} E={E} H={H} k={k} {dtype}", flush=True)
+    x, w, lg = inputs.moe(T, D, E, H, k, dtype, seed=T + H + k)
+    y = ops.moe(x.to(dev), w.to(dev), lg.to(dev), k)
+    assert y.dtype == dtype and y.shape == (T, H)
+    cmp = compare(y, om.forward(_f(x), _f(w), _f(lg), k))
+    assert cmp.ok, cmp
+    y2 = ops.moe(x.to(dev), w.to(dev), lg.to(dev), k)
+    assert torch.equal(y, y2)
+
+
+@pytest.mark.parametrize("k,dtype", [(2, torch.float16), (6, torch.float16), (8, torch.bfloat16)])
+def test_one_hot_matches_native_rounding(dev, k, dtype):
+    """One-hot rows make each expert output a weight row (exact), so every later rounding (the
+    routing weight products and the k-term sum) must match the oracle's native path bit for bit."""
+    T, D, E, H = 64, 256, 16, 256
+    _, w, lg = inputs.moe(T, D, E, H, k, dtype, seed=11 + k)
+    g = torch.Generator().manual_seed(12)
+    x = torch.zeros(T, D, dtype=dtype)
+    x[torch.arange(T), torch.randint(0, D, (T,), generator=g)] = 1.0
+    y = ops.moe(x.to(dev), w.to(dev), lg.to(dev), k).float().cpu().numpy()
+    want = om.forward(_f(x), _f(w), _f(lg), k, dtype="f16" if dtype == torch.float16 else "bf16")
+    assert np.array_equal(y, want), np.abs(y - want).max()
+
+
+def test_empty_tokens(dev):
+    x = torch.zeros(0, 128, dtype=torch.float16, device=dev)
+    w = torch.zeros(4, 128, 128, dtype=torch.float16, device=dev)
+    lg = torch.zeros(0, 4, dtype=torch.float16, device=dev)
+    assert ops.moe(x, w, lg, 2).shape == (0, 128)
+
+
+MOE_LAYERS = [  # (name, D, E, H, topk), generate_tasks.py:189-195
+    ("mixtral_8x7b", 4096, 8, 14336, 2),
+    ("grok1", 6144, 8, 8192, 2),
+    ("qwen2_57b", 3584, 64, 2560, 8),
+    ("deepseek_v2_lite", 2048, 64, 1408, 6),
+    ("qwen3_30b", 2048, 128, 768, 8),
+]
+MOE_GRID = [(n, D, E, H, k, T, torch.float16) for (n, D, E, H, k) in MOE_LAYERS for T in (16, 128, 512)]
+MOE_GRID += [(n, D, E, H, k, 512, torch.bfloat16) for (n, D, E, H, k) in MOE_LAYERS]
+MODEL = {2: MoEModel, 6: MoETop6Model, 8: MoETop8Model}
+
+
+@functools.lru_cache(maxsize=1)
+def _weights(D, E, H, dtype):
+    g = torch.Generator().manual_seed(D + E + H)
+    return (torch.randn(E, D, H, generator=g) * 0.02).to(dtype)
+
+
+@pytest.mark.parametrize("name,D,E,H,k,T,dtype", MOE_GRID)
+def test_moe_task(dev, name, D, E, H, k, T, dtype):
+    print(f"[grid moe] {name} D={D} E={E} H={H} top{k} T={T} {dtype}", flush=True)
+    x, _, lg = inputs.moe(T, 128, E, 128, k, dtype, seed=T + E)
+    x = torch.randn(T, D, generator=torch.Generator().manual_seed(T + D)).to(dtype)
+    w = _weights(D, E, H, dtype)
+    y = MODEL[k]()(x.to(dev), w.to(dev), lg.to(dev)).cpu()
+    assert y.shape == (T, H) and y.dtype == dtype
+    for c in (slice(0, 256), slice(H - 256, H)):
+        cmp = compare(y[:, c], om.forward(_f(x), _f(w[:, :, c]), _f(lg), k))
+        assert cmp.ok, (c, cmp)

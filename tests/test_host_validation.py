@@ -86,3 +86,17 @@ def test_silu_fp8_rejects_bad_inputs():
         ops.silu_fp8_quant(y, 100)
     with pytest.raises(ValueError, match="HIP device"):
         ops.silu_fp8_quant(y)
+
+
+def test_moe_rejects_bad_inputs():
+    x = torch.zeros(4, 256, dtype=torch.float16)
+    w = torch.zeros(8, 256, 128, dtype=torch.float16)
+    lg = torch.zeros(4, 8, dtype=torch.float16)
+    with pytest.raises(ValueError, match="topk"):
+        ops.moe(x, w, lg, 9)
+    with pytest.raises(ValueError, match="w must be"):
+        ops.moe(x, w[:4], lg, 2)
+    with pytest.raises(ValueError, match="H="):
+        ops.moe(x, torch.zeros(8, 256, 100, dtype=torch.float16), lg, 2)
+    with pytest.raises(ValueError, match="HIP device"):
+        ops.moe(x, w, lg, 2)
