@@ -85,6 +85,17 @@ def qmoe_flops(T=256, D=4096, N=14336):
     return 2 * T * 2 * D * N
 
 
+def moe_bytes(T, D, E, H, k):
+    """x, y, logits and the weights of the experts the routing selects (expected count for
+    uniform routing: E (1 - (1 - k/E)^T))."""
+    touched = E * (1.0 - (1.0 - k / E) ** T)
+    return int(touched * D * H * 2) + 2 * T * D + 2 * T * H + 2 * T * E
+
+
+def moe_flops(T, D, H, k):
+    return 2 * T * k * D * H
+
+
 def silu_fp8_bytes(T=512, H=14336):
     """gate and up (fp16/bf16) read once, the fp32 dequantised output written once."""
     return T * 2 * H * 2 + T * H * 4
@@ -191,13 +202,18 @@ GRID_LINEAR = [("llama3_8b_qkv", 4096, 6144), ("llama3_8b_o", 4096, 4096),
                ("qwen2_7b_gate", 3584, 18944), ("qwen2_72b_down", 29568, 8192)]
 GRID_QMOE = [("deepseek_moe", 2048, 64, 1408), ("mixtral", 4096, 8, 14336),
              ("qwen_moe", 2048, 60, 1408)]
+GRID_MOE = [("mixtral_8x7b", 4096, 8, 14336, 2), ("grok1", 6144, 8, 8192, 2),   # generate_tasks.py:189-195
+            ("qwen2_57b", 3584, 64, 2560, 8), ("deepseek_v2_lite", 2048, 64, 1408, 6),
+            ("qwen3_30b", 2048, 128, 768, 8)]
 GRID_SILU = [("deepseek_moe", 1408), ("qwen_moe", 2560), ("mixtral", 14336)]   # generate_tasks.py:351-355
 
 
-def run_grid(torch, dev, inputs, ops):
+def run_grid(torch, dev, inputs, ops, families=None):
     """Times every task of the grid (M=16 unless the task says otherwise; T=256 for the qMoE)
-    on rotated HBM-cold inputs; one record per task."""
+    on rotated HBM-cold inputs; one record per task. `families` limits it to some of
+    w4a16, w8a8, fp8w, qmoe, moe, silu_fp8."""
     recs = []
+    fams = set(families or ["w4a16", "w8a8", "fp8w", "qmoe", "moe", "silu_fp8"])
     f16, bf16 = torch.float16, torch.bfloat16
 
     def one(name, make, fn, by, fl, peak, n_sets_bytes, **extra):
@@ -209,31 +225,38 @@ def run_grid(torch, dev, inputs, ops):
         print(f"[grid] {name}: {recs[-1]['us_batched']} us, frac {recs[-1]['roofline_frac']}",
               file=sys.stderr, flush=True)
 
-    for (n, K, N) in GRID_LAYERS:
+    for (n, K, N) in (GRID_LAYERS if "w4a16" in fams else []):
         for g, dt in ((64, f16), (128, f16), (128, bf16)):
             by = w4a16_bytes(16, K, N, g)
             one(f"w4a16 {n} g{g} {str(dt)[6:]}",
                 lambda: [t.to(dev) for t in inputs.w4a16(16, K, N, g, dt, seed=1)],
                 ops.w4a16_gemm, by, 2 * 16 * N * K, PEAK["f16"], by, M=16, K=K, N=N)
-    for (n, K, N) in GRID_LINEAR:
+    for (n, K, N) in (GRID_LINEAR if "w8a8" in fams else []):
         for M in (16, 64, 256):
             by = w8a8_bytes(M, K, N)
             one(f"w8a8 {n} M={M}",
                 lambda: [t.to(dev) for t in inputs.w8a8(M, K, N, seed=1, dist="reference")],
                 ops.w8a8_gemm, by, 2 * M * N * K, PEAK["i8"], by, M=M, K=K, N=N)
-    for (n, K, N) in GRID_LINEAR:
+    for (n, K, N) in (GRID_LINEAR if "fp8w" in fams else []):
         for b, dt in ((32, f16), (128, f16), (32, bf16)):
             by = fp8w_bytes(16, K, N, b)
             one(f"fp8w {n} b{b} {str(dt)[6:]}",
                 lambda: [t.to(dev) for t in inputs.fp8w(16, K, N, b, dt, seed=1)],
                 ops.fp8w_gemm, by, 2 * 16 * N * K, PEAK["f16"], by, M=16, K=K, N=N)
-    for (n, D, E, N) in GRID_QMOE:
+    for (n, D, E, N) in (GRID_QMOE if "qmoe" in fams else []):
         for dt in (f16, bf16):
             by = qmoe_bytes(256, D, N, E)
             one(f"qmoe {n} {str(dt)[6:]}",
                 lambda: [t.to(dev) for t in inputs.qmoe(256, D, E, N, dt, seed=1)],
                 ops.qmoe, by, qmoe_flops(256, D, N), PEAK["f16"], by, T=256, D=D, E=E, N=N)
-    for (n, H) in GRID_SILU:
+    for (n, D, E, H, k) in (GRID_MOE if "moe" in fams else []):
+        for T, dt in ((16, f16), (128, f16), (512, f16), (512, bf16)):
+            by = moe_bytes(T, D, E, H, k)
+            one(f"moe {n} top{k} T={T} {str(dt)[6:]}",
+                lambda: [t.to(dev) for t in inputs.moe(T, D, E, H, k, dt, seed=1)],
+                lambda x, w, lg, k=k: ops.moe(x, w, lg, k), by, moe_flops(T, D, H, k), PEAK["f16"],
+                E * D * H * 2, T=T, D=D, E=E, H=H, topk=k)
+    for (n, H) in (GRID_SILU if "silu_fp8" in fams else []):
         for T, dt in ((256, f16), (512, f16), (512, bf16)):
             by = silu_fp8_bytes(T, H)
             one(f"silu_fp8 {n} T={T} {str(dt)[6:]}",
@@ -287,6 +310,8 @@ def main():
     ap.add_argument("--grid", action="store_true",
                     help="only time the reference's task grid (all W4A16/W8A8/FP8/qMoE tasks at "
                          "their real shapes) and print one JSON line of per-task records")
+    ap.add_argument("--families", type=str, default="",
+                    help="with --grid: comma list of task families to time (default: all)")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                     help="only run 5 device copies of MIB MiB (calibrates rocprofv3 FETCH_SIZE/"
                          "WRITE_SIZE against a kernel of known traffic) and exit")
@@ -315,7 +340,7 @@ def main():
         print(json.dumps({"copy_probe_bytes": n, "copies": 5}))
         return
     if args.grid:
-        recs = run_grid(torch, dev, inputs, ops)
+        recs = run_grid(torch, dev, inputs, ops, [f for f in args.families.split(",") if f])
         print(json.dumps({"grid": recs, "n_gpus": 1, "data": "synthetic (seeded; the reference "
                           "task distributions; inputs rotated to stay HBM-cold)"}))
         return
