@@ -197,6 +197,25 @@ int kbh_moe(const void* x, const void* w, const void* router_logits, int logits_
             int dtype, void* stream);
 
 /* ---------------------------------------------------------------------------------------
+ * Multi-LoRA quantized linear: int4 base weight (one value per int8) plus per-token adapters.
+ * Replaces tasks/multi_lora_qgemm/multi_lora_qgemm__llama3_8b_r16__fp16/environment/
+ * reference.py:10-17 (Model.forward(x, qweight, scales, A, B, lora_ids)); template
+ * generate_tasks.py:396-420.
+ *
+ *   x [T, D] dtype; qweight [D, N] int8 (values -8..7); scales [D/group, N] dtype;
+ *   A [L, D, r] dtype; B [L, r, N] dtype; lora_ids [T] int64 (clamped to [0, L))
+ *   y [T, N] dtype = dtype(dtype(x @ dtype(q * s)) + dtype(dtype(x[t] @ A[id]) @ B[id]))
+ * Requirements: N % 128 == 0, D % 32 == 0, group in {32, 64, 128, 256} dividing D,
+ * r in {4, 8, 16, 32, 64}; x/qweight/scales/y/workspace 16-byte, A/B 8-byte aligned.
+ * workspace >= kbh_lora_qgemm_workspace_bytes(T, D, N, r), no content requirement.
+ */
+size_t kbh_lora_qgemm_workspace_bytes(int T, int D, int N, int r);
+int kbh_lora_qgemm(const void* x, const int8_t* qweight, const void* scales, const void* A,
+                   const void* B, const int64_t* lora_ids, void* y, void* workspace,
+                   size_t workspace_bytes, int T, int D, int N, int r, int L, int group, int dtype,
+                   void* stream);
+
+/* ---------------------------------------------------------------------------------------
  * Fused SiLU x up with per-group dynamic FP8 (e4m3fn) quantisation.
  * Replaces tasks/fused_silu_fp8/fused_silu_fp8__mixtral__T512__fp16/environment/reference.py:13-23
  * (Model.forward(y)); template generate_tasks.py:321-348.

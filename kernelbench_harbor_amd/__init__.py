@@ -6,7 +6,9 @@ drop-in ``nn.Module`` classes.
 """
 from ._lib import KbhError  # noqa: F401
 from .modules import (FP8WModel, FusedSiluFP8Model, MoEModel, MoETop6Model,  # noqa: F401
-                      MoETop8Model, MXFP8Model, QMoEFFNModel, QMoEModel, W4A16Model, W8A8Model)
+                      MoETop8Model, MultiLoRAQGemmModel, MXFP8Model, QMoEFFNModel, QMoEModel,
+                      W4A16Model, W8A8Model)
 
 __all__ = ["KbhError", "W4A16Model", "W8A8Model", "FP8WModel", "MXFP8Model", "QMoEModel", "QMoEFFNModel",
-           "FusedSiluFP8Model", "MoEModel", "MoETop6Model", "MoETop8Model"]
+           "FusedSiluFP8Model", "MoEModel", "MoETop6Model", "MoETop8Model",
+           "MultiLoRAQGemmModel"]

@@ -56,6 +56,8 @@ SIGNATURES = {
     "kbh_moe_workspace_bytes": (_sz, [_i, _i, _i, _i, _i]),
     "kbh_moe_route_topk": (_i, [_vp, _i, _vp, _vp, _vp, _sz, _i, _i, _i, _i, _vp]),
     "kbh_moe": (_i, [_vp, _vp, _vp, _i, _vp, _vp, _sz, _i, _i, _i, _i, _i, _i, _vp]),
+    "kbh_lora_qgemm_workspace_bytes": (_sz, [_i, _i, _i, _i]),
+    "kbh_lora_qgemm": (_i, [_vp] * 7 + [_vp, _sz] + [_i] * 7 + [_vp]),
 }
 
 

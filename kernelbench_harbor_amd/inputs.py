@@ -181,3 +181,17 @@ def moe(T: int = 16, D: int = 4096, E: int = 8, H: int = 14336, topk: int = 2,
     w = (torch.randn(E, D, H, generator=g) * 0.02).to(dtype)
     logits = _topk_distinct_logits(T, E, topk, g, dtype)
     return [x, w, logits]
+
+
+def lora_qgemm(T: int = 64, D: int = 4096, N: int = 4096, r: int = 16, L: int = 8,
+               dtype: torch.dtype = torch.float16, seed: int = 0):
+    """[x, qweight, scales, A, B, lora_ids] with the distributions of the reference task
+    (tasks/multi_lora_qgemm/*/environment/reference.py:19-27)."""
+    g = _gen(seed)
+    x = torch.randn(T, D, generator=g).to(dtype)
+    qweight = torch.randint(-8, 8, (D, N), generator=g, dtype=torch.int8)
+    scales = (torch.randn(D // 128, N, generator=g) * 0.01).to(dtype)
+    A = (torch.randn(L, D, r, generator=g) * 0.02).to(dtype)
+    B = (torch.randn(L, r, N, generator=g) * 0.02).to(dtype)
+    lora_ids = torch.randint(0, L, (T,), generator=g)
+    return [x, qweight, scales, A, B, lora_ids]

@@ -112,3 +112,15 @@ class MoETop6Model(MoEModel):
 
 class MoETop8Model(MoEModel):
     TOPK = 8
+
+
+class MultiLoRAQGemmModel(nn.Module):
+    """Multi-LoRA quantized linear (int4 base stored int8, GROUP 128 scales, batched adapters).
+
+    Reference: tasks/multi_lora_qgemm/*/environment/reference.py:10-17,
+    forward(x [T,D], qweight [D,N] int8, scales [D/128,N], A [L,D,r], B [L,r,N], lora_ids [T])
+    -> [T, N] x.dtype.
+    """
+
+    def forward(self, x, qweight, scales, A, B, lora_ids):
+        return ops.lora_qgemm(x, qweight, scales, A, B, lora_ids)

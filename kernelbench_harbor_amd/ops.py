@@ -418,3 +418,45 @@ def moe(x: torch.Tensor, w: torch.Tensor, router_logits: torch.Tensor, topk: int
                      T, D, H, E, topk, _DT_CODE[x.dtype], _stream_ptr(dev))
     _lib.check(st, "kbh_moe")
     return y
+
+
+def lora_qgemm(x: torch.Tensor, qweight: torch.Tensor, scales: torch.Tensor, A: torch.Tensor,
+               B: torch.Tensor, lora_ids: torch.Tensor) -> torch.Tensor:
+    """Multi-LoRA quantized linear: y = x @ dequant(W) + (x @ A[id]) @ B[id] per token.
+
+    Follows tasks/multi_lora_qgemm/multi_lora_qgemm__llama3_8b_r16__fp16/environment/
+    reference.py:10-17: qweight [D, N] int8 holding int4 values, scales [D/G, N] (G = D /
+    scales.shape[0]), A [L, D, r], B [L, r, N], lora_ids [T] integer; every intermediate
+    (dequantised weight, base, shrink, expand) rounded to x.dtype as the reference."""
+    _require(x.dtype in _DT_CODE and x.dim() == 2, "x must be a float16/bfloat16 [T, D] tensor")
+    T, D = x.shape
+    _require(qweight.dtype == torch.int8 and qweight.dim() == 2 and qweight.shape[0] == D,
+             f"qweight must be int8 [{D}, N], got {qweight.dtype} {tuple(qweight.shape)}")
+    N = qweight.shape[1]
+    _require(scales.dim() == 2 and scales.shape[1] == N and scales.shape[0] > 0 and
+             D % scales.shape[0] == 0, f"scales must be [D/G, {N}], got {tuple(scales.shape)}")
+    group = D // scales.shape[0]
+    _require(A.dim() == 3 and A.shape[1] == D and B.dim() == 3 and B.shape[0] == A.shape[0] and
+             B.shape[1] == A.shape[2] and B.shape[2] == N,
+             f"A must be [L, {D}, r] and B [L, r, {N}], got {tuple(A.shape)} / {tuple(B.shape)}")
+    L, r = A.shape[0], A.shape[2]
+    for name, t_ in (("scales", scales), ("A", A), ("B", B)):
+        _require(t_.dtype == x.dtype, f"{name} must have x's dtype {x.dtype}, got {t_.dtype}")
+    _require(lora_ids.dim() == 1 and lora_ids.shape[0] == T and not lora_ids.is_floating_point(),
+             f"lora_ids must be an integer [{T}] tensor")
+    _require(r in (4, 8, 16, 32, 64), f"rank r must be 4, 8, 16, 32 or 64, got {r}")
+    _require(N % 128 == 0 and D % 32 == 0, f"need N % 128 == 0 and D % 32 == 0 (D={D}, N={N})")
+    _require(group in (32, 64, 128, 256), f"group size {group} not supported")
+    dev = _check_device(x, qweight, scales, A, B, lora_ids)
+    y = torch.empty((T, N), dtype=x.dtype, device=dev)
+    if T == 0:
+        return y
+    lib = _lib.load()
+    ws = workspaces.get(lib.kbh_lora_qgemm_workspace_bytes(T, D, N, r), dev)
+    ts = [t_.contiguous() for t_ in (x, qweight, scales, A, B)]
+    ids = lora_ids.to(torch.int64).contiguous()
+    st = lib.kbh_lora_qgemm(*[t_.data_ptr() for t_ in ts], ids.data_ptr(), y.data_ptr(),
+                            ws.data_ptr(), ws.numel(), T, D, N, r, L, group, _DT_CODE[x.dtype],
+                            _stream_ptr(dev))
+    _lib.check(st, "kbh_lora_qgemm")
+    return y

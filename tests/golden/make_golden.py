@@ -13,6 +13,7 @@ move with the installed torch. The sequences follow:
   qMoE    tasks/fused_qmoe/<task>/environment/reference.py:14-21
   SiLU-FP8 tasks/fused_silu_fp8/<task>/environment/reference.py:13-23
   MoE     tasks/moe/<task>/environment/reference.py:10-17 (top-2 and top-6)
+  LoRA    tasks/multi_lora_qgemm/<task>/environment/reference.py:10-17
 
 `python tests/golden/make_golden.py [name ...]` rewrites only the named files (default: all);
 each file draws from its own seeded generator, so one can be rewritten without the others.
@@ -148,18 +149,40 @@ def moe(g):
     return out
 
 
+def lora(g):
+    """Multi-LoRA quantized linear at T=5, D=256, N=16, r=4, L=3 (GROUP 128): the reference's op
+    sequence in fp16 (native path) and on fp32-upcast inputs (the ground truth)."""
+    T, D, N, r, L, G = 5, 256, 16, 4, 3, 128
+    x = torch.randn(T, D, generator=g).half()
+    q = torch.randint(-8, 8, (D, N), generator=g, dtype=torch.int8)
+    s = (torch.randn(D // G, N, generator=g) * 0.01).half()
+    A = (torch.randn(L, D, r, generator=g) * 0.02).half()
+    B = (torch.randn(L, r, N, generator=g) * 0.02).half()
+    ids = torch.randint(0, L, (T,), generator=g)
+    out = {"x": _np(x.float()), "qweight": _np(q), "scales": _np(s.float()), "A": _np(A.float()),
+           "B": _np(B.float()), "lora_ids": _np(ids)}
+    for tag, (xx, ss, AA, BB) in (("f16", (x, s, A, B)),
+                                  ("gt", (x.float(), s.float(), A.float(), B.float()))):
+        w = (q.reshape(D // G, G, N).to(xx.dtype) * ss[:, None, :].to(xx.dtype)).reshape(D, N)
+        base = xx @ w
+        lo = torch.einsum("td,tdr->tr", xx, AA[ids])
+        lo = torch.einsum("tr,trn->tn", lo, BB[ids])
+        out[f"y_{tag}"] = _np((base + lo).float())
+    return out
+
+
 def e4m3fn_table():
     v = torch.arange(256, dtype=torch.uint8).view(torch.float8_e4m3fn).float()
     return ["nan" if np.isnan(a) else float(a).hex() for a in v.tolist()]
 
 
-SEEDS = {"w4a16": 20240611, "silu_fp8": 20240612, "moe": 20240613}
+SEEDS = {"w4a16": 20240611, "silu_fp8": 20240612, "moe": 20240613, "lora": 20240614}
 SETS = (("w4a16", w4a16), ("w8a8", w8a8), ("fp8w", fp8w), ("mxfp8", mxfp8),
         ("qmoe_route", qmoe_route))
 
 
 def main(names=()):
-    names = set(names) or {n for n, _ in SETS} | {"silu_fp8", "moe", "e4m3fn_table"}
+    names = set(names) or {n for n, _ in SETS} | {"silu_fp8", "moe", "lora", "e4m3fn_table"}
     # The first five sets share one generator, drawn in this order (as first written).
     if names & {n for n, _ in SETS}:
         g = torch.Generator().manual_seed(SEEDS["w4a16"])
@@ -173,6 +196,9 @@ def main(names=()):
     if "moe" in names:
         g = torch.Generator().manual_seed(SEEDS["moe"])
         np.savez(os.path.join(HERE, "moe.npz"), **moe(g))
+    if "lora" in names:
+        g = torch.Generator().manual_seed(SEEDS["lora"])
+        np.savez(os.path.join(HERE, "lora.npz"), **lora(g))
     if "e4m3fn_table" in names:
         with open(os.path.join(HERE, "e4m3fn_table.json"), "w") as f:
             json.dump({"source": "torch.float8_e4m3fn -> float32, codes 0..255",

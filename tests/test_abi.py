@@ -84,6 +84,16 @@ def test_host_checks_run_without_gpu():
     assert lib.kbh_moe(p, p, p, 3, p, p, need, 16, 4096, 14336, 8, 2, 0, None) == _lib.KBH_ERR_DTYPE
     assert lib.kbh_moe(None, p, p, 0, p, p, need, 16, 4096, 14336, 8, 2, 0, None) == _lib.KBH_ERR_NULL
     assert lib.kbh_moe_route_topk(p, 0, p, p, p, need, 16, 4, 6, 0, None) == _lib.KBH_ERR_SHAPE
+    # multi-LoRA: rank, group, N divisibility, workspace
+    need = lib.kbh_lora_qgemm_workspace_bytes(64, 4096, 4096, 16)
+    assert need >= 64 * 16 * 2
+    args = lambda T=64, D=4096, N=4096, r=16, g=128, dt=0, ws=need: (
+        p, p, p, p, p, p, p, p, ws, T, D, N, r, 8, g, dt, None)
+    assert lib.kbh_lora_qgemm(*args(r=12)) == _lib.KBH_ERR_SHAPE
+    assert lib.kbh_lora_qgemm(*args(g=100)) == _lib.KBH_ERR_SHAPE
+    assert lib.kbh_lora_qgemm(*args(N=4000)) == _lib.KBH_ERR_SHAPE
+    assert lib.kbh_lora_qgemm(*args(dt=2)) == _lib.KBH_ERR_DTYPE
+    assert lib.kbh_lora_qgemm(*args(ws=need - 1)) == _lib.KBH_ERR_WORKSPACE
 
 
 def test_workspace_sizes():

@@ -1,0 +1,65 @@
+"""GPU parity of the multi-LoRA quantized linear (kbh_lora_qgemm) against the CPU oracle
+(oracle/lora.py): the reference's six tasks at their real shapes (generate_tasks.py:427-431,
+632-638: T=64, three adapter configurations x fp16/bf16) and ragged cases to the BASELINE
+tolerance against the fp32 ground truth, and one-hot activations with dyadic adapters (every
+sum exact in fp32) bit-exactly against the oracle's native-dtype path, which checks each
+rounding: dequantised weight, base, shrink, expand and the final add."""
+import numpy as np
+import pytest
+import torch
+
+from kernelbench_harbor_amd import MultiLoRAQGemmModel, inputs, ops
+from kernelbench_harbor_amd.harness import compare
+from oracle import lora as ol
+
+pytestmark = pytest.mark.gpu
+
+
+def _np(ts):
+    return [t.float().numpy() if t.is_floating_point() else t.numpy() for t in ts]
+
+
+LORA_CFG = [("llama3_8b_r16", 4096, 4096, 16, 8), ("qwen_7b_r32", 3584, 3584, 32, 8),
+            ("llama3_8b_r64", 4096, 4096, 64, 4)]
+GRID = [(n, D, N, r, L, dt) for (n, D, N, r, L) in LORA_CFG for dt in (torch.float16, torch.bfloat16)]
+
+
+@pytest.mark.parametrize("name,D,N,r,L,dtype", GRID)
+def test_reference_task(dev, name, D, N, r, L, dtype):
+    print(f"[lora] {name} D={D} N={N} r={r} L={L} {dtype}", flush=True)
+    ins = inputs.lora_qgemm(64, D, N, r, L, dtype, seed=D + r)
+    y = MultiLoRAQGemmModel()(*[t.to(dev) for t in ins])
+    assert y.dtype == dtype and y.shape == (64, N)
+    cmp = compare(y, ol.forward(*_np(ins)))
+    assert cmp.ok, cmp
+    assert torch.equal(y, MultiLoRAQGemmModel()(*[t.to(dev) for t in ins]))
+
+
+@pytest.mark.parametrize("T,D,N,r,L,dtype", [
+    (1, 256, 128, 4, 2, torch.float16),
+    (17, 512, 384, 8, 3, torch.bfloat16),
+    (130, 1024, 256, 32, 5, torch.float16),      # M >= 128: tiled base GEMM
+    (200, 1056, 256, 16, 4, torch.bfloat16),     # D % 128 != 0 (group 32): split-K at M >= 128
+])
+def test_ragged(dev, T, D, N, r, L, dtype):
+    print(f"[lora ragged] T={T} D={D} N={N} r={r} L={L} {dtype}", flush=True)
+    x, q, s, A, B, ids = inputs.lora_qgemm(T, D, N, r, L, dtype, seed=T)
+    if D % 128:
+        s = (torch.randn(D // 32, N, generator=torch.Generator().manual_seed(1)) * 0.01).to(dtype)
+    y = ops.lora_qgemm(*[t.to(dev) for t in (x, q, s, A, B, ids)])
+    cmp = compare(y, ol.forward(*_np([x, q, s, A, B, ids])))
+    assert cmp.ok, cmp
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_one_hot_matches_native_rounding(dev, dtype):
+    T, D, N, r, L = 48, 512, 256, 16, 4
+    _, q, s, _, _, ids = inputs.lora_qgemm(T, D, N, r, L, dtype, seed=7)
+    g = torch.Generator().manual_seed(8)
+    A = (torch.randint(-8, 8, (L, D, r), generator=g).float() / 16).to(dtype)
+    B = (torch.randint(-8, 8, (L, r, N), generator=g).float() / 64).to(dtype)
+    x = torch.zeros(T, D, dtype=dtype)
+    x[torch.arange(T), torch.randint(0, D, (T,), generator=g)] = 1.0
+    y = ops.lora_qgemm(*[t.to(dev) for t in (x, q, s, A, B, ids)]).float().cpu().numpy()
+    want = ol.forward(*_np([x, q, s, A, B, ids]), dtype="f16" if dtype == torch.float16 else "bf16")
+    assert np.array_equal(y, want), np.abs(y - want).max()

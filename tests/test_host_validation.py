@@ -100,3 +100,22 @@ def test_moe_rejects_bad_inputs():
         ops.moe(x, torch.zeros(8, 256, 100, dtype=torch.float16), lg, 2)
     with pytest.raises(ValueError, match="HIP device"):
         ops.moe(x, w, lg, 2)
+
+
+def test_lora_rejects_bad_inputs():
+    x, q, s, A, B, ids = (torch.zeros(4, 256, dtype=torch.float16),
+                          torch.zeros(256, 128, dtype=torch.int8),
+                          torch.zeros(2, 128, dtype=torch.float16),
+                          torch.zeros(3, 256, 16, dtype=torch.float16),
+                          torch.zeros(3, 16, 128, dtype=torch.float16),
+                          torch.zeros(4, dtype=torch.int64))
+    with pytest.raises(ValueError, match="int8"):
+        ops.lora_qgemm(x, q.to(torch.int32), s, A, B, ids)
+    with pytest.raises(ValueError, match="rank"):
+        ops.lora_qgemm(x, q, s, A[:, :, :12], B[:, :12], ids)
+    with pytest.raises(ValueError, match="x's dtype"):
+        ops.lora_qgemm(x, q, s, A.bfloat16(), B, ids)
+    with pytest.raises(ValueError, match="integer"):
+        ops.lora_qgemm(x, q, s, A, B, ids.float())
+    with pytest.raises(ValueError, match="HIP device"):
+        ops.lora_qgemm(x, q, s, A, B, ids)
