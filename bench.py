@@ -96,6 +96,15 @@ def moe_flops(T, D, H, k):
     return 2 * T * k * D * H
 
 
+def lora_bytes(T, D, N, r, L):
+    """int8 base weight + scales + every adapter (ids drawn uniformly: all touched) + x + y."""
+    return D * N + 2 * (D // 128) * N + 2 * L * r * (D + N) + 2 * T * D + 2 * T * N + 8 * T
+
+
+def lora_flops(T, D, N, r):
+    return 2 * T * N * D + 2 * T * r * (D + N)
+
+
 def silu_fp8_bytes(T=512, H=14336):
     """gate and up (fp16/bf16) read once, the fp32 dequantised output written once."""
     return T * 2 * H * 2 + T * H * 4
@@ -205,15 +214,17 @@ GRID_QMOE = [("deepseek_moe", 2048, 64, 1408), ("mixtral", 4096, 8, 14336),
 GRID_MOE = [("mixtral_8x7b", 4096, 8, 14336, 2), ("grok1", 6144, 8, 8192, 2),   # generate_tasks.py:189-195
             ("qwen2_57b", 3584, 64, 2560, 8), ("deepseek_v2_lite", 2048, 64, 1408, 6),
             ("qwen3_30b", 2048, 128, 768, 8)]
+GRID_LORA = [("llama3_8b_r16", 4096, 4096, 16, 8), ("qwen_7b_r32", 3584, 3584, 32, 8),  # generate_tasks.py:427-431
+             ("llama3_8b_r64", 4096, 4096, 64, 4)]
 GRID_SILU = [("deepseek_moe", 1408), ("qwen_moe", 2560), ("mixtral", 14336)]   # generate_tasks.py:351-355
 
 
 def run_grid(torch, dev, inputs, ops, families=None):
     """Times every task of the grid (M=16 unless the task says otherwise; T=256 for the qMoE)
     on rotated HBM-cold inputs; one record per task. `families` limits it to some of
-    w4a16, w8a8, fp8w, qmoe, moe, silu_fp8."""
+    w4a16, w8a8, fp8w, qmoe, moe, lora, silu_fp8."""
     recs = []
-    fams = set(families or ["w4a16", "w8a8", "fp8w", "qmoe", "moe", "silu_fp8"])
+    fams = set(families or ["w4a16", "w8a8", "fp8w", "qmoe", "moe", "lora", "silu_fp8"])
     f16, bf16 = torch.float16, torch.bfloat16
 
     def one(name, make, fn, by, fl, peak, n_sets_bytes, **extra):
@@ -256,6 +267,13 @@ def run_grid(torch, dev, inputs, ops, families=None):
                 lambda: [t.to(dev) for t in inputs.moe(T, D, E, H, k, dt, seed=1)],
                 lambda x, w, lg, k=k: ops.moe(x, w, lg, k), by, moe_flops(T, D, H, k), PEAK["f16"],
                 E * D * H * 2, T=T, D=D, E=E, H=H, topk=k)
+    for (n, D, N, r, L) in (GRID_LORA if "lora" in fams else []):
+        for dt in (f16, bf16):
+            by = lora_bytes(64, D, N, r, L)
+            one(f"lora {n} {str(dt)[6:]}",
+                lambda: [t.to(dev) for t in inputs.lora_qgemm(64, D, N, r, L, dt, seed=1)],
+                ops.lora_qgemm, by, lora_flops(64, D, N, r), PEAK["f16"], by, T=64, D=D, N=N, r=r,
+                L=L)
     for (n, H) in (GRID_SILU if "silu_fp8" in fams else []):
         for T, dt in ((256, f16), (512, f16), (512, bf16)):
             by = silu_fp8_bytes(T, H)

@@ -11,7 +11,9 @@
 // Both kernels transpose 4x4 byte blocks in registers so that each lane holds consecutive k of
 // one column, as the MFMA B operand needs.
 //  * byte_decode_kernel (small M): a wave owns 128 columns (8 per lane, dwordx2 loads) and SPW
-//    steps of 32 k; all loads up front; 16x16x32 fp16/bf16 MFMAs; split-K epilogue of splitk.h.
+//    steps of 32 k for MB blocks of 16 rows (each dequantised weight fragment feeds MB MFMAs, so
+//    the weights are streamed once per 16 MB rows); all loads up front; 16x16x32 fp16/bf16
+//    MFMAs; split-K epilogue of splitk.h, once per row block.
 //  * larger M: tiled_f16_gemm (tiled_f16.h) with ByteSlabPolicy.
 #pragma once
 
@@ -79,7 +81,7 @@ __device__ inline uint16_t half_of(kbh_u32x4 v, int i) {
   return (uint16_t)((i & 1) ? (v[i >> 1] >> 16) : (v[i >> 1] & 0xffffu));
 }
 
-template <int SPW, bool BF16, int DEC>
+template <int SPW, bool BF16, int DEC, int MB>
 __global__ __launch_bounds__(kSplitKMaxWaves * 64) void byte_decode_kernel(
     const uint16_t* __restrict__ x, const uint8_t* __restrict__ w,
     const uint16_t* __restrict__ scales, uint16_t* __restrict__ y, float* __restrict__ acc,
@@ -93,7 +95,7 @@ __global__ __launch_bounds__(kSplitKMaxWaves * 64) void byte_decode_kernel(
   const int id = xcd_remap(blockIdx.x, gridDim.x);
   const int tile = id / splits, split = id - tile * splits;
   const int n0 = tile * NWG;
-  const int m0 = blockIdx.y * 16;
+  const int m0 = blockIdx.y * 16 * MB;
   const int st0 = (split * waves + wave) * SPW;  // first 32-deep K step of this wave
 
   // lane (c, g): rows k0 + 8g + i (i < 8), bytes n0 + 8c .. +7
@@ -104,23 +106,31 @@ __global__ __launch_bounds__(kSplitKMaxWaves * 64) void byte_decode_kernel(
 #pragma unroll
     for (int i = 0; i < 8; ++i)
       wd[u][i] = __builtin_nontemporal_load(reinterpret_cast<const kbh_u32x2*>(wb + (size_t)(u * 32 + i) * N));
-  kbh_u32x4 af[SPW], sv[SPW];
-  const bool xok = m0 + c < M;
-  const uint16_t* xb = x + (size_t)(xok ? m0 + c : 0) * K + st0 * 32 + 8 * g;
+  kbh_u32x4 af[SPW][MB], sv[SPW];
+  bool xok[MB];
 #pragma unroll
-  for (int u = 0; u < SPW; ++u) {
-    af[u] = *reinterpret_cast<const kbh_u32x4*>(xb + u * 32);
-    sv[u] = *reinterpret_cast<const kbh_u32x4*>(scales + (size_t)(((st0 + u) * 32) / block) * N + n0 + 8 * c);
+  for (int mb = 0; mb < MB; ++mb) {
+    xok[mb] = m0 + 16 * mb + c < M;
+    const uint16_t* xb = x + (size_t)(xok[mb] ? m0 + 16 * mb + c : 0) * K + st0 * 32 + 8 * g;
+#pragma unroll
+    for (int u = 0; u < SPW; ++u) af[u][mb] = *reinterpret_cast<const kbh_u32x4*>(xb + u * 32);
   }
+#pragma unroll
+  for (int u = 0; u < SPW; ++u)
+    sv[u] = *reinterpret_cast<const kbh_u32x4*>(scales + (size_t)(((st0 + u) * 32) / block) * N + n0 + 8 * c);
   // All loads are issued before any use (a consumer between them stalls the stream).
   __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
   for (int u = 0; u < SPW; ++u)
-    if (!xok) af[u] = kbh_u32x4{0u, 0u, 0u, 0u};  // rows past M contribute zero
-
-  kbh_f32x4 part[NCS];
 #pragma unroll
-  for (int cs = 0; cs < NCS; ++cs) part[cs] = kbh_f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int mb = 0; mb < MB; ++mb)
+      if (!xok[mb]) af[u][mb] = kbh_u32x4{0u, 0u, 0u, 0u};  // rows past M contribute zero
+
+  kbh_f32x4 part[MB][NCS];
+#pragma unroll
+  for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+    for (int cs = 0; cs < NCS; ++cs) part[mb][cs] = kbh_f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int u = 0; u < SPW; ++u) {
 #pragma unroll
@@ -142,14 +152,21 @@ __global__ __launch_bounds__(kSplitKMaxWaves * 64) void byte_decode_kernel(
         const kbh_u32x2 lo = byte4_dequant<BF16, DEC>(col[j][0], s);
         const kbh_u32x2 hi = byte4_dequant<BF16, DEC>(col[j][1], s);
         const kbh_u32x4 bf = {lo[0], lo[1], hi[0], hi[1]};
-        part[cs] = mfma16x16x32<BF16>(af[u], bf, part[cs]);
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb) part[mb][cs] = mfma16x16x32<BF16>(af[u][mb], bf, part[mb][cs]);
       }
     }
   }
-  const int rows = min(16, M - m0);
-  splitk_reduce<NCS, float>(part, sm, acc, split, splits, rows, M, N, m0, n0, [&](int r, int n, float v) {
-    y[(size_t)(m0 + r) * N + n0 + n] = f32_to_half_bits<BF16>(v);
-  });
+#pragma unroll
+  for (int mb = 0; mb < MB; ++mb) {
+    const int mr = m0 + 16 * mb;
+    const int rows = min(16, M - mr);
+    if (rows <= 0) break;      // uniform across the workgroup
+    if (mb) __syncthreads();   // the previous block's LDS reads are done
+    splitk_reduce<NCS, float>(part[mb], sm, acc, split, splits, rows, M, N, mr, n0, [&](int r, int n, float v) {
+      y[(size_t)(mr + r) * N + n0 + n] = f32_to_half_bits<BF16>(v);
+    });
+  }
 }
 
 // Weight-slab producer for tiled_f16_gemm: thread t loads rows 4*(t/32) .. +3 of the slab for
@@ -186,16 +203,20 @@ struct ByteSlabPolicy {
 constexpr int kByteTiledMinM = 128;
 
 struct BytePlan {
-  int spw, waves, ntiles, mblocks, splits;
+  int spw, waves, ntiles, mb, mblocks, splits;
 };
 
-// 4-step (128-deep) wave K ranges when they divide K, waves per workgroup and K splits as for the
-// W4 decode kernel.
+// Row blocks per wave (MB: 1 up to 16 rows, 2 up to 32, 4 up to 64, then 16-row blocks of 4),
+// 4-step (128-deep) wave K ranges when they divide K (2 at MB = 4, for registers), waves per
+// workgroup and K splits as for the W4 decode kernel.
 bool plan_byte_decode(int M, int N, int K, BytePlan* p) {
   const int nsteps = K / 32;
-  p->spw = (nsteps % 4 == 0) ? 4 : (nsteps % 2 == 0 ? 2 : 1);
+  const int m16 = (M + 15) / 16;
+  p->mb = m16 <= 1 ? 1 : (m16 <= 2 ? 2 : 4);
+  const int smax = p->mb == 4 ? 2 : 4;
+  p->spw = (nsteps % smax == 0) ? smax : (nsteps % 2 == 0 ? 2 : 1);
   p->ntiles = N / 128;
-  p->mblocks = (M + 15) / 16;
+  p->mblocks = (m16 + p->mb - 1) / p->mb;
   p->splits = 0;
   p->waves = splitk_pick_waves(nsteps / p->spw, p->ntiles * p->mblocks, &p->splits);
   return p->waves > 0;
@@ -218,12 +239,14 @@ int byte_gemm_run(const void* x, const void* w, const void* scales, void* y, voi
   if (need > 0 && !aligned16(workspace)) return KBH_ERR_ALIGN;
   dim3 grid(pl.ntiles * splits, pl.mblocks);
   float* acc = (float*)workspace;
-#define KBH_BYTE_DEC(SPW_)                                                                       \
-  if (spw == SPW_)                                                                               \
-    hipLaunchKernelGGL((byte_decode_kernel<SPW_, BF16, DEC>), grid, dim3(waves * 64), 0, st,      \
+#define KBH_BYTE_DEC(SPW_, MB_)                                                                  \
+  if (spw == SPW_ && pl.mb == MB_)                                                               \
+    hipLaunchKernelGGL((byte_decode_kernel<SPW_, BF16, DEC, MB_>), grid, dim3(waves * 64), 0, st, \
                        (const uint16_t*)x, (const uint8_t*)w, (const uint16_t*)scales,           \
                        (uint16_t*)y, acc, M, N, K, block, splits);
-  KBH_BYTE_DEC(4) else KBH_BYTE_DEC(2) else KBH_BYTE_DEC(1)
+  KBH_BYTE_DEC(4, 1) else KBH_BYTE_DEC(2, 1) else KBH_BYTE_DEC(1, 1)
+  else KBH_BYTE_DEC(4, 2) else KBH_BYTE_DEC(2, 2) else KBH_BYTE_DEC(1, 2)
+  else KBH_BYTE_DEC(2, 4) else KBH_BYTE_DEC(1, 4)
 #undef KBH_BYTE_DEC
   if (splits > 1)
     launch_splitk_sum(reinterpret_cast<const kbh_f32x4*>(acc), HalfOut<BF16>{(uint16_t*)y, N}, M, N,

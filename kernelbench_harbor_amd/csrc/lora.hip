@@ -9,8 +9,10 @@
 //   y    = dtype(base + dtype(lo[t] @ B[id_t]))                      [T, N]      (:16-17)
 // Three launches (plus the split-K slice sum of the base GEMM): the base GEMM is the byte-weight
 // GEMM of byte_weight_gemm.h with the int8 decoder, writing base into y; lora_shrink_kernel
-// computes lo (one workgroup per token); lora_expand_add_kernel adds dtype(lo @ B) to y in place
-// (four columns per thread). Adapter ids outside [0, L) are clamped (torch would raise).
+// computes fp32 partial sums of x[t] @ A[id] over DS ranges of D (T x DS workgroups, so that a
+// few tokens still fill the chip); lora_expand_add_kernel sums the DS partials in order, rounds
+// lo to dtype and adds dtype(lo @ B) to y in place (four columns per thread). Adapter ids
+// outside [0, L) are clamped (torch would raise).
 #include "byte_weight_gemm.h"
 
 namespace kbh {
@@ -18,21 +20,24 @@ namespace {
 
 constexpr int kLoraMaxRank = 64;
 constexpr int kLoraThreads = 256;
+constexpr int kLoraMaxSplits = 16;  // D ranges of the shrink
 
 __device__ inline int lora_id(const int64_t* ids, int t, int L) {
   const int64_t v = ids[t];
   return v < 0 ? 0 : (v >= L ? L - 1 : (int)v);
 }
 
-// lo[t][j] = dtype(sum_d x[t][d] A[id][d][j]) in fp32. Lane (row rr, column group c4) of a wave
-// reads 8 bytes (columns 4c4..4c4+3) of row d of A; a wave covers 256 / r rows per step, the
-// four waves interleave their rows; partial sums meet by lane shuffles, then across waves in LDS.
+// part[ds][t][j] = sum over d in range ds of x[t][d] A[id][d][j], fp32. Lane (row rr, column
+// group c4) of a wave reads 8 bytes (columns 4c4..4c4+3) of row d of A; a wave covers 256 / r
+// rows per step, the four waves interleave their rows; partial sums meet by lane shuffles, then
+// across waves in LDS.
 template <bool BF16>
 __global__ __launch_bounds__(kLoraThreads) void lora_shrink_kernel(
     const uint16_t* __restrict__ x, const uint16_t* __restrict__ A, const int64_t* __restrict__ ids,
-    uint16_t* __restrict__ lo, int D, int r, int L) {
+    float* __restrict__ out, int T, int D, int r, int L, int dchunk) {
   __shared__ float part[kLoraThreads / 64][kLoraMaxRank];
   const int t = blockIdx.x;
+  const int d0 = blockIdx.y * dchunk, d1 = min(D, d0 + dchunk);
   const int l = lora_id(ids, t, L);
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int lpr = r >> 2;          // lanes per row of A
@@ -42,8 +47,8 @@ __global__ __launch_bounds__(kLoraThreads) void lora_shrink_kernel(
   const uint16_t* Al = A + (size_t)l * D * r + 4 * c4;
   float acc[4] = {0.f, 0.f, 0.f, 0.f};
   const int step = 4 * rps;
-  int d = wave * rps + rr;
-  for (; d + 3 * step < D; d += 4 * step) {  // four rows in flight
+  int d = d0 + wave * rps + rr;
+  for (; d + 3 * step < d1; d += 4 * step) {  // four rows in flight
     kbh_u32x2 a[4];
     float xv[4];
 #pragma unroll
@@ -57,7 +62,7 @@ __global__ __launch_bounds__(kLoraThreads) void lora_shrink_kernel(
       for (int c = 0; c < 4; ++c)
         acc[c] += xv[u] * half_bits_to_f32<BF16>((uint16_t)(a[u][c >> 1] >> (16 * (c & 1))));
   }
-  for (; d < D; d += step) {
+  for (; d < d1; d += step) {
     const kbh_u32x2 a = *reinterpret_cast<const kbh_u32x2*>(Al + (size_t)d * r);
     const float xv = half_bits_to_f32<BF16>(xr[d]);
 #pragma unroll
@@ -73,20 +78,30 @@ __global__ __launch_bounds__(kLoraThreads) void lora_shrink_kernel(
   __syncthreads();
   if (threadIdx.x < r) {
     const int j = threadIdx.x;
-    const float v = part[0][j] + part[1][j] + part[2][j] + part[3][j];
-    lo[(size_t)t * r + j] = f32_to_half_bits<BF16>(v);
+    out[((size_t)blockIdx.y * T + t) * r + j] = part[0][j] + part[1][j] + part[2][j] + part[3][j];
   }
 }
 
+// lo[t][j] = dtype(sum over ds in order of part[ds][t][j]);
 // y[t][n] = dtype(fp32(y[t][n]) + fp32(dtype(sum_j lo[t][j] B[id][j][n]))), y holding base.
 template <bool BF16>
 __global__ __launch_bounds__(kLoraThreads) void lora_expand_add_kernel(
-    const uint16_t* __restrict__ lo, const uint16_t* __restrict__ B, const int64_t* __restrict__ ids,
-    uint16_t* __restrict__ y, int N, int r, int L) {
+    const float* __restrict__ part, const uint16_t* __restrict__ B, const int64_t* __restrict__ ids,
+    uint16_t* __restrict__ y, int T, int N, int r, int L, int ds) {
   __shared__ float los[kLoraMaxRank];
   const int t = blockIdx.y;
   const int l = lora_id(ids, t, L);
-  if (threadIdx.x < r) los[threadIdx.x] = half_bits_to_f32<BF16>(lo[(size_t)t * r + threadIdx.x]);
+  if (threadIdx.x < r) {
+    float pv[kLoraMaxSplits];  // all partials requested before the first add
+#pragma unroll
+    for (int s = 0; s < kLoraMaxSplits; ++s)
+      pv[s] = s < ds ? part[((size_t)s * T + t) * r + threadIdx.x] : 0.f;
+    float v = pv[0];
+#pragma unroll
+    for (int s = 1; s < kLoraMaxSplits; ++s)
+      if (s < ds) v += pv[s];
+    los[threadIdx.x] = half_bits_to_f32<BF16>(f32_to_half_bits<BF16>(v));
+  }
   __syncthreads();
   const int n = (blockIdx.x * kLoraThreads + threadIdx.x) * 4;
   if (n >= N) return;
@@ -119,14 +134,20 @@ __global__ __launch_bounds__(kLoraThreads) void lora_expand_add_kernel(
 }
 
 struct LoraLayout {
-  size_t gemm, lo, total;
+  size_t part, total;
+  int ds, dchunk;
 };
 
+// DS ranges of D for the shrink: enough workgroups (T x DS >= 1024, DS <= 16) while each keeps
+// at least four steps of 1024 / r rows (one round of four loads in flight per lane).
 LoraLayout lora_layout(int T, int D, int N, int r) {
   LoraLayout L;
-  L.gemm = 0;
-  L.lo = round_up(byte_gemm_workspace_bytes(T, N, D), 256);
-  L.total = L.lo + round_up((size_t)T * r * 2, 256);
+  const int step = 1024 / r;
+  const int ds_max = max(1, min(kLoraMaxSplits, D / (4 * step)));
+  L.ds = max(1, min((1024 + T - 1) / T, ds_max));
+  L.dchunk = (D + L.ds - 1) / L.ds;
+  L.part = round_up(byte_gemm_workspace_bytes(T, N, D), 256);
+  L.total = L.part + round_up((size_t)L.ds * T * r * 4, 256);
   return L;
 }
 
@@ -135,14 +156,14 @@ int lora_run(const void* x, const int8_t* qweight, const void* scales, const voi
              const void* B, const int64_t* ids, void* y, void* ws, size_t ws_bytes, int T, int D,
              int N, int r, int L, int group, hipStream_t st) {
   const LoraLayout lay = lora_layout(T, D, N, r);
-  uint16_t* lo = (uint16_t*)((char*)ws + lay.lo);
-  const int s = byte_gemm_run<BF16, kDecInt8>(x, qweight, scales, y, ws, lay.lo, T, N, D, group, st);
+  float* part = (float*)((char*)ws + lay.part);
+  const int s = byte_gemm_run<BF16, kDecInt8>(x, qweight, scales, y, ws, lay.part, T, N, D, group, st);
   if (s != KBH_OK) return s;
-  hipLaunchKernelGGL(lora_shrink_kernel<BF16>, dim3(T), dim3(kLoraThreads), 0, st,
-                     (const uint16_t*)x, (const uint16_t*)A, ids, lo, D, r, L);
+  hipLaunchKernelGGL(lora_shrink_kernel<BF16>, dim3(T, lay.ds), dim3(kLoraThreads), 0, st,
+                     (const uint16_t*)x, (const uint16_t*)A, ids, part, T, D, r, L, lay.dchunk);
   const dim3 grid((N / 4 + kLoraThreads - 1) / kLoraThreads, T);
   hipLaunchKernelGGL(lora_expand_add_kernel<BF16>, grid, dim3(kLoraThreads), 0, st,
-                     (const uint16_t*)lo, (const uint16_t*)B, ids, (uint16_t*)y, N, r, L);
+                     (const float*)part, (const uint16_t*)B, ids, (uint16_t*)y, T, N, r, L, lay.ds);
   return launch_status();
 }
 
