@@ -112,71 +112,95 @@ __global__ __launch_bounds__(1024) void moe_route_kernel(const void* __restrict_
   }
 }
 
-// Top-k routing (k <= kMoeMaxTopk) for the fp16/bf16-weight MoE (tasks/moe/<task>/environment/
-// reference.py:11-13): probs = softmax(fp32 logits), the k largest in descending order (the lower
-// expert index first among equal logits: an expert only displaces strictly smaller entries),
-// weights p_j / sum_j p_j (summed in k order) rounded to the activation dtype. Slots, permutation
-// (perm[slot] = k t + j) and tile table as moe_route_kernel. Indices start as 0..k-1 so that
-// every id is in range whatever the logits hold (NaN, -inf).
+// Top-k routing (k <= kMoeMaxTopk, E <= kMoeMaxExperts) for the fp16/bf16-weight MoE
+// (tasks/moe/<task>/environment/reference.py:11-13), in two kernels:
+//  * moe_topk_select_kernel: one wave per token, lanes across experts (up to 4 each). The
+//    softmax max and sum are wave reductions; the k picks are k rounds of a wave argmax on
+//    (logit descending, index ascending), so the lower expert index wins a tie, each pick
+//    excluded from the later rounds. NaN logits rank as -inf (every id is a distinct expert in
+//    range). Weights p_j / sum_j p_j (summed in k order) rounded to the activation dtype.
+//  * moe_route_build_kernel (one workgroup): per-expert slot counts (LDS atomics), offsets,
+//    the permutation perm[slot] = k t + j and the tile table, as moe_route_kernel.
 constexpr int kMoeMaxTopk = 8;
+constexpr int kTopkWaves = 4;  // tokens per workgroup of the select kernel
+
 template <int LDT>
-__global__ __launch_bounds__(1024) void moe_route_topk_kernel(const void* __restrict__ logits,
-                                                              int T, int E, int K, int out_bf16,
-                                                              MoeBuffers mb, int max_tiles, int bm) {
+__global__ __launch_bounds__(kTopkWaves * 64) void moe_topk_select_kernel(
+    const void* __restrict__ logits, int T, int E, int K, int out_bf16, MoeBuffers mb) {
+  constexpr int EPL = kMoeMaxExperts / 64;
+  const int lane = threadIdx.x & 63;
+  const int t = blockIdx.x * kTopkWaves + (threadIdx.x >> 6);
+  if (t >= T) return;  // whole waves
+  const size_t row = (size_t)t * E;
+  float v[EPL];
+  float mx = -INFINITY;
+#pragma unroll
+  for (int i = 0; i < EPL; ++i) {
+    const int e = lane + 64 * i;
+    v[i] = e < E ? logit_at<LDT>(logits, row + e) : -INFINITY;
+    mx = fmaxf(mx, v[i]);
+  }
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+  float sum = 0.f;
+#pragma unroll
+  for (int i = 0; i < EPL; ++i)
+    if (lane + 64 * i < E) sum += expf(v[i] - mx);
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) sum += __shfl_xor(sum, o, 64);
+  unsigned taken = 0;
+  float lv[kMoeMaxTopk];
+  int li[kMoeMaxTopk];
+#pragma unroll
+  for (int j = 0; j < kMoeMaxTopk; ++j) {
+    lv[j] = -INFINITY;
+    li[j] = 0;
+    if (j >= K) continue;
+    float bv = -INFINITY;
+    int be = kMoeMaxExperts;  // sentinel above every index
+#pragma unroll
+    for (int i = 0; i < EPL; ++i) {
+      const int e = lane + 64 * i;
+      const float w = v[i] != v[i] ? -INFINITY : v[i];
+      if (e < E && !((taken >> i) & 1u) && (w > bv || (w == bv && e < be))) { bv = w; be = e; }
+    }
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) {
+      const float ov = __shfl_xor(bv, o, 64);
+      const int oe = __shfl_xor(be, o, 64);
+      if (ov > bv || (ov == bv && oe < be)) { bv = ov; be = oe; }
+    }
+    if ((be & 63) == lane) taken |= 1u << (be >> 6);
+    li[j] = be;
+    lv[j] = logit_at<LDT>(logits, row + be);
+  }
+  float pk[kMoeMaxTopk], ps = 0.f;
+#pragma unroll
+  for (int j = 0; j < kMoeMaxTopk; ++j) {
+    if (j < K) {
+      pk[j] = keep_f32(expf(lv[j] - mx) / sum);
+      ps = keep_f32(ps + pk[j]);
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < kMoeMaxTopk; ++j) {
+    if (j < K && lane == j) {
+      const float w = keep_f32(pk[j] / ps);
+      mb.topi[K * t + j] = li[j];
+      mb.topw[K * t + j] = out_bf16 ? f32_to_bf16_bits(w) : f32_to_f16_bits(w);
+    }
+  }
+}
+
+__global__ __launch_bounds__(1024) void moe_route_build_kernel(int T, int E, int K, MoeBuffers mb,
+                                                               int max_tiles, int bm) {
   __shared__ int cnt[kMoeMaxExperts];
   __shared__ int off[kMoeMaxExperts];
   __shared__ int tbase[kMoeMaxExperts + 1];
+  const int S = K * T;
   for (int e = threadIdx.x; e < E; e += blockDim.x) cnt[e] = 0;
   __syncthreads();
-  for (int t = threadIdx.x; t < T; t += blockDim.x) {
-    const size_t row = (size_t)t * E;
-    float lv[kMoeMaxTopk];
-    int li[kMoeMaxTopk];
-#pragma unroll
-    for (int j = 0; j < kMoeMaxTopk; ++j) {
-      lv[j] = -INFINITY;
-      li[j] = j < K ? j : 0;
-    }
-    float mx = -INFINITY;
-    for (int e = 0; e < E; ++e) {
-      const float v = logit_at<LDT>(logits, row + e);
-      mx = fmaxf(mx, v);
-      if (!(v > lv[K - 1])) continue;
-      // insertion into the descending list: entries below position p shift down by one
-      int p = K - 1;
-#pragma unroll
-      for (int j = kMoeMaxTopk - 1; j > 0; --j) {
-        if (j < K && j <= p && v > lv[j - 1]) {
-          lv[j] = lv[j - 1];
-          li[j] = li[j - 1];
-          p = j - 1;
-        }
-      }
-#pragma unroll
-      for (int j = 0; j < kMoeMaxTopk; ++j)
-        if (j == p) { lv[j] = v; li[j] = e; }
-    }
-    float sum = 0.f;
-    for (int e = 0; e < E; ++e) sum += expf(logit_at<LDT>(logits, row + e) - mx);
-    float pk[kMoeMaxTopk], ps = 0.f;
-#pragma unroll
-    for (int j = 0; j < kMoeMaxTopk; ++j) {
-      if (j < K) {
-        pk[j] = keep_f32(expf(logit_at<LDT>(logits, row + li[j]) - mx) / sum);
-        ps = keep_f32(ps + pk[j]);
-      }
-    }
-#pragma unroll
-    for (int j = 0; j < kMoeMaxTopk; ++j) {
-      if (j < K) {
-        const float w = keep_f32(pk[j] / ps);
-        const int e = min(max(li[j], 0), E - 1);
-        mb.topi[K * t + j] = e;
-        mb.topw[K * t + j] = out_bf16 ? f32_to_bf16_bits(w) : f32_to_f16_bits(w);
-        mb.slot_of[K * t + j] = atomicAdd(&cnt[e], 1);
-      }
-    }
-  }
+  for (int i = threadIdx.x; i < S; i += blockDim.x) mb.slot_of[i] = atomicAdd(&cnt[mb.topi[i]], 1);
   __syncthreads();
   if (threadIdx.x == 0) {
     int o = 0, tb = 0;
@@ -189,8 +213,7 @@ __global__ __launch_bounds__(1024) void moe_route_topk_kernel(const void* __rest
     tbase[E] = tb;
   }
   __syncthreads();
-  for (int i = threadIdx.x; i < K * T; i += blockDim.x)
-    mb.perm[off[mb.topi[i]] + mb.slot_of[i]] = i;
+  for (int i = threadIdx.x; i < S; i += blockDim.x) mb.perm[off[mb.topi[i]] + mb.slot_of[i]] = i;
   for (int e = threadIdx.x; e < E; e += blockDim.x) {
     for (int j = 0; j < tbase[e + 1] - tbase[e]; ++j) {
       int* tl = &mb.tiles[3 * (tbase[e] + j)];
@@ -628,14 +651,16 @@ void launch_route(const void* logits, int logits_dtype, int T, int E, bool bf16,
 
 void launch_route_topk(const void* logits, int logits_dtype, int T, int E, bool bf16,
                        const MoeBuffers& mb, const MoeLayout& L, hipStream_t st) {
-  const dim3 g(1), b(1024);
+  const dim3 g((T + kTopkWaves - 1) / kTopkWaves), b(kTopkWaves * 64);
   const int K = L.topk;
   if (logits_dtype == 0)
-    hipLaunchKernelGGL(moe_route_topk_kernel<0>, g, b, 0, st, logits, T, E, K, (int)bf16, mb, L.max_tiles, L.bm);
+    hipLaunchKernelGGL(moe_topk_select_kernel<0>, g, b, 0, st, logits, T, E, K, (int)bf16, mb);
   else if (logits_dtype == 1)
-    hipLaunchKernelGGL(moe_route_topk_kernel<1>, g, b, 0, st, logits, T, E, K, (int)bf16, mb, L.max_tiles, L.bm);
+    hipLaunchKernelGGL(moe_topk_select_kernel<1>, g, b, 0, st, logits, T, E, K, (int)bf16, mb);
   else
-    hipLaunchKernelGGL(moe_route_topk_kernel<2>, g, b, 0, st, logits, T, E, K, (int)bf16, mb, L.max_tiles, L.bm);
+    hipLaunchKernelGGL(moe_topk_select_kernel<2>, g, b, 0, st, logits, T, E, K, (int)bf16, mb);
+  hipLaunchKernelGGL(moe_route_build_kernel, dim3(1), dim3(1024), 0, st, T, E, K, mb, L.max_tiles,
+                     L.bm);
 }
 
 template <bool BF16, class BP, bool GATHER, bool GATED, bool OUT_PERM>
