@@ -77,10 +77,6 @@ __device__ inline kbh_u32x2 byte4_dequant(uint32_t v, uint16_t s) {
   }
 }
 
-__device__ inline uint16_t half_of(kbh_u32x4 v, int i) {
-  return (uint16_t)((i & 1) ? (v[i >> 1] >> 16) : (v[i >> 1] & 0xffffu));
-}
-
 template <int SPW, bool BF16, int DEC, int MB>
 __global__ __launch_bounds__(kSplitKMaxWaves * 64) void byte_decode_kernel(
     const uint16_t* __restrict__ x, const uint8_t* __restrict__ w,

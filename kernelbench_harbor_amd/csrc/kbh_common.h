@@ -82,6 +82,11 @@ __device__ inline float half_bits_to_f32(uint16_t h) {
   if constexpr (BF16) return bf16_bits_to_f32(h); else return f16_bits_to_f32(h);
 }
 
+// 16-bit element i (0..7) of a 16-byte vector.
+__device__ inline uint16_t half_of(kbh_u32x4 v, int i) {
+  return (uint16_t)((i & 1) ? (v[i >> 1] >> 16) : (v[i >> 1] & 0xffffu));
+}
+
 // Materialises v as an fp32 register value. Used where the reference rounds an intermediate to
 // fp32 before a narrower conversion: without it the compiler may fuse a multiply with the
 // conversion (v_fma_mix*), which rounds once and can differ from the reference in a tie.
