@@ -9,11 +9,12 @@
 // with W4A16 g128 gate/up/down weights (packed along their output dimension).
 //
 // Kernels:
-//  * moe_route_kernel (one workgroup): softmax + top-2 per token, per-expert counts (LDS
-//    atomics), prefix sums, the slot permutation perm[slot] = 2t + k (slots grouped by expert)
-//    and a tile table of (expert, first slot, rows) with BM rows per tile; unused table entries
-//    get rows = 0. Only the routed (token, expert) pairs are computed downstream — the reference
-//    computes all experts densely (reference.py:19).
+//  * moe_topk_select_kernel + moe_route_build_kernel (with k = 2): softmax + top-2 per token
+//    (one wave per token), then per-expert counts (LDS atomics), prefix sums, the slot
+//    permutation perm[slot] = 2t + k (slots grouped by expert) and a tile table of (expert,
+//    first slot, rows) with BM rows per tile; unused table entries get rows = 0. Only the
+//    routed (token, expert) pairs are computed downstream — the reference computes all experts
+//    densely (reference.py:19).
 //  * moe_gemm_kernel: expert-grouped GEMM. A workgroup takes one tile of one expert and 128
 //    output columns; x rows are gathered through perm, the expert's weights come from a slab
 //    policy (int8-stored int4 or packed int4, dequantized exactly into LDS), the K loop is the
@@ -47,71 +48,6 @@ struct MoeBuffers {
   int* tiles;       // [max_tiles][3] = expert, first slot, rows
 };
 
-template <int LDT>
-__global__ __launch_bounds__(1024) void moe_route_kernel(const void* __restrict__ logits, int T,
-                                                         int E, int out_bf16, MoeBuffers mb,
-                                                         int max_tiles, int bm) {
-  __shared__ int cnt[kMoeMaxExperts];
-  __shared__ int off[kMoeMaxExperts];
-  __shared__ int tbase[kMoeMaxExperts + 1];
-  for (int e = threadIdx.x; e < E; e += blockDim.x) cnt[e] = 0;
-  __syncthreads();
-  for (int t = threadIdx.x; t < T; t += blockDim.x) {
-    const size_t row = (size_t)t * E;
-    float mx = -INFINITY;
-    int i0 = 0;
-    for (int e = 0; e < E; ++e) {
-      const float v = logit_at<LDT>(logits, row + e);
-      if (v > mx) { mx = v; i0 = e; }  // first index among equal maxima
-    }
-    float sum = 0.f, m1 = -INFINITY;
-    int i1 = (i0 == 0) ? 1 : 0;
-    for (int e = 0; e < E; ++e) {
-      const float v = logit_at<LDT>(logits, row + e);
-      sum += expf(v - mx);
-      if (e != i0 && v > m1) { m1 = v; i1 = e; }
-    }
-    // softmax probabilities of the two picks, renormalised (reference.py:14-16)
-    const float p0 = keep_f32(expf(logit_at<LDT>(logits, row + i0) - mx) / sum);
-    const float p1 = keep_f32(expf(logit_at<LDT>(logits, row + i1) - mx) / sum);
-    const float s = keep_f32(p0 + p1);
-    const float w0 = keep_f32(p0 / s), w1 = keep_f32(p1 / s);
-    mb.topi[2 * t] = i0;
-    mb.topi[2 * t + 1] = i1;
-    mb.topw[2 * t] = out_bf16 ? f32_to_bf16_bits(w0) : f32_to_f16_bits(w0);
-    mb.topw[2 * t + 1] = out_bf16 ? f32_to_bf16_bits(w1) : f32_to_f16_bits(w1);
-    mb.slot_of[2 * t] = atomicAdd(&cnt[i0], 1);
-    mb.slot_of[2 * t + 1] = atomicAdd(&cnt[i1], 1);
-  }
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    int o = 0, tb = 0;
-    for (int e = 0; e < E; ++e) {
-      off[e] = o;
-      tbase[e] = tb;
-      o += cnt[e];
-      tb += (cnt[e] + bm - 1) / bm;
-    }
-    tbase[E] = tb;
-  }
-  __syncthreads();
-  for (int i = threadIdx.x; i < 2 * T; i += blockDim.x)
-    mb.perm[off[mb.topi[i]] + mb.slot_of[i]] = i;
-  for (int e = threadIdx.x; e < E; e += blockDim.x) {
-    for (int j = 0; j < tbase[e + 1] - tbase[e]; ++j) {
-      int* tl = &mb.tiles[3 * (tbase[e] + j)];
-      tl[0] = e;
-      tl[1] = off[e] + j * bm;
-      tl[2] = min(bm, cnt[e] - j * bm);
-    }
-  }
-  for (int i = tbase[E] + threadIdx.x; i < max_tiles; i += blockDim.x) {
-    mb.tiles[3 * i] = 0;
-    mb.tiles[3 * i + 1] = 0;
-    mb.tiles[3 * i + 2] = 0;
-  }
-}
-
 // Top-k routing (k <= kMoeMaxTopk, E <= kMoeMaxExperts) for the fp16/bf16-weight MoE
 // (tasks/moe/<task>/environment/reference.py:11-13), in two kernels:
 //  * moe_topk_select_kernel: one wave per token, lanes across experts (up to 4 each). The
@@ -120,7 +56,7 @@ __global__ __launch_bounds__(1024) void moe_route_kernel(const void* __restrict_
 //    excluded from the later rounds. NaN logits rank as -inf (every id is a distinct expert in
 //    range). Weights p_j / sum_j p_j (summed in k order) rounded to the activation dtype.
 //  * moe_route_build_kernel (one workgroup): per-expert slot counts (LDS atomics), offsets,
-//    the permutation perm[slot] = k t + j and the tile table, as moe_route_kernel.
+//    the permutation perm[slot] = k t + j and the tile table (unused entries: rows = 0).
 constexpr int kMoeMaxTopk = 8;
 constexpr int kTopkWaves = 4;  // tokens per workgroup of the select kernel
 
@@ -638,17 +574,6 @@ MoeBuffers moe_buffers(void* ws, const MoeLayout& L) {
                     (int*)(b + L.perm), (int*)(b + L.tiles)};
 }
 
-void launch_route(const void* logits, int logits_dtype, int T, int E, bool bf16, const MoeBuffers& mb,
-                  const MoeLayout& L, hipStream_t st) {
-  const dim3 g(1), b(1024);
-  if (logits_dtype == 0)
-    hipLaunchKernelGGL(moe_route_kernel<0>, g, b, 0, st, logits, T, E, (int)bf16, mb, L.max_tiles, L.bm);
-  else if (logits_dtype == 1)
-    hipLaunchKernelGGL(moe_route_kernel<1>, g, b, 0, st, logits, T, E, (int)bf16, mb, L.max_tiles, L.bm);
-  else
-    hipLaunchKernelGGL(moe_route_kernel<2>, g, b, 0, st, logits, T, E, (int)bf16, mb, L.max_tiles, L.bm);
-}
-
 void launch_route_topk(const void* logits, int logits_dtype, int T, int E, bool bf16,
                        const MoeBuffers& mb, const MoeLayout& L, hipStream_t st) {
   const dim3 g((T + kTopkWaves - 1) / kTopkWaves), b(kTopkWaves * 64);
@@ -790,7 +715,7 @@ extern "C" int kbh_moe_route_top2(const void* router_logits, int logits_dtype, i
   MoeBuffers mb = moe_buffers(workspace, L);
   mb.topi = topi;
   mb.topw = (uint16_t*)topw;
-  launch_route(router_logits, logits_dtype, T, E, dtype == KBH_BF16, mb, L, (hipStream_t)stream);
+  launch_route_topk(router_logits, logits_dtype, T, E, dtype == KBH_BF16, mb, L, (hipStream_t)stream);
   return launch_status();
 }
 
@@ -810,7 +735,7 @@ extern "C" int kbh_qmoe(const void* x, const int8_t* qweight, const void* scales
   hipStream_t st = (hipStream_t)stream;
   void* o = (char*)workspace + L.o;
   const bool bf = dtype == KBH_BF16;
-  launch_route(router_logits, logits_dtype, T, E, bf, mb, L, st);
+  launch_route_topk(router_logits, logits_dtype, T, E, bf, mb, L, st);
   const size_t ws_ = (size_t)D * N, ss_ = (size_t)(D / group) * N;
   if (bf) {
     const I8SlabPolicy<true> bp{qweight, (const uint16_t*)scales, N, group, ws_, ss_};
@@ -866,7 +791,7 @@ extern "C" int kbh_qmoe_ffn(const void* x, const void* router_logits, int logits
   void* h = (char*)workspace + L.h;
   void* o = (char*)workspace + L.o;
   const bool bf = dtype == KBH_BF16;
-  launch_route(router_logits, logits_dtype, T, E, bf, mb, L, st);
+  launch_route_topk(router_logits, logits_dtype, T, E, bf, mb, L, st);
   // gate/up: [D -> F] packed along F; down: [F -> D] packed along D
   const size_t gq = (size_t)D * (F / 8), gs = (size_t)(D / group) * F;
   const size_t dq = (size_t)F * (D / 8), ds = (size_t)(F / group) * D;
