@@ -218,9 +218,13 @@ bool plan_byte_decode(int M, int N, int K, BytePlan* p) {
   return p->waves > 0;
 }
 
+// Runs the GEMM; with `defer_sum` and a split K the slices are left in the workspace
+// (acc[splits][M][N] fp32) for the caller to sum, and *splits_out tells how many (1: y written).
 template <bool BF16, int DEC>
 int byte_gemm_run(const void* x, const void* w, const void* scales, void* y, void* workspace,
-                  size_t workspace_bytes, int M, int N, int K, int block, hipStream_t st) {
+                  size_t workspace_bytes, int M, int N, int K, int block, hipStream_t st,
+                  bool defer_sum = false, int* splits_out = nullptr) {
+  if (splits_out) *splits_out = 1;
   if (M >= kByteTiledMinM && K % (TBK * TDEPTH) == 0) {
     const ByteSlabPolicy<BF16, DEC> bp{(const uint8_t*)w, (const uint16_t*)scales, N, block};
     hipLaunchKernelGGL((tiled_f16_gemm<BF16, ByteSlabPolicy<BF16, DEC>>), tiled_f16_grid(M, N),
@@ -244,7 +248,8 @@ int byte_gemm_run(const void* x, const void* w, const void* scales, void* y, voi
   else KBH_BYTE_DEC(4, 2) else KBH_BYTE_DEC(2, 2) else KBH_BYTE_DEC(1, 2)
   else KBH_BYTE_DEC(2, 4) else KBH_BYTE_DEC(1, 4)
 #undef KBH_BYTE_DEC
-  if (splits > 1)
+  if (splits_out) *splits_out = splits;
+  if (splits > 1 && !defer_sum)
     launch_splitk_sum(reinterpret_cast<const kbh_f32x4*>(acc), HalfOut<BF16>{(uint16_t*)y, N}, M, N,
                       pl.ntiles, 128, splits, st);
   return launch_status();

@@ -7,12 +7,13 @@
 //   base = dtype(x @ W)                                              [T, N]      (:13)
 //   lo   = dtype(x[t] @ A[id_t])                                     [T, r]      (:14-15)
 //   y    = dtype(base + dtype(lo[t] @ B[id_t]))                      [T, N]      (:16-17)
-// Three launches (plus the split-K slice sum of the base GEMM): the base GEMM is the byte-weight
-// GEMM of byte_weight_gemm.h with the int8 decoder, writing base into y; lora_shrink_kernel
-// computes fp32 partial sums of x[t] @ A[id] over DS ranges of D (T x DS workgroups, so that a
-// few tokens still fill the chip); lora_expand_add_kernel sums the DS partials in order, rounds
-// lo to dtype and adds dtype(lo @ B) to y in place (four columns per thread). Adapter ids
-// outside [0, L) are clamped (torch would raise).
+// Three launches: the base GEMM is the byte-weight GEMM of byte_weight_gemm.h with the int8
+// decoder (its split-K slices left in the workspace, or base written into y when K is not
+// split); lora_shrink_kernel computes fp32 partial sums of x[t] @ A[id] over DS ranges of D
+// (T x DS workgroups, so that a few tokens still fill the chip); lora_expand_add_kernel sums
+// the DS partials in order and rounds lo to dtype, sums the GEMM's slices in split order (or
+// reads base from y) and rounds base, and writes dtype(base + dtype(lo @ B)) (four columns per
+// thread). Adapter ids outside [0, L) are clamped (torch would raise).
 #include "byte_weight_gemm.h"
 
 namespace kbh {
@@ -83,11 +84,13 @@ __global__ __launch_bounds__(kLoraThreads) void lora_shrink_kernel(
 }
 
 // lo[t][j] = dtype(sum over ds in order of part[ds][t][j]);
-// y[t][n] = dtype(fp32(y[t][n]) + fp32(dtype(sum_j lo[t][j] B[id][j][n]))), y holding base.
+// base[t][n] = dtype(sum over s in order of slices[s][t][n]) (splits > 1), else y[t][n];
+// y[t][n] = dtype(fp32(base) + fp32(dtype(sum_j lo[t][j] B[id][j][n]))).
 template <bool BF16>
 __global__ __launch_bounds__(kLoraThreads) void lora_expand_add_kernel(
     const float* __restrict__ part, const uint16_t* __restrict__ B, const int64_t* __restrict__ ids,
-    uint16_t* __restrict__ y, int T, int N, int r, int L, int ds) {
+    const float* __restrict__ slices, int splits, uint16_t* __restrict__ y, int T, int N, int r,
+    int L, int ds) {
   __shared__ float los[kLoraMaxRank];
   const int t = blockIdx.y;
   const int l = lora_id(ids, t, L);
@@ -106,6 +109,19 @@ __global__ __launch_bounds__(kLoraThreads) void lora_expand_add_kernel(
   const int n = (blockIdx.x * kLoraThreads + threadIdx.x) * 4;
   if (n >= N) return;
   const uint16_t* Bl = B + (size_t)l * r * N + n;
+  uint16_t* yr = y + (size_t)t * N + n;
+  float bs[4];
+  if (splits > 1) {  // the base GEMM's split-K slices, added in split order
+    const size_t stride = (size_t)T * N;
+    const kbh_f32x4 v = sum_slices(reinterpret_cast<const kbh_f32x4*>(slices + (size_t)t * N + n),
+                                   stride / 4, splits);
+#pragma unroll
+    for (int c = 0; c < 4; ++c) bs[c] = half_bits_to_f32<BF16>(f32_to_half_bits<BF16>(v[c]));
+  } else {
+    const kbh_u32x2 base = *reinterpret_cast<const kbh_u32x2*>(yr);
+#pragma unroll
+    for (int c = 0; c < 4; ++c) bs[c] = half_bits_to_f32<BF16>((uint16_t)(base[c >> 1] >> (16 * (c & 1))));
+  }
   float acc[4] = {0.f, 0.f, 0.f, 0.f};
   for (int j = 0; j < r; j += 4) {  // r % 4 == 0: four rows of B in flight
     kbh_u32x2 b[4];
@@ -117,8 +133,6 @@ __global__ __launch_bounds__(kLoraThreads) void lora_expand_add_kernel(
       for (int c = 0; c < 4; ++c)
         acc[c] += los[j + u] * half_bits_to_f32<BF16>((uint16_t)(b[u][c >> 1] >> (16 * (c & 1))));
   }
-  uint16_t* yr = y + (size_t)t * N + n;
-  const kbh_u32x2 base = *reinterpret_cast<const kbh_u32x2*>(yr);
   kbh_u32x2 out;
 #pragma unroll
   for (int h = 0; h < 2; ++h) {
@@ -126,7 +140,7 @@ __global__ __launch_bounds__(kLoraThreads) void lora_expand_add_kernel(
 #pragma unroll
     for (int c = 0; c < 2; ++c) {
       const float e = half_bits_to_f32<BF16>(f32_to_half_bits<BF16>(acc[2 * h + c]));
-      v[c] = keep_f32(half_bits_to_f32<BF16>((uint16_t)(base[h] >> (16 * c))) + e);
+      v[c] = keep_f32(bs[2 * h + c] + e);
     }
     out[h] = (uint32_t)f32_to_half_bits<BF16>(v[0]) | ((uint32_t)f32_to_half_bits<BF16>(v[1]) << 16);
   }
@@ -157,13 +171,16 @@ int lora_run(const void* x, const int8_t* qweight, const void* scales, const voi
              int N, int r, int L, int group, hipStream_t st) {
   const LoraLayout lay = lora_layout(T, D, N, r);
   float* part = (float*)((char*)ws + lay.part);
-  const int s = byte_gemm_run<BF16, kDecInt8>(x, qweight, scales, y, ws, lay.part, T, N, D, group, st);
+  int splits = 1;
+  const int s = byte_gemm_run<BF16, kDecInt8>(x, qweight, scales, y, ws, lay.part, T, N, D, group,
+                                              st, true, &splits);
   if (s != KBH_OK) return s;
   hipLaunchKernelGGL(lora_shrink_kernel<BF16>, dim3(T, lay.ds), dim3(kLoraThreads), 0, st,
                      (const uint16_t*)x, (const uint16_t*)A, ids, part, T, D, r, L, lay.dchunk);
   const dim3 grid((N / 4 + kLoraThreads - 1) / kLoraThreads, T);
   hipLaunchKernelGGL(lora_expand_add_kernel<BF16>, grid, dim3(kLoraThreads), 0, st,
-                     (const float*)part, (const uint16_t*)B, ids, (uint16_t*)y, T, N, r, L, lay.ds);
+                     (const float*)part, (const uint16_t*)B, ids, (const float*)ws, splits,
+                     (uint16_t*)y, T, N, r, L, lay.ds);
   return launch_status();
 }
 
