@@ -191,7 +191,7 @@ struct ByteSlabPolicy {
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const uint16_t s = (uint16_t)((j & 1) ? (r.s[j >> 1] >> 16) : (r.s[j >> 1] & 0xffffu));
-      *reinterpret_cast<kbh_u32x2*>(&Bs[(4 * cq + j) * TLD + 4 * rq]) = byte4_dequant<BF16, DEC>(cols[j], s);
+      *reinterpret_cast<kbh_u32x2*>(&Bs[tld_row(4 * cq + j) * TLD + 4 * rq]) = byte4_dequant<BF16, DEC>(cols[j], s);
     }
   }
 };

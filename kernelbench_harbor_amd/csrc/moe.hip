@@ -167,7 +167,7 @@ __global__ __launch_bounds__(1024) void moe_route_build_kernel(int T, int E, int
 
 // Slab producer for fp16/bf16 weights [E][K][N] (N contiguous), used as they are: each thread
 // loads 4 rows x 4 columns (8 bytes per row; a row of the 128-column slab is 256 contiguous
-// bytes across 32 threads) and writes the 4x4 block transposed, Bs[n * TLD + k], as four 8-byte
+// bytes across 32 threads) and writes the 4x4 block transposed, Bs[tld_row(n) * TLD + k], as four 8-byte
 // LDS stores (two v_perm_b32 per column).
 struct F16SlabPolicy {
   const uint16_t* w;
@@ -196,7 +196,7 @@ struct F16SlabPolicy {
       kbh_u32x2 out;
       out[0] = __builtin_amdgcn_perm(r.r[1][j >> 1], r.r[0][j >> 1], sel);
       out[1] = __builtin_amdgcn_perm(r.r[3][j >> 1], r.r[2][j >> 1], sel);
-      *reinterpret_cast<kbh_u32x2*>(&Bs[(4 * cq + j) * TLD + 4 * rq]) = out;
+      *reinterpret_cast<kbh_u32x2*>(&Bs[tld_row(4 * cq + j) * TLD + 4 * rq]) = out;
     }
   }
 };
@@ -265,7 +265,7 @@ struct I8SlabPolicy {
           out[h] = __builtin_bit_cast(uint32_t, q * h2{sc, sc});
         }
       }
-      *reinterpret_cast<kbh_u32x2*>(&Bs[(4 * cq + j) * TLD + 4 * rq]) = out;
+      *reinterpret_cast<kbh_u32x2*>(&Bs[tld_row(4 * cq + j) * TLD + 4 * rq]) = out;
     }
   }
 };
@@ -348,7 +348,7 @@ __global__ __launch_bounds__(256) void moe_gemm_kernel(const uint16_t* __restric
 #pragma unroll
         for (int j = 0; j < WNT; ++j) {
           const kbh_u32x4 b = *reinterpret_cast<const kbh_u32x4*>(
-              &Bs[q][buf][(wn * 32 * WNT + j * 32 + fr) * TLD + fk + kk * 16]);
+              &Bs[q][buf][tld_row(wn * 32 * WNT + j * 32 + fr) * TLD + fk + kk * 16]);
 #pragma unroll
           for (int i = 0; i < 2; ++i) accv[q][i][j] = mfma32x32x16<BF16>(a[i], b, accv[q][i][j]);
         }

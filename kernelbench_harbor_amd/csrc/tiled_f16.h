@@ -9,7 +9,8 @@
 //  * Two LDS buffers. Per slab: the MFMAs of slab kt run while the wave copies x and the
 //    policy's dequantized weights of slab kt+1 into the other buffer; one barrier per slab.
 //  * LDS rows are 40 elements (80 bytes): 16-byte fragment reads of 32 consecutive rows hit
-//    distinct banks. The weight slab is stored k-major per output column ([128][40]).
+//    distinct banks. The weight slab is stored k-major per output column ([128][40]), column n
+//    at row tld_row(n).
 //  * 2x2 waves, each 128x64 with 32x32x16 MFMAs (4x2 accumulator tiles).
 //  * Workgroup ids are remapped so that each XCD receives consecutive tiles of the same rows of
 //    x (its L2 then serves the shared x slabs).
@@ -17,7 +18,7 @@
 // Policy interface (BP):
 //   struct Regs;                                          per-thread raw data of one slab
 //   void load(Regs&, int k0, int n0, int t) const;        issue global loads of slab [k0, k0+32)
-//   void store(const Regs&, uint16_t* Bs, int t) const;   write Bs[n * TLD + k] for the slab
+//   void store(const Regs&, uint16_t* Bs, int t) const;   write Bs[tld_row(n) * TLD + k] for the slab
 #pragma once
 
 #include "kbh_common.h"
@@ -27,6 +28,17 @@ namespace kbh {
 constexpr int TBM = 256, TBN = 128, TBK = 32;
 constexpr int TLD = TBK + 8;  // LDS row stride in 16-bit elements
 constexpr int TDEPTH = 4;     // K slabs in flight in registers ahead of the MFMAs
+
+// LDS row of output column n in a [column][TLD] weight slab. The low three bits of n are permuted
+// within each 8-column block, l -> l ^ (((n >> 2) & 6) | (l >> 2)) (a bijection of 0..7 for every
+// block): the producers' 8-byte stores of columns 4c + j (c = 0..7, one j) then land in 8
+// distinct 16-byte bank groups instead of 2 (an 80-byte row stride puts columns 8 apart on the
+// same banks), while 8 consecutive columns, one fragment read, stay in distinct bank groups.
+// Bits 3 and up are kept, so tld_row(n + 32 i) = tld_row(n) + 32 i.
+__device__ inline int tld_row(int n) {
+  const int l = n & 7;
+  return (n & ~7) | (l ^ (((n >> 2) & 6) | (l >> 2)));
+}
 
 template <bool BF16, class BP>
 __global__ __launch_bounds__(256) void tiled_f16_gemm(const uint16_t* __restrict__ x, BP bp,
@@ -80,7 +92,7 @@ __global__ __launch_bounds__(256) void tiled_f16_gemm(const uint16_t* __restrict
   // One 16-deep K step of the wave's 128x64 tile: 6 LDS fragment reads, 8 MFMAs.
   auto mma_k16 = [&](int buf, int kk) {
     const uint16_t* Ab = &As[buf][(wm * 128 + fr) * TLD + fk + kk * 16];
-    const uint16_t* Bb = &Bs[buf][(wn * 64 + fr) * TLD + fk + kk * 16];
+    const uint16_t* Bb = &Bs[buf][tld_row(wn * 64 + fr) * TLD + fk + kk * 16];
     kbh_u32x4 a[4], b[2];
 #pragma unroll
     for (int i = 0; i < 4; ++i) a[i] = *reinterpret_cast<const kbh_u32x4*>(Ab + i * 32 * TLD);

@@ -103,7 +103,7 @@ struct W4SlabPolicy {
     uint32_t dq[8];
     dequant_2x8<BF16>(r.b[0], r.b[1], r.s, r.z, dq);
 #pragma unroll
-    for (int c = 0; c < 8; ++c) *reinterpret_cast<uint32_t*>(&Bs[(wc * 8 + c) * TLD + 2 * kp]) = dq[c];
+    for (int c = 0; c < 8; ++c) *reinterpret_cast<uint32_t*>(&Bs[tld_row(wc * 8 + c) * TLD + 2 * kp]) = dq[c];
   }
 };
 
