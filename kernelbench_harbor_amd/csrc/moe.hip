@@ -542,13 +542,13 @@ struct MoeLayout {
 };
 
 // Slots: topk per token (slot order grouped by expert). bm: rows per tile-table entry (0: 128
-// when an expert averages more than 96 rows, else 64).
+// when an expert averages more than 48 rows, else 64).
 MoeLayout moe_layout(int T, int E, int hidden, int out_cols, int bm = 0, size_t part_bytes = 0,
                      int topk = 2) {
   MoeLayout L;
   const size_t S = (size_t)topk * T;
   L.topk = topk;
-  L.bm = bm ? bm : ((int)S / (E > 0 ? E : 1) > 96 ? 128 : 64);
+  L.bm = bm ? bm : ((int)S / (E > 0 ? E : 1) > 48 ? 128 : 64);
   L.max_tiles = (int)((S + L.bm - 1) / L.bm) + E;
   size_t o = 0;
   auto take = [&](size_t bytes) {
