@@ -21,8 +21,8 @@ def _f(t):
     return t.float().numpy()
 
 
-@pytest.mark.parametrize("E,k", [(8, 2), (64, 6), (128, 8), (8, 8), (60, 1)])
-@pytest.mark.parametrize("ldt", [torch.float16, torch.float32])
+@pytest.mark.parametrize("E,k", [(8, 2), (64, 6), (128, 8), (8, 8), (60, 1), (256, 8), (200, 3)])
+@pytest.mark.parametrize("ldt", [torch.float16, torch.bfloat16, torch.float32])
 def test_route_topk(dev, E, k, ldt):
     g = torch.Generator().manual_seed(E + k)
     lg = inputs._topk_distinct_logits(333, E, k, g, ldt)
@@ -39,7 +39,9 @@ CASES = [
     (100, 256, 128, 128, 8, torch.bfloat16),
     (300, 512, 8, 256, 2, torch.bfloat16),
     (1, 128, 4, 128, 1, torch.float16),
-    (250, 384, 16, 640, 8, torch.float16),   # > 96 rows per expert: 128-row tiles
+    (250, 384, 16, 640, 8, torch.float16),   # > 48 rows per expert: 128-row tiles
+    (5, 128, 256, 128, 8, torch.float16),    # the largest expert count
+    (1, 256, 64, 256, 8, torch.bfloat16),    # one token, eight experts
 ]
 
 
