@@ -72,6 +72,9 @@ FFN_CASES = [
     (64, 256, 512, 4, torch.float16),
     (128, 512, 1024, 8, torch.float16),
     (96, 512, 384, 8, torch.bfloat16),
+    # 64..191 rows per expert: 128-row tiles, experts above 128 rows on one 256-row tile
+    (300, 256, 512, 4, torch.float16),
+    (160, 512, 256, 4, torch.bfloat16),      # all experts at most 128 rows: big table empty
     # >= 192 routed rows per expert on average: 256-row expert tiles
     (400, 256, 256, 4, torch.float16),
     (512, 512, 512, 4, torch.bfloat16),
