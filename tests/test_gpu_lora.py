@@ -63,3 +63,13 @@ def test_one_hot_matches_native_rounding(dev, dtype):
     y = ops.lora_qgemm(*[t.to(dev) for t in (x, q, s, A, B, ids)]).float().cpu().numpy()
     want = ol.forward(*_np([x, q, s, A, B, ids]), dtype="f16" if dtype == torch.float16 else "bf16")
     assert np.array_equal(y, want), np.abs(y - want).max()
+
+
+def test_out_of_range_ids_are_clamped(dev):
+    """Adapter ids outside [0, L) select the nearest adapter (documented; torch would raise)."""
+    T, D, N, r, L = 8, 256, 128, 8, 3
+    x, q, s, A, B, ids = inputs.lora_qgemm(T, D, N, r, L, torch.float16, seed=3)
+    bad = torch.tensor([-5, 0, 1, 2, 3, 7, -1, 2])
+    y = ops.lora_qgemm(*[t.to(dev) for t in (x, q, s, A, B, bad)])
+    want = ol.forward(*_np([x, q, s, A, B, bad.clamp(0, L - 1)]))
+    assert compare(y, want).ok
