@@ -23,6 +23,8 @@
 //    (gate and up) and applies silu(g) * u before rounding.
 //  * moe_combine_kernel: y[t] = dtype(o[2t] w[2t] + o[2t+1] w[2t+1]) with the reference's
 //    roundings (each product rounded to dtype, fp32 sum of the two, one rounding).
+#include <type_traits>
+
 #include "kbh_common.h"
 #include "tiled_f16.h"
 #include "tiled_wide.h"
@@ -165,11 +167,14 @@ __global__ __launch_bounds__(1024) void moe_route_build_kernel(int T, int E, int
   }
 }
 
-// Slab producer for fp16/bf16 weights [E][K][N] (N contiguous), used as they are: each thread
-// loads 4 rows x 4 columns (8 bytes per row; a row of the 128-column slab is 256 contiguous
-// bytes across 32 threads) and writes the 4x4 block transposed, Bs[tld_row(n) * TLD + k], as four 8-byte
-// LDS stores (two v_perm_b32 per column).
+// Slab producer for fp16/bf16 weights [E][K][N] (N contiguous), used as they are and stored
+// as they lie in memory: LDS rows of kBnPitch halves per k (128 columns + 32 of padding), each
+// thread copying 16 bytes of rows t / 16 and t / 16 + 16. The GEMM reads its B fragments with
+// the transposing LDS read (kNMajor; see moe_gemm_kernel), so no transpose happens here.
+constexpr int kBnPitch = 160;  // 320-byte rows: the 4 rows x 64 bytes of one 32-lane read fill
+                               // 64 distinct banks
 struct F16SlabPolicy {
+  static constexpr bool kNMajor = true;
   const uint16_t* w;
   int N;
   size_t w_stride;
@@ -179,27 +184,41 @@ struct F16SlabPolicy {
     return p;
   }
   struct Regs {
-    kbh_u32x2 r[4];
+    kbh_u32x4 r[2];
   };
   __device__ void load(Regs& r, int k0, int n0, int t) const {
-    const int cq = t & 31, rq = t >> 5;
-    const uint16_t* p = w + (size_t)(k0 + 4 * rq) * N + n0 + 4 * cq;
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-      r.r[i] = __builtin_nontemporal_load(reinterpret_cast<const kbh_u32x2*>(p + (size_t)i * N));
+    const int c = t & 15, k = t >> 4;
+    const uint16_t* p = w + (size_t)(k0 + k) * N + n0 + 8 * c;
+    r.r[0] = __builtin_nontemporal_load(reinterpret_cast<const kbh_u32x4*>(p));
+    r.r[1] = __builtin_nontemporal_load(reinterpret_cast<const kbh_u32x4*>(p + (size_t)16 * N));
   }
   __device__ void store(const Regs& r, uint16_t* Bs, int t) const {
-    const int cq = t & 31, rq = t >> 5;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const uint32_t sel = (j & 1) ? 0x07060302u : 0x05040100u;  // high or low halves
-      kbh_u32x2 out;
-      out[0] = __builtin_amdgcn_perm(r.r[1][j >> 1], r.r[0][j >> 1], sel);
-      out[1] = __builtin_amdgcn_perm(r.r[3][j >> 1], r.r[2][j >> 1], sel);
-      *reinterpret_cast<kbh_u32x2*>(&Bs[tld_row(4 * cq + j) * TLD + 4 * rq]) = out;
-    }
+    const int c = t & 15, k = t >> 4;
+    *reinterpret_cast<kbh_u32x4*>(&Bs[k * kBnPitch + 8 * c]) = r.r[0];
+    *reinterpret_cast<kbh_u32x4*>(&Bs[(k + 16) * kBnPitch + 8 * c]) = r.r[1];
   }
 };
+static_assert(32 * kBnPitch == 128 * TLD, "an N-major slab uses the buffer of a k-major one");
+
+// Policies without kNMajor store k-major slabs (Bs[tld_row(n) * TLD + k]).
+template <class BP, class = void>
+struct NMajor {
+  static constexpr bool value = false;
+};
+template <class BP>
+struct NMajor<BP, std::void_t<decltype(BP::kNMajor)>> {
+  static constexpr bool value = BP::kNMajor;
+};
+
+typedef short kbh_i16x4 __attribute__((ext_vector_type(4)));
+// ds_read_b64_tr_b16 (measured lane layout): within each 16-lane group, output lane i element j
+// is element i % 4 of the 8 bytes addressed by lane 4j + i / 4. With lane 4j + q addressing row
+// k0 + j, columns n0 + 4q .. +3 of an N-major slab, lane i receives rows k0 .. k0 + 3 of column
+// n0 + i.
+__device__ inline kbh_i16x4 lds_read_tr16(const uint16_t* p) {
+  return __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (__attribute__((address_space(3))) kbh_i16x4*)(const_cast<uint16_t*>(p)));
+}
 
 // Slab producer for int8-stored weights [E][K][N] (N contiguous) with scales [E][K/G][N] in the
 // activation dtype: W = dtype(dtype(q) * s), one rounding (q is exact in either dtype).
@@ -347,8 +366,20 @@ __global__ __launch_bounds__(256) void moe_gemm_kernel(const uint16_t* __restric
       for (int q = 0; q < NB; ++q)
 #pragma unroll
         for (int j = 0; j < WNT; ++j) {
-          const kbh_u32x4 b = *reinterpret_cast<const kbh_u32x4*>(
-              &Bs[q][buf][tld_row(wn * 32 * WNT + j * 32 + fr) * TLD + fk + kk * 16]);
+          kbh_u32x4 b;
+          if constexpr (NMajor<BP>::value) {
+            // 32x32x16 B operand: lane l takes k 8(l / 32) .. +7 of column l % 32; 16-lane group
+            // g = l / 16 covers columns 16(g & 1) .. +15 at k 8(g >> 1), in two 4-row reads.
+            const int g16 = lane >> 4, s16 = lane & 15;
+            const uint16_t* p = &Bs[q][buf][(kk * 16 + 8 * (g16 >> 1) + (s16 >> 2)) * kBnPitch +
+                                            wn * 32 * WNT + j * 32 + 16 * (g16 & 1) + 4 * (s16 & 3)];
+            const kbh_i16x4 lo = lds_read_tr16(p), hi = lds_read_tr16(p + 4 * kBnPitch);
+            b = kbh_u32x4{__builtin_bit_cast(kbh_u32x2, lo)[0], __builtin_bit_cast(kbh_u32x2, lo)[1],
+                          __builtin_bit_cast(kbh_u32x2, hi)[0], __builtin_bit_cast(kbh_u32x2, hi)[1]};
+          } else {
+            b = *reinterpret_cast<const kbh_u32x4*>(
+                &Bs[q][buf][tld_row(wn * 32 * WNT + j * 32 + fr) * TLD + fk + kk * 16]);
+          }
 #pragma unroll
           for (int i = 0; i < 2; ++i) accv[q][i][j] = mfma32x32x16<BF16>(a[i], b, accv[q][i][j]);
         }
