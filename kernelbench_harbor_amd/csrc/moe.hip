@@ -221,15 +221,68 @@ __device__ inline kbh_i16x4 lds_read_tr16(const uint16_t* p) {
 }
 
 // Slab producer for int8-stored weights [E][K][N] (N contiguous) with scales [E][K/G][N] in the
-// activation dtype: W = dtype(dtype(q) * s), one rounding (q is exact in either dtype).
-template <bool BF16>
-struct I8SlabPolicy {
+// activation dtype: W = dtype(dtype(q) * s), one rounding (q is exact in either dtype). Stored
+// N-major like F16SlabPolicy (read with the transposing LDS read): thread t dequantises 16
+// consecutive columns (16 bytes) of row t / 8, so each pair of neighbouring columns meets its
+// pair of scales in one dword, and writes them as two 16-byte stores. fp16 activations only
+// (bf16 uses I8KSlabPolicy).
+struct I8NSlabPolicy {
+  static constexpr bool kNMajor = true;
   const int8_t* w;
   const uint16_t* scales;
   int N, group;
   size_t w_stride, s_stride;
-  __device__ I8SlabPolicy at_expert(int e) const {
-    I8SlabPolicy p = *this;
+  __device__ I8NSlabPolicy at_expert(int e) const {
+    I8NSlabPolicy p = *this;
+    p.w += (size_t)e * w_stride;
+    p.scales += (size_t)e * s_stride;
+    return p;
+  }
+  struct Regs {
+    kbh_u32x4 q;
+    kbh_u32x4 s[2];
+  };
+  __device__ void load(Regs& r, int k0, int n0, int t) const {
+    const int c = t & 7, k = t >> 3;
+    r.q = __builtin_nontemporal_load(
+        reinterpret_cast<const kbh_u32x4*>(w + (size_t)(k0 + k) * N + n0 + 16 * c));
+    const uint16_t* sp = scales + (size_t)(k0 / group) * N + n0 + 16 * c;  // slab within a group
+    r.s[0] = *reinterpret_cast<const kbh_u32x4*>(sp);
+    r.s[1] = *reinterpret_cast<const kbh_u32x4*>(sp + 8);
+  }
+  __device__ void store(const Regs& r, uint16_t* Bs, int t) const {
+    const int c = t & 7, k = t >> 3;
+    kbh_u32x4 out[2];
+#pragma unroll
+    for (int d = 0; d < 4; ++d) {  // dword d of the 16 bytes: columns 4d .. 4d + 3
+      const uint32_t v = r.q[d];
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {  // columns 4d + 2h, 4d + 2h + 1
+        const uint32_t sc = r.s[d >> 1][2 * (d & 1) + h];
+        // fp16 magic: (byte ^ 0x80) | 0x6400 is 1024 + (q + 128); minus 1152 gives q exactly.
+        typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+        const _Float16 bias = (_Float16)1152.0f;
+        const uint32_t P = __builtin_amdgcn_perm(0u, v, h ? 0x0c030c02u : 0x0c010c00u);
+        const h2 q = __builtin_bit_cast(h2, (P ^ 0x00800080u) | 0x64006400u) - h2{bias, bias};
+        out[d >> 1][2 * (d & 1) + h] = __builtin_bit_cast(uint32_t, q * __builtin_bit_cast(h2, sc));
+      }
+    }
+    *reinterpret_cast<kbh_u32x4*>(&Bs[k * kBnPitch + 16 * c]) = out[0];
+    *reinterpret_cast<kbh_u32x4*>(&Bs[k * kBnPitch + 16 * c + 8]) = out[1];
+  }
+};
+
+// k-major variant of the int8 producer (a 4x4 byte transpose in registers, Bs[tld_row(n) * TLD +
+// k]): used for bf16, where the N-major one's 16 columns per thread of fp32 dequantisation cost
+// registers and occupancy (measured 1.15-1.8x slower); same values.
+template <bool BF16>
+struct I8KSlabPolicy {
+  const int8_t* w;
+  const uint16_t* scales;
+  int N, group;
+  size_t w_stride, s_stride;
+  __device__ I8KSlabPolicy at_expert(int e) const {
+    I8KSlabPolicy p = *this;
     p.w += (size_t)e * w_stride;
     p.scales += (size_t)e * s_stride;
     return p;
@@ -769,12 +822,12 @@ extern "C" int kbh_qmoe(const void* x, const int8_t* qweight, const void* scales
   launch_route_topk(router_logits, logits_dtype, T, E, bf, mb, L, st);
   const size_t ws_ = (size_t)D * N, ss_ = (size_t)(D / group) * N;
   if (bf) {
-    const I8SlabPolicy<true> bp{qweight, (const uint16_t*)scales, N, group, ws_, ss_};
-    launch_moe_gemm<true, I8SlabPolicy<true>, true, false, true>(L, x, D, mb, bp, bp, o, N, N, D, st);
+    const I8KSlabPolicy<true> bp{qweight, (const uint16_t*)scales, N, group, ws_, ss_};
+    launch_moe_gemm<true, I8KSlabPolicy<true>, true, false, true>(L, x, D, mb, bp, bp, o, N, N, D, st);
     launch_combine<true>(o, mb.topw, y, T, N, st);
   } else {
-    const I8SlabPolicy<false> bp{qweight, (const uint16_t*)scales, N, group, ws_, ss_};
-    launch_moe_gemm<false, I8SlabPolicy<false>, true, false, true>(L, x, D, mb, bp, bp, o, N, N, D, st);
+    const I8NSlabPolicy bp{qweight, (const uint16_t*)scales, N, group, ws_, ss_};
+    launch_moe_gemm<false, I8NSlabPolicy, true, false, true>(L, x, D, mb, bp, bp, o, N, N, D, st);
     launch_combine<false>(o, mb.topw, y, T, N, st);
   }
   return launch_status();
