@@ -203,7 +203,8 @@ int kbh_moe(const void* x, const void* w, const void* router_logits, int logits_
  * generate_tasks.py:396-420.
  *
  *   x [T, D] dtype; qweight [D, N] int8 (values -8..7); scales [D/group, N] dtype;
- *   A [L, D, r] dtype; B [L, r, N] dtype; lora_ids [T] int64 (clamped to [0, L))
+ *   A [L, D, r] dtype; B [L, r, N] dtype; lora_ids [T] int64 (torch indexing: an id in
+ *   [-L, 0) selects adapter id + L; ids outside [-L, L), where torch raises, are clamped)
  *   y [T, N] dtype = dtype(dtype(x @ dtype(q * s)) + dtype(dtype(x[t] @ A[id]) @ B[id]))
  * Requirements: N % 128 == 0, D % 32 == 0, group in {32, 64, 128, 256} dividing D,
  * r in {4, 8, 16, 32, 64}; x/qweight/scales/y/workspace 16-byte, A/B 8-byte aligned.

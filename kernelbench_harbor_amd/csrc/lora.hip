@@ -13,7 +13,8 @@
 // (T x DS workgroups, so that a few tokens still fill the chip); lora_expand_add_kernel sums
 // the DS partials in order and rounds lo to dtype, sums the GEMM's slices in split order (or
 // reads base from y) and rounds base, and writes dtype(base + dtype(lo @ B)) (four columns per
-// thread). Adapter ids outside [0, L) are clamped (torch would raise).
+// thread). Adapter ids index as torch does (reference.py:14-16, A[lora_ids]): an id in [-L, 0)
+// selects adapter id + L. Ids outside [-L, L), for which torch raises, are clamped to [0, L).
 #include "byte_weight_gemm.h"
 
 namespace kbh {
@@ -24,7 +25,8 @@ constexpr int kLoraThreads = 256;
 constexpr int kLoraMaxSplits = 16;  // D ranges of the shrink
 
 __device__ inline int lora_id(const int64_t* ids, int t, int L) {
-  const int64_t v = ids[t];
+  int64_t v = ids[t];
+  if (v < 0 && v >= -(int64_t)L) v += L;
   return v < 0 ? 0 : (v >= L ? L - 1 : (int)v);
 }
 

@@ -122,13 +122,14 @@ def _distinct_logits(T: int, E: int, g: torch.Generator, dtype: torch.dtype) -> 
 
 
 def qmoe(T: int = 256, D: int = 4096, E: int = 8, N: int = 14336,
-         dtype: torch.dtype = torch.float16, seed: int = 0):
+         dtype: torch.dtype = torch.float16, seed: int = 0, group: int = 128):
     """[x, qweight, scales, router_logits] with the distributions of the reference qMoE task
-    (reference.py:23-29): qweight int8 in [-8, 7], scales N(0,1)*0.01, logits in x.dtype."""
+    (reference.py:23-29): qweight int8 in [-8, 7], scales N(0,1)*0.01 [E, D/group, N] (the
+    reference's GROUP is 128), logits in x.dtype."""
     g = _gen(seed)
     x = torch.randn(T, D, generator=g).to(dtype)
     qweight = torch.randint(-8, 8, (E, D, N), generator=g, dtype=torch.int8)
-    scales = (torch.randn(E, D // 128, N, generator=g) * 0.01).to(dtype)
+    scales = (torch.randn(E, D // group, N, generator=g) * 0.01).to(dtype)
     logits = _distinct_logits(T, E, g, dtype)
     return [x, qweight, scales, logits]
 

@@ -18,10 +18,17 @@ _DT_CODE = {torch.float16: _lib.KBH_F16, torch.bfloat16: _lib.KBH_BF16}
 class _WorkspacePool:
     """Device buffers per (device, stream), grown on demand. The kernels put no requirement on
     their content, so one buffer serves every call ordered on the same stream; the two pools
-    below exist because an op may need a workspace and a scratch buffer that do not overlap."""
+    below exist because an op may need a workspace and a scratch buffer that do not overlap.
+
+    A buffer is never freed: a HIP graph captured while it was current keeps its address, and
+    replays must not write into memory the caching allocator has handed to someone else. When a
+    larger call outgrows the current buffer, it is retired (kept alive for the process) and
+    replaced by one at least twice its size, so the retired buffers together stay below the
+    size of the current one."""
 
     def __init__(self):
         self._bufs: dict[tuple[int, int], torch.Tensor] = {}
+        self._retired: list[torch.Tensor] = []
         self._lock = threading.Lock()
 
     def get(self, nbytes: int, device: torch.device) -> torch.Tensor:
@@ -30,7 +37,11 @@ class _WorkspacePool:
         with self._lock:
             buf = self._bufs.get(key)
             if buf is None or buf.numel() < nbytes:
-                buf = torch.empty(max(nbytes, 256), dtype=torch.uint8, device=device)
+                size = max(nbytes, 256)
+                if buf is not None:
+                    self._retired.append(buf)
+                    size = max(size, 2 * buf.numel())
+                buf = torch.empty(size, dtype=torch.uint8, device=device)
                 self._bufs[key] = buf
             return buf
 

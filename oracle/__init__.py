@@ -23,7 +23,12 @@ modules' op sequences on small seeded inputs; the reference itself ships none):
                 exact power-of-two GEMM KAT.
   qmoe          top-2 closed form w1 = 1/(1+exp(l2-l1)), dense-vs-sparse equivalence on tiny
                 shapes, brute-force loops.
-  qmoe_ffn      brute-force per-token loops on tiny shapes; SiLU closed form.
+  qmoe_ffn      golden vectors from a torch per-token loop (fp32 ground truth and the fused
+                fp16 sequence with h, expert outputs and combine rounded); float64
+                per-token loops written from the definition on tiny shapes (32-row groups);
+                a closed form (one-hot x, up weights dequantising to 1, one down row of 3s)
+                whose output is 3 * silu(gate) combined, bit-exact in fp16, which fails if
+                gate and up trade places; silu against torch.nn.functional.silu.
   silu_fp8      golden vectors (torch CPU ops of the reference sequence); silu(x) = x exactly
                 for x >= 17 (e^-x < 2^-24), so act is exact there; the group's absmax element
                 quantises to +-448; power-of-two scales make act/scale exact, so crafted values

@@ -76,14 +76,25 @@ def qmoe_dense_forward(x, qweight, scales, logits) -> np.ndarray:
 
 
 def silu(v):
+    """SiLU in fp32, v / (1 + e^-v) (torch.nn.functional.silu, generate_tasks.py:337)."""
     v = np.asarray(v, dtype=np.float32)
     return (v / (1.0 + np.exp(-v))).astype(np.float32)
 
 
 def ffn_forward(x, logits, gq, gs, gz, uq, us, uz, dq, ds, dz, dtype: str = F32) -> np.ndarray:
-    """y[t] = sum_k w_k * down_e(silu(gate_e x_t) * up_e x_t) with W4A16 experts. dtype F32 is
-    the ground truth; a 16-bit dtype rounds the dequantized weights, h, each expert output and
-    the combine like the reference's native path."""
+    """y[t] = sum_k w_k * down_e(silu(gate_e x_t) * up_e x_t) with W4A16 experts, e = topi[t, k].
+
+    Routing and combine: reference.py:14-16, 20-21 (fused_qmoe). Expert weights: the W4A16
+    dequantisation of tasks/quant_w4a16_pa/<task>/environment/reference.py:12-17 (oracle/w4a16.py).
+    The gated product: `F.silu(gate.float()) * up.float()` (generate_tasks.py:337). dtype F32 is the
+    ground truth (every floating input upcast, all math in fp32). The FFN has no reference
+    module, so its 16-bit path is the fused one the GPU computes: the dequantised weights are
+    rounded to dtype, gate and up stay fp32 (accumulators) and h = dtype(silu(gate) * up) is
+    rounded once, then each expert output dtype(h @ Wd) and the combine round as
+    qmoe_forward's. (validate/measure_pass1.py:432-437 also rounds each x @ W to dtype before the
+    SiLU; in bf16 those two extra roundings alone exceed the 5e-3 Frobenius gate.) Down weights
+    may be a column slice of D (packed words [:, :, c0/8:c1/8] with the matching scale/zero
+    columns); the result then holds those columns."""
     topi, w = route_top2(logits, dtype)
     xf = round_to(np.asarray(x, dtype=np.float32), dtype)
     T = xf.shape[0]

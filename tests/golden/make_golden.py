@@ -14,6 +14,9 @@ move with the installed torch. The sequences follow:
   SiLU-FP8 tasks/fused_silu_fp8/<task>/environment/reference.py:13-23
   MoE     tasks/moe/<task>/environment/reference.py:10-17 (top-2 and top-6)
   LoRA    tasks/multi_lora_qgemm/<task>/environment/reference.py:10-17
+  SiLU FFN routing and combine of tasks/fused_qmoe/<task>/environment/reference.py:14-21, W4A16
+          experts as reference.py:11-17 of the W4A16 task, `F.silu(gate.float()) * up.float()`
+          (generate_tasks.py:337), h rounded once to the activation dtype
 
 `python tests/golden/make_golden.py [name ...]` rewrites only the named files (default: all);
 each file draws from its own seeded generator, so one can be rewritten without the others.
@@ -171,18 +174,72 @@ def lora(g):
     return out
 
 
+def qmoe_ffn(g):
+    """Top-2 SiLU FFN with W4A16 experts at T=7, D=256, F=128, E=4 (GROUP 128), fp32 router
+    logits: one per-token loop in torch, run once on fp32-upcast inputs (the ground truth) and
+    once in fp16 the way the fused GPU path rounds: dequantised weights in fp16, gate and up
+    accumulated in fp32, h = fp16(silu(gate) * up), each expert output fp16(h @ Wd), the weighted
+    products and their sum in fp16."""
+    import torch.nn.functional as F
+    T, D, Fd, E, G = 7, 256, 128, 4, 128
+    x = torch.randn(T, D, generator=g).half()
+    lg = torch.randn(T, E, generator=g)
+
+    def w4(K, N):
+        nib = torch.randint(0, 16, (E, K, N), generator=g, dtype=torch.int64)
+        packed = torch.zeros(E, K, N // 8, dtype=torch.int64)
+        for i in range(8):
+            packed |= nib[:, :, i::8] << (4 * i)
+        s = (torch.rand(E, K // G, N, generator=g) * 0.018 + 0.002).half()
+        z = torch.randint(0, 16, (E, K // G, N), generator=g).half()
+        return packed.to(torch.int32), s, z
+
+    gq, gs, gz = w4(D, Fd)
+    uq, us, uz = w4(D, Fd)
+    dq, ds, dz = w4(Fd, D)
+    shifts = torch.arange(0, 32, 4, dtype=torch.int32)
+
+    def deq(q, s, z, dt):
+        w = ((q.unsqueeze(-1) >> shifts) & 0xF).reshape(q.shape[0], q.shape[1], -1)
+        return (w.to(dt) - z.repeat_interleave(G, dim=1).to(dt)) * s.repeat_interleave(G, dim=1).to(dt)
+
+    out = {"x": _np(x.float()), "logits": _np(lg), "gq": _np(gq), "gs": _np(gs.float()),
+           "gz": _np(gz.float()), "uq": _np(uq), "us": _np(us.float()), "uz": _np(uz.float()),
+           "dq": _np(dq), "ds": _np(ds.float()), "dz": _np(dz.float())}
+    for tag, dt in (("gt", torch.float32), ("f16", torch.float16)):
+        probs = torch.softmax(lg.float(), dim=-1)
+        topv, topi = probs.topk(2, dim=-1)
+        topv = (topv / topv.sum(dim=-1, keepdim=True)).to(dt)
+        Wg, Wu, Wd = deq(gq, gs, gz, dt), deq(uq, us, uz, dt), deq(dq, ds, dz, dt)
+        xx = x.to(dt)
+        o = torch.zeros(T, 2, D, dtype=dt)
+        for t in range(T):
+            for k in range(2):
+                e = int(topi[t, k])
+                gate = xx[t].float() @ Wg[e].float()
+                up = xx[t].float() @ Wu[e].float()
+                h = (F.silu(gate) * up).to(dt)
+                o[t, k] = (h.float() @ Wd[e].float()).to(dt)
+        y = (o * topv.unsqueeze(-1)).sum(dim=1)
+        out[f"y_{tag}"] = _np(y.float())
+        out["topi"] = _np(topi)
+    return out
+
+
 def e4m3fn_table():
     v = torch.arange(256, dtype=torch.uint8).view(torch.float8_e4m3fn).float()
     return ["nan" if np.isnan(a) else float(a).hex() for a in v.tolist()]
 
 
-SEEDS = {"w4a16": 20240611, "silu_fp8": 20240612, "moe": 20240613, "lora": 20240614}
+SEEDS = {"w4a16": 20240611, "silu_fp8": 20240612, "moe": 20240613, "lora": 20240614,
+         "qmoe_ffn": 20240615}
 SETS = (("w4a16", w4a16), ("w8a8", w8a8), ("fp8w", fp8w), ("mxfp8", mxfp8),
         ("qmoe_route", qmoe_route))
 
 
 def main(names=()):
-    names = set(names) or {n for n, _ in SETS} | {"silu_fp8", "moe", "lora", "e4m3fn_table"}
+    names = set(names) or {n for n, _ in SETS} | {"silu_fp8", "moe", "lora", "qmoe_ffn",
+                                                  "e4m3fn_table"}
     # The first five sets share one generator, drawn in this order (as first written).
     if names & {n for n, _ in SETS}:
         g = torch.Generator().manual_seed(SEEDS["w4a16"])
@@ -199,6 +256,9 @@ def main(names=()):
     if "lora" in names:
         g = torch.Generator().manual_seed(SEEDS["lora"])
         np.savez(os.path.join(HERE, "lora.npz"), **lora(g))
+    if "qmoe_ffn" in names:
+        g = torch.Generator().manual_seed(SEEDS["qmoe_ffn"])
+        np.savez(os.path.join(HERE, "qmoe_ffn.npz"), **qmoe_ffn(g))
     if "e4m3fn_table" in names:
         with open(os.path.join(HERE, "e4m3fn_table.json"), "w") as f:
             json.dump({"source": "torch.float8_e4m3fn -> float32, codes 0..255",

@@ -9,6 +9,7 @@ import pytest
 import torch
 
 from kernelbench_harbor_amd import MultiLoRAQGemmModel, inputs, ops
+from _grader import grader_ok
 from kernelbench_harbor_amd.harness import compare
 from oracle import lora as ol
 
@@ -30,8 +31,11 @@ def test_reference_task(dev, name, D, N, r, L, dtype):
     ins = inputs.lora_qgemm(64, D, N, r, L, dtype, seed=D + r)
     y = MultiLoRAQGemmModel()(*[t.to(dev) for t in ins])
     assert y.dtype == dtype and y.shape == (64, N)
-    cmp = compare(y, ol.forward(*_np(ins)))
+    gt = ol.forward(*_np(ins))
+    cmp = compare(y, gt)
     assert cmp.ok, cmp
+    dt = "f16" if dtype == torch.float16 else "bf16"
+    assert grader_ok(cmp, "multi_lora_qgemm", gt, lambda: ol.forward(*_np(ins), dtype=dt)), cmp
     assert torch.equal(y, MultiLoRAQGemmModel()(*[t.to(dev) for t in ins]))
 
 
@@ -65,11 +69,18 @@ def test_one_hot_matches_native_rounding(dev, dtype):
     assert np.array_equal(y, want), np.abs(y - want).max()
 
 
-def test_out_of_range_ids_are_clamped(dev):
-    """Adapter ids outside [0, L) select the nearest adapter (documented; torch would raise)."""
+def test_negative_and_out_of_range_ids(dev):
+    """Ids index like torch's A[lora_ids] (reference.py:14-16): -L..-1 select adapters 0..L-1.
+    Ids outside [-L, L), where torch raises, select the nearest adapter (documented)."""
     T, D, N, r, L = 8, 256, 128, 8, 3
     x, q, s, A, B, ids = inputs.lora_qgemm(T, D, N, r, L, torch.float16, seed=3)
-    bad = torch.tensor([-5, 0, 1, 2, 3, 7, -1, 2])
+    bad = torch.tensor([-5, 0, 1, 2, 3, 7, -1, -3])
     y = ops.lora_qgemm(*[t.to(dev) for t in (x, q, s, A, B, bad)])
-    want = ol.forward(*_np([x, q, s, A, B, bad.clamp(0, L - 1)]))
+    wrapped = torch.where((bad < 0) & (bad >= -L), bad + L, bad).clamp(0, L - 1)
+    assert wrapped.tolist() == [0, 0, 1, 2, 2, 2, 2, 0]
+    want = ol.forward(*_np([x, q, s, A, B, wrapped]))
     assert compare(y, want).ok
+    # the in-range negative ids alone give what torch's indexing gives
+    neg = torch.tensor([-1, -2, -3, -1, -2, -3, -1, -2])
+    y2 = ops.lora_qgemm(*[t.to(dev) for t in (x, q, s, A, B, neg)])
+    assert compare(y2, ol.forward(*_np([x, q, s, A, B, neg + L]))).ok

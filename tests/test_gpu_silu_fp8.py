@@ -70,7 +70,7 @@ def test_reference_task_grid(dev, name, H, T, dtype):
     assert out.dtype == torch.float32 and out.shape == (T, H)
     r_out, r_codes, _ = o.forward(y.float().numpy())
     cmp = compare(out, r_out)
-    assert cmp.ok, cmp
+    assert cmp.ok and cmp.task_ok("fused_silu_fp8"), cmp
     cos, rel = _cosine_rel(out.cpu().numpy(), r_out)
     assert cos >= 0.99 and rel <= 0.05, (cos, rel)
     _, codes, _ = _run(y.to(dev))

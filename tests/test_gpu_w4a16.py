@@ -102,6 +102,20 @@ def test_w4a16_dequant_bit_exact(dev, dtype, M, N, frac_zeros):
     assert np.array_equal(y, want), np.abs(y - want).max()
 
 
+@pytest.mark.parametrize("M", [64, 256, 1024])
+def test_w4a16_full_size_sweep_points(dev, M):
+    """The remaining BASELINE config 1 sweep points at K=14336, N=4096, g128 (64-row tiles with
+    many K splits, 256-row tiles, split-K 256-row tiles), checked against the oracle on the first
+    and last 256 output columns (every K split and group crosses both)."""
+    print(f"[w4a16 full] M={M}", flush=True)
+    x, qw, s, z = inputs.w4a16(M, 14336, 4096, 128, torch.float16, seed=M)
+    y = W4A16Model()(x.to(dev), qw.to(dev), s.to(dev), z.to(dev)).cpu()
+    for c in (slice(0, 256), slice(4096 - 256, 4096)):
+        gt = ow.forward(_np(x), qw[:, c.start // 8:c.stop // 8].numpy(), _np(s[:, c]), _np(z[:, c]))
+        cmp = compare(y[:, c], gt)
+        assert cmp.ok, (c, cmp)
+
+
 def test_w4a16_full_size_prefill(dev):
     """BASELINE config 1 largest point: M=2048, K=14336, N=4096."""
     print("[w4a16 full] M=2048", flush=True)

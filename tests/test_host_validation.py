@@ -56,6 +56,23 @@ def test_harness_compare_and_gate():
         harness.compare(gt[:4], gt)
 
 
+def test_harness_task_metrics():
+    """Each family's grader metric (allclose 2e-2 / cosine 0.99 + relative L1 0.05): a result
+    can pass one and fail the other, so both are reported and checked."""
+    gt = torch.randn(64, 128)
+    near = harness.compare(gt * 1.03, gt)          # cosine 1, rel_l1 0.03, allclose fails
+    assert near.cosine > 0.9999 and abs(near.rel_l1 - 0.03) < 1e-4
+    assert near.task_ok("fused_silu_fp8") and not near.task_ok("quant_w4a16_pa")
+    noisy = harness.compare(gt + 0.15 * torch.randn(64, 128), gt)
+    assert not noisy.task_ok("fused_silu_fp8") and not noisy.task_ok("moe")
+    exact = harness.compare(gt, gt)
+    assert all(exact.task_ok(f) for f in harness.TASK_METRICS)
+    res = harness.grade(lambda a: a * 1.03, lambda i: [gt], lambda inp: gt, draws=2,
+                        family="fused_silu_fp8")
+    assert [d["task_ok"] for d in res.draws] == [True, True]
+    assert res.correct is False          # the 3% error still fails the benchmark gate
+
+
 def test_harness_grade_records_errors_and_continues():
     def boom(*a):
         raise RuntimeError("kernel exploded")
