@@ -32,7 +32,8 @@ enum kbh_status {
   KBH_ERR_DTYPE = 3,         /* dtype code not supported */
   KBH_ERR_WORKSPACE = 4,     /* workspace NULL or smaller than *_workspace_bytes() */
   KBH_ERR_ALIGN = 5,         /* pointer not aligned as the kernel requires (16 B) */
-  KBH_ERR_LAUNCH = 6         /* the HIP runtime refused the launch (see kbh_last_hip_error) */
+  KBH_ERR_LAUNCH = 6,        /* the HIP runtime refused the launch (see kbh_last_hip_error) */
+  KBH_ERR_SCRATCH_LIMIT = 7  /* the call needs more than the fixed scratch of a no-alloc entry */
 };
 
 /* Library version of this ABI (KBH_ABI_VERSION). */
@@ -71,6 +72,21 @@ size_t kbh_w4a16_scratch_bytes(int M, int N, int K, int group);
 int kbh_w4a16_gemm(const void* x, const int32_t* qweight, const void* scales, const void* zeros,
                    void* y, void* workspace, size_t workspace_bytes, void* scratch,
                    size_t scratch_bytes, int M, int N, int K, int group, int dtype, void* stream);
+
+/* The same W4A16 GEMM without any caller buffer or allocation. No counterpart in the reference:
+ * it is for callers that cannot allocate device memory or pass a workspace (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc). The split-K partial sums live
+ * in a fixed array inside the library, KBH_W4A16_NOALLOC_SCRATCH_BYTES per GPU, held from the
+ * first call on that GPU until the process ends (enough for every M at K=14336, N=4096); calls
+ * whose path needs more (e.g. M=128, N=12288, K=14336: 84 MiB of K-split partial sums) return
+ * KBH_ERR_SCRATCH_LIMIT without launching. The array needs no
+ * particular content. All calls on one GPU share it: calls that may overlap in time on the same
+ * GPU (different streams, or host threads) race and must be ordered by the caller. Runs on the
+ * device current at the call. Results are bit-identical to kbh_w4a16_gemm's. */
+#define KBH_W4A16_NOALLOC_SCRATCH_BYTES ((size_t)64 << 20)
+int kbh_w4a16_gemm_noalloc(const void* x, const int32_t* qweight, const void* scales,
+                           const void* zeros, void* y, int M, int N, int K, int group, int dtype,
+                           void* stream);
 
 /* ---------------------------------------------------------------------------------------
  * W8A8 SmoothQuant int8 GEMM.

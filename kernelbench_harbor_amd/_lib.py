@@ -23,6 +23,11 @@ KBH_ERR_DTYPE = 3
 KBH_ERR_WORKSPACE = 4
 KBH_ERR_ALIGN = 5
 KBH_ERR_LAUNCH = 6
+KBH_ERR_SCRATCH_LIMIT = 7
+
+# KBH_W4A16_NOALLOC_SCRATCH_BYTES of include/kbh_qgemm.h: the fixed per-GPU scratch of
+# kbh_w4a16_gemm_noalloc.
+W4A16_NOALLOC_SCRATCH_BYTES = 64 << 20
 
 KBH_F16 = 0
 KBH_BF16 = 1
@@ -39,6 +44,7 @@ SIGNATURES = {
     "kbh_w4a16_workspace_bytes": (_sz, [_i, _i, _i, _i]),
     "kbh_w4a16_scratch_bytes": (_sz, [_i, _i, _i, _i]),
     "kbh_w4a16_gemm": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _sz, _vp, _sz, _i, _i, _i, _i, _i, _vp]),
+    "kbh_w4a16_gemm_noalloc": (_i, [_vp] * 5 + [_i] * 5 + [_vp]),
     "kbh_w8a8_workspace_bytes": (_sz, [_i, _i, _i]),
     "kbh_w8a8_scratch_bytes": (_sz, [_i, _i, _i]),
     "kbh_w8a8_gemm": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _sz, _vp, _sz, _i, _i, _i, _vp]),

@@ -31,6 +31,8 @@ extern "C" const char* kbh_status_string(int status) {
     case KBH_ERR_WORKSPACE: return "workspace missing or too small";
     case KBH_ERR_ALIGN: return "pointer not 16-byte aligned";
     case KBH_ERR_LAUNCH: return "kernel launch failed";
+    case KBH_ERR_SCRATCH_LIMIT:
+      return "the call needs more than the library's fixed scratch (use the workspace entry point)";
     default: return "unknown status";
   }
 }

@@ -54,6 +54,13 @@ def test_host_checks_run_without_gpu():
     need = lib.kbh_w4a16_scratch_bytes(2048, 4096, 14336, 128)
     assert lib.kbh_w4a16_gemm(p, p, p, p, p, p, 1 << 20, p, need - 1, 2048, 4096, 14336, 128, 0, None) == _lib.KBH_ERR_WORKSPACE
     assert lib.kbh_w4a16_gemm(p, p, p, p, p, p, 1 << 20, None, 0, 2048, 4096, 14336, 128, 0, None) == _lib.KBH_ERR_WORKSPACE
+    # the no-alloc W4A16 entry point checks its arguments and the size of its fixed scratch
+    # before any HIP call
+    assert lib.kbh_w4a16_gemm_noalloc(None, p, p, p, p, 16, 4096, 4096, 128, 0, None) == _lib.KBH_ERR_NULL
+    assert lib.kbh_w4a16_gemm_noalloc(p, p, p, p, p, 16, 4096, 4100, 128, 0, None) == _lib.KBH_ERR_SHAPE
+    assert lib.kbh_w4a16_gemm_noalloc(p, p, p, p, p, 128, 12288, 14336, 128, 0, None) == _lib.KBH_ERR_SCRATCH_LIMIT
+    assert b"fixed scratch" in lib.kbh_status_string(_lib.KBH_ERR_SCRATCH_LIMIT)
+    assert lib.kbh_w4a16_scratch_bytes(2048, 4096, 14336, 128) <= _lib.W4A16_NOALLOC_SCRATCH_BYTES
     assert lib.kbh_w8a8_gemm(p, p, p, p, p, p, 1 << 20, p, 1 << 20, 16, 4096, 100, None) == _lib.KBH_ERR_SHAPE
     assert lib.kbh_w8a8_gemm(p, p, p, p, p, None, 0, p, 1 << 20, 16, 4096, 4096, None) == _lib.KBH_ERR_WORKSPACE
     need = lib.kbh_w8a8_scratch_bytes(512, 4096, 14336)

@@ -1,0 +1,51 @@
+"""The W4A16 entry point that allocates nothing (kbh_w4a16_gemm_noalloc), called through the C
+ABI: bit-identical to kbh_w4a16_gemm (same kernels, same split-K sum order) on consecutive
+calls that use the library's fixed scratch array, each call smaller than the one before it,
+across the wide-tile (split-K scratch), LDS-staged and decode (split-K workspace) paths."""
+import ctypes
+
+import pytest
+import torch
+
+from kernelbench_harbor_amd import _lib, inputs, ops
+
+pytestmark = pytest.mark.gpu
+
+# (M, K, N): M=2048 fills the 64 MiB array exactly (two K splits of 2048 x 4096 fp32), M=64 takes
+# 28 K splits on 64 x 256 tiles, M=160 with N=384 the LDS-staged kernel (no scratch), M=16 and
+# M=1 the split-K decode kernel.
+CASES = [(2048, 14336, 4096), (64, 14336, 4096), (160, 2048, 384), (16, 4096, 512), (1, 1024, 256)]
+
+
+def _noalloc(lib, x, qw, s, z, y, group):
+    M, K = x.shape
+    N = y.shape[1]
+    dt = _lib.KBH_F16 if x.dtype == torch.float16 else _lib.KBH_BF16
+    return lib.kbh_w4a16_gemm_noalloc(x.data_ptr(), qw.data_ptr(), s.data_ptr(), z.data_ptr(),
+                                      y.data_ptr(), M, N, K, group, dt,
+                                      ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_noalloc_matches_workspace_entry_point(dev, dtype):
+    lib = _lib.load()
+    assert lib.kbh_w4a16_scratch_bytes(2048, 4096, 14336, 128) == _lib.W4A16_NOALLOC_SCRATCH_BYTES
+    for M, K, N in CASES:
+        print(f"[noalloc] M={M} K={K} N={N} {dtype}", flush=True)
+        x, qw, s, z = [t.to(dev) for t in inputs.w4a16(M, K, N, 128, dtype, seed=M + K)]
+        want = ops.w4a16_gemm(x, qw, s, z)
+        y = torch.full_like(want, float("nan"))
+        _lib.check(_noalloc(lib, x, qw, s, z, y, 128), "kbh_w4a16_gemm_noalloc")
+        torch.cuda.synchronize()
+        assert torch.equal(y, want), (M, K, N)
+
+
+def test_noalloc_rejects_oversize_before_launch(dev):
+    lib = _lib.load()
+    M, K, N = 128, 14336, 12288          # 14 K splits of 128 x 12288 fp32 = 84 MiB
+    x, qw, s, z = [t.to(dev) for t in inputs.w4a16(1, K, N, seed=9)]
+    x = torch.zeros(M, K, dtype=torch.float16, device=dev)
+    y = torch.zeros(M, N, dtype=torch.float16, device=dev)
+    assert _noalloc(lib, x, qw, s, z, y, 128) == _lib.KBH_ERR_SCRATCH_LIMIT
+    torch.cuda.synchronize()
+    assert bool((y == 0).all())          # nothing was launched
