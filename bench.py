@@ -12,12 +12,15 @@ M in {128, 2048}, the top-2 W4A16 MoE SiLU FFN (T=512, Mixtral layer), the refer
 
 Inputs are synthetic (seeded, BASELINE distributions) and resident in HBM before timing. Each
 configuration rotates over enough input copies (> 2x the 256 MB Infinity Cache) that every call
-streams its weights from HBM. Per configuration two timings are reported: the median of
-event-bracketed single calls (the reference grader's protocol, which includes ~4-5 us of event
-overhead per call) and the mean of a batch of back-to-back calls between two events
+streams its weights from HBM. Per configuration two timings are reported: the median of 100
+event-bracketed single calls after 25 warm-up calls (`us_median`, the reference grader's
+protocol, common/kb_verifier.py:132-143, through harness.bench; it includes ~4-5 us of event
+overhead per call) and the mean of a batch of back-to-back calls replayed from a HIP graph
 (`us_batched`, close to the kernel duration); roofline fractions use the batched time.
 
-Prints ONE JSON line. The CPU baseline times the numpy oracle on the host cores.
+Prints ONE JSON line. The CPU baseline times the reference modules' own torch op sequences
+(oracle/torch_ref.py) on the host cores, for every sweep point and configuration: the
+native-dtype path and the fp32 ground truth separately.
 """
 from __future__ import annotations
 
@@ -161,24 +164,17 @@ def graph_batch(torch, fn, sets, batch, reps=4):
     return sorted(times)[len(times) // 2]
 
 
-def time_config(torch, fn, sets, iters, batch):
-    """(per-call event times [s], batched mean [s]) over rotating input sets. The batched time
-    comes from graph_batch, falling back to back-to-back eager calls."""
-    for i in range(3):
-        fn(*sets[i % len(sets)])
-    torch.cuda.synchronize()
-    ts = []
-    for i in range(iters):
-        a = torch.cuda.Event(enable_timing=True)
-        b = torch.cuda.Event(enable_timing=True)
-        a.record()
-        fn(*sets[i % len(sets)])
-        b.record()
-        b.synchronize()
-        ts.append(a.elapsed_time(b) * 1e-3)
+def time_config(torch, fn, sets, iters=100, batch=20, warmup=25):
+    """(per-call event times [s], batched mean [s]) over rotating input sets. The per-call
+    times follow the reference grader (harness.bench: `warmup` calls, then `iters` calls each
+    between two events and a synchronise); the batched time comes from graph_batch, falling back
+    to back-to-back eager calls."""
+    from kernelbench_harbor_amd import harness
+    ts = [t * 1e-3 for t in harness.bench(lambda i: fn(*sets[i]), warmup=warmup, iters=iters,
+                                          rotate=len(sets))]
     gb = graph_batch(torch, fn, sets, batch)
     if gb is not None:
-        return sorted(ts), gb
+        return ts, gb
     a = torch.cuda.Event(enable_timing=True)
     b = torch.cuda.Event(enable_timing=True)
     a.record()
@@ -186,7 +182,7 @@ def time_config(torch, fn, sets, iters, batch):
         fn(*sets[i % len(sets)])
     b.record()
     b.synchronize()
-    return sorted(ts), a.elapsed_time(b) * 1e-3 / batch
+    return ts, a.elapsed_time(b) * 1e-3 / batch
 
 
 def record(name, ts, batched, by, fl, peak, **extra):
@@ -284,39 +280,142 @@ def run_grid(torch, dev, inputs, ops, families=None):
 
 
 # ---- CPU baseline ----------------------------------------------------------------------------
-def cpu_baseline(sample_m, seed=0, per_m_seconds=3.0):
-    """Times the numpy oracle (oracle/w4a16.py, fp32 ground-truth path) on the host cores: a
-    bounded sample of repeated calls, about per_m_seconds at each M (10-30 s in all)."""
+def cpu_time(fn, ins, max_calls=3, budget_s=1.0):
+    """Host seconds per call of fn(*ins): one warm-up call (the first call also pays for faulting
+    in its fresh working memory), then timed calls until their sum passes budget_s or max_calls
+    are done; returns the median and the number of timed calls."""
+    fn(*ins)
+    ts = []
+    while len(ts) < max_calls and sum(ts) < budget_s:
+        t0 = time.perf_counter()
+        fn(*ins)
+        ts.append(time.perf_counter() - t0)
+    return sorted(ts)[len(ts) // 2], len(ts)
+
+
+def cpu_reference(jobs, native_budget_s=1.0):
+    """Times the reference modules' own torch op sequences (oracle/torch_ref.py: W4A16
+    reference.py:10-17, W8A8 :7-9, FP8 :9-12, qMoE :11-21, SiLU-FP8 :13-23, and the MXFP8 and
+    SiLU FFN restatements) on CPU tensors on this host: the fp32 ground truth (floating inputs
+    upcast, kb_verifier.py:195-196) for every record, and the native-dtype path (the task's own
+    dtypes) where it fits the time budget. Some hosts' torch runs fp16 GEMMs without vector
+    support (0.4 GFLOP/s measured on the GPU box, against 100+ for fp32): a probe measures this
+    host's fp16 GEMM rate, and a native call predicted to take longer than native_budget_s is
+    skipped with that prediction recorded. `jobs` maps a record name to (make_inputs, fn, flops,
+    native_is_fp16_gemm). torch uses the cores of the process's affinity mask, or the host share
+    when the environment states one in OMP_NUM_THREADS. Returns {name: {...}} and the setup."""
+    import torch
+
+    from oracle import torch_ref as tr
+    cores = len(os.sched_getaffinity(0))
+    share = int(os.environ.get("OMP_NUM_THREADS", "0") or 0)
+    torch.set_num_threads(min(cores, share) if share > 0 else cores)
+    g = torch.Generator().manual_seed(0)
+    a = torch.randn(16, 4096, generator=g).half()
+    b = torch.randn(4096, 1024, generator=g).half()
+    torch.matmul(a, b)
+    probe = []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        torch.matmul(a, b)
+        probe.append(time.perf_counter() - t0)
+    f16_rate = 2 * 16 * 4096 * 1024 / sorted(probe)[1]
+    res = {}
+    for name, (make, fn, fl, f16_gemm) in jobs.items():
+        print(f"[cpu] {name} ...", file=sys.stderr, flush=True)
+        ins = make()
+        gt_ins = tr.upcast(ins)
+        tg, ng = cpu_time(fn, gt_ins)
+        del gt_ins
+        r = {"gt_s": round(tg, 4), "gt_calls": ng,
+             "gt_tflops": round(fl / tg / 1e12, 4) if fl else None}
+        predicted = fl / f16_rate if (f16_gemm and fl) else 0.0
+        if predicted > native_budget_s:
+            r.update({"native_s": None, "native_skipped": (
+                f"predicted {predicted:.0f} s per call at this host's measured fp16 GEMM rate "
+                f"({f16_rate / 1e9:.2f} GFLOP/s)")})
+        else:
+            t, n = cpu_time(fn, ins)
+            r.update({"native_s": round(t, 4), "native_calls": n,
+                      "native_tflops": round(fl / t / 1e12, 4) if fl else None})
+        res[name] = r
+        del ins
+        print(f"[cpu] {name}: fp32 GT {tg:.3f} s, native {r['native_s']} s", file=sys.stderr,
+              flush=True)
+    return res, {"cores": cores, "torch_threads": torch.get_num_threads(),
+                 "omp_num_threads": share or None, "f16_gemm_gflops": round(f16_rate / 1e9, 3)}
+
+
+def cpu_jobs(ms, with_configs):
+    """The CPU workloads: one per sweep M and one per BASELINE configuration, on the same seeded
+    inputs the GPU records use (CPU tensors)."""
     import torch
 
     from kernelbench_harbor_amd import inputs
-    from oracle import w4a16 as ow
-    try:
-        from threadpoolctl import threadpool_info
-        threads = max([i.get("num_threads", 1) for i in threadpool_info()] or [1])
-    except Exception:
-        threads = os.cpu_count() or 1
-    total_flops, total_s, per = 0.0, 0.0, []
-    for M in sample_m:
-        x, qw, s, z = inputs.w4a16(M, K_DIM, N_DIM, GROUP, torch.float16, seed=seed)
-        xn, qn, sn, zn = x.float().numpy(), qw.numpy(), s.float().numpy(), z.float().numpy()
-        ts = []
-        while not ts or (sum(ts) < per_m_seconds and len(ts) < 50):
-            t0 = time.perf_counter()
-            ow.forward(xn, qn, sn, zn)
-            ts.append(time.perf_counter() - t0)
-        total_flops += gemm_flops(M) * len(ts)
-        total_s += sum(ts)
-        per.append({"M": M, "calls": len(ts), "median_s": round(sorted(ts)[len(ts) // 2], 4)})
-    return {"value": total_flops / total_s / 1e12, "unit": "TFLOP/s", "cores": threads,
-            "kind": "port",
-            "sample": (f"repeated calls of the numpy oracle forward (unpack, fp32 dequant, fp32 "
-                       f"BLAS matmul), about {per_m_seconds:g} s at each M in {sample_m}, "
-                       "K=14336 N=4096 g128; value = total FLOPs / total seconds"),
-            "seconds": round(total_s, 2), "per_m": per}
+    from oracle import torch_ref as tr
+    f16 = torch.float16
+    jobs = {}
+    for M in ms:
+        jobs[f"w4a16 M={M}"] = (lambda M=M: inputs.w4a16(M, K_DIM, N_DIM, GROUP, f16, seed=0),
+                                tr.w4a16, gemm_flops(M), True)
+    if with_configs:
+        for M in (16, 512):      # int8 operands upcast to fp32 by the reference itself
+            jobs[f"w8a8 M={M}"] = (lambda M=M: inputs.w8a8(M, K_DIM, N_DIM, seed=0), tr.w8a8,
+                                   gemm_flops(M), False)
+        for M in (128, 2048):    # fp32 GEMM of the decoded operands
+            jobs[f"mxfp8 M={M}"] = (lambda M=M: inputs.mxfp8(M, K_DIM, N_DIM, seed=0), tr.mxfp8,
+                                    gemm_flops(M), False)
+        jobs["fp8w (reference op) M=16 b128"] = (
+            lambda: inputs.fp8w(16, K_DIM, N_DIM, 128, f16, 0), tr.fp8w, gemm_flops(16), True)
+        jobs["qmoe_ffn T=512 D=4096 F=14336 E=8 top2"] = (
+            lambda: inputs.qmoe_ffn(seed=0), tr.qmoe_ffn, 2 * 512 * 8 * 3 * 4096 * 14336, True)
+        jobs["silu_fp8 (reference op) T=512 H=14336 g128"] = (
+            lambda: inputs.silu_fp8(512, 14336, f16, 0), tr.silu_fp8, 0, False)
+        jobs["qmoe (reference op) T=256 D=4096 N=14336 E=8"] = (
+            lambda: inputs.qmoe(seed=0), tr.qmoe, 2 * 256 * 8 * 4096 * 14336, True)
+    return jobs
 
 
-# ---- main ------------------------------------------------------------------------------------
+# ---- workloads -------------------------------------------------------------------------------
+def config_table(torch, dev, inputs, ops):
+    """The BASELINE configurations besides the headline sweep: name -> (make the rotated device
+    input sets, the op, algorithmic bytes, flops, MFMA peak, record fields). The qMoE FFN and the
+    reference qMoE op hold 757 / 470 MB of weights per set, already larger than the Infinity
+    Cache, so they use one set."""
+    f16 = torch.float16
+
+    def rot(make, by):
+        return lambda: rotation(lambda: [t.to(dev) for t in make()], by)
+    t = {}
+    for M in (16, 512):
+        t[f"w8a8 M={M}"] = (rot(lambda M=M: inputs.w8a8(M, K_DIM, N_DIM, seed=0), w8a8_bytes(M)),
+                            ops.w8a8_gemm, w8a8_bytes(M), gemm_flops(M), PEAK["i8"], {"M": M})
+    for M in (128, 2048):
+        t[f"mxfp8 M={M}"] = (rot(lambda M=M: inputs.mxfp8(M, K_DIM, N_DIM, seed=0), mxfp8_bytes(M)),
+                             ops.mxfp8_gemm, mxfp8_bytes(M), gemm_flops(M), PEAK["f8"], {"M": M})
+    t["fp8w (reference op) M=16 b128"] = (
+        rot(lambda: inputs.fp8w(16, K_DIM, N_DIM, 128, f16, 0), fp8w_bytes(16)), ops.fp8w_gemm,
+        fp8w_bytes(16), gemm_flops(16), PEAK["f16"], {"M": 16})
+    t["qmoe_ffn T=512 D=4096 F=14336 E=8 top2"] = (
+        lambda: [[x.to(dev) for x in inputs.qmoe_ffn(seed=0)]], ops.qmoe_ffn, ffn_bytes(),
+        ffn_flops(), PEAK["f16"], {"T": 512})
+    t["silu_fp8 (reference op) T=512 H=14336 g128"] = (
+        rot(lambda: inputs.silu_fp8(512, 14336, f16, 0), silu_fp8_bytes()), ops.silu_fp8_quant,
+        silu_fp8_bytes(), 0, PEAK["f16"], {"T": 512, "H": 14336})
+    t["qmoe (reference op) T=256 D=4096 N=14336 E=8"] = (
+        lambda: [[x.to(dev) for x in inputs.qmoe(seed=0)]], ops.qmoe, qmoe_bytes(), qmoe_flops(),
+        PEAK["f16"], {"T": 256})
+    return t
+
+
+def sweep_workload(torch, dev, inputs, M):
+    """Rotated device input sets of the headline sweep at one M."""
+    return rotation(lambda: [t.to(dev) for t in inputs.w4a16(M, K_DIM, N_DIM, GROUP,
+                                                               torch.float16, seed=0)],
+                    w4a16_bytes(M))
+
+
+# ---- main ----------------------------------------------------------------------------------
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -333,6 +432,10 @@ def main():
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                     help="only run 5 device copies of MIB MiB (calibrates rocprofv3 FETCH_SIZE/"
                          "WRITE_SIZE against a kernel of known traffic) and exit")
+    ap.add_argument("--only", type=str, default="",
+                    help="run only the named record ('w4a16 M=<M>' or a configuration name) "
+                         "--steps times after --warmup calls, eagerly, and print its call count "
+                         "(for rocprofv3 counter runs: one process per record)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (got --gpus {args.gpus}); this build has no "
@@ -357,6 +460,22 @@ def main():
         torch.cuda.synchronize()
         print(json.dumps({"copy_probe_bytes": n, "copies": 5}))
         return
+    if args.only:
+        table = config_table(torch, dev, inputs, ops)
+        if args.only.startswith("w4a16 M="):
+            M = int(args.only.split("=")[1])
+            sets, fn = sweep_workload(torch, dev, inputs, M), ops.w4a16_gemm
+        elif args.only in table:
+            sets, fn = table[args.only][0](), table[args.only][1]
+        else:
+            raise SystemExit(f"--only: unknown record {args.only!r}; one of 'w4a16 M=<M>', "
+                             + ", ".join(repr(k) for k in table))
+        torch.cuda.synchronize()
+        for i in range(args.warmup + args.steps):
+            fn(*sets[i % len(sets)])
+        torch.cuda.synchronize()
+        print(json.dumps({"only": args.only, "warmup": args.warmup, "calls": args.steps}))
+        return
     if args.grid:
         recs = run_grid(torch, dev, inputs, ops, [f for f in args.families.split(",") if f])
         print(json.dumps({"grid": recs, "n_gpus": 1, "data": "synthetic (seeded; the reference "
@@ -365,11 +484,7 @@ def main():
     ms = [int(v) for v in args.m.split(",") if v]
 
     # ---- headline: W4A16 sweep ----
-    sets = {}
-    for M in ms:
-        sets[M] = rotation(lambda: [t.to(dev) for t in inputs.w4a16(M, K_DIM, N_DIM, GROUP,
-                                                                     torch.float16, seed=0)],
-                           w4a16_bytes(M))
+    sets = {M: sweep_workload(torch, dev, inputs, M) for M in ms}
     torch.cuda.synchronize()
     calls = {M: 0 for M in ms}
     ev = {M: [] for M in ms}
@@ -388,6 +503,8 @@ def main():
             else:
                 ops.w4a16_gemm(*sets[M][i])
 
+    print(f"[bench] sweep M={ms}: {args.warmup} warm-up and {args.steps} timed steps",
+          file=sys.stderr, flush=True)
     for _ in range(args.warmup):
         step(False)
     torch.cuda.synchronize()
@@ -401,10 +518,12 @@ def main():
     for M in ms:
         ts = sorted(a.elapsed_time(b) * 1e-3 for a, b in ev[M])
         mean_s[M] = sum(ts) / len(ts)
-        _, batched = time_config(torch, ops.w4a16_gemm, sets[M], 3, 20)
-        sweep.append(record(f"w4a16 M={M}", ts, batched, w4a16_bytes(M), gemm_flops(M),
-                            PEAK["f16"], M=M, us_mean=round(mean_s[M] * 1e6, 2)))
+        grader, batched = time_config(torch, ops.w4a16_gemm, sets[M])
+        sweep.append(record(f"w4a16 M={M}", grader, batched, w4a16_bytes(M), gemm_flops(M),
+                            PEAK["f16"], M=M, us_step_mean=round(mean_s[M] * 1e6, 2)))
         step_flops += gemm_flops(M)
+        print(f"[bench] w4a16 M={M}: {sweep[-1]['us_batched']} us batched, "
+              f"{sweep[-1]['us_median']} us median", file=sys.stderr, flush=True)
     del sets
     torch.cuda.empty_cache()
 
@@ -419,52 +538,23 @@ def main():
         ach = d["flops"] / mean_s[Md] / 1e12
         roof = {"bound": "mfma", "achieved": round(ach, 1), "peak": PEAK["f16"] / 1e12,
                 "unit": "TFLOP/s", "frac": round(ach / (PEAK["f16"] / 1e12), 4)}
-    roof.update({"traffic": W4A16_PMC_TRAFFIC.get(Md), "launch": f"kbh_w4a16_gemm M={Md} K=14336 N=4096 g128",
+    roof.update({"traffic": W4A16_PMC_TRAFFIC.get(Md),
+                 "launch": f"kbh_w4a16_gemm M={Md} K=14336 N=4096 g128 (every kernel of the call)",
                  "avg_launch_us": round(mean_s[Md] * 1e6, 2),
-                 "timing": "mean of the HIP-event-bracketed launches of the timed steps"})
+                 "timing": "mean of the HIP-event-bracketed calls of the timed steps, on the "
+                           "stream the kernels run on"})
 
     # ---- the other BASELINE configurations ----
     configs = []
     if not args.no_configs:
-        it, bt = 20, 20
-        for M in (16, 512):
-            s_ = rotation(lambda: [t.to(dev) for t in inputs.w8a8(M, K_DIM, N_DIM, seed=0)],
-                          w8a8_bytes(M))
-            ts, bm = time_config(torch, ops.w8a8_gemm, s_, it, bt)
-            configs.append(record(f"w8a8 M={M}", ts, bm, w8a8_bytes(M), gemm_flops(M), PEAK["i8"], M=M))
+        for name, (make, fn, by, fl, peak, extra) in config_table(torch, dev, inputs, ops).items():
+            s_ = make()
+            ts, bm = time_config(torch, fn, s_, 100, 20 if len(s_) > 1 else 10)
+            configs.append(record(name, ts, bm, by, fl, peak, **extra))
+            print(f"[bench] {name}: {configs[-1]['us_batched']} us batched", file=sys.stderr,
+                  flush=True)
             del s_
-        for M in (128, 2048):
-            s_ = rotation(lambda: [t.to(dev) for t in inputs.mxfp8(M, K_DIM, N_DIM, seed=0)],
-                          mxfp8_bytes(M))
-            ts, bm = time_config(torch, ops.mxfp8_gemm, s_, it, bt)
-            configs.append(record(f"mxfp8 M={M}", ts, bm, mxfp8_bytes(M), gemm_flops(M), PEAK["f8"], M=M))
-            del s_
-        s_ = rotation(lambda: [t.to(dev) for t in inputs.fp8w(16, K_DIM, N_DIM, 128, torch.float16, 0)],
-                      fp8w_bytes(16))
-        ts, bm = time_config(torch, ops.fp8w_gemm, s_, it, bt)
-        configs.append(record("fp8w (reference op) M=16 b128", ts, bm, fp8w_bytes(16), gemm_flops(16),
-                              PEAK["f16"], M=16))
-        del s_
-        torch.cuda.empty_cache()
-        s_ = [[t.to(dev) for t in inputs.qmoe_ffn(seed=0)]]   # 757 MB of weights: no rotation
-        ts, bm = time_config(torch, ops.qmoe_ffn, s_, 10, 10)
-        configs.append(record("qmoe_ffn T=512 D=4096 F=14336 E=8 top2", ts, bm, ffn_bytes(),
-                              ffn_flops(), PEAK["f16"], T=512))
-        del s_
-        torch.cuda.empty_cache()
-        s_ = rotation(lambda: [t.to(dev) for t in inputs.silu_fp8(512, 14336, torch.float16, 0)],
-                      silu_fp8_bytes())
-        ts, bm = time_config(torch, ops.silu_fp8_quant, s_, it, bt)
-        configs.append(record("silu_fp8 (reference op) T=512 H=14336 g128", ts, bm,
-                              silu_fp8_bytes(), 0, PEAK["f16"], T=512, H=14336))
-        del s_
-        torch.cuda.empty_cache()
-        s_ = [[t.to(dev) for t in inputs.qmoe(seed=0)]]       # 470 MB of weights
-        ts, bm = time_config(torch, ops.qmoe, s_, 10, 10)
-        configs.append(record("qmoe (reference op) T=256 D=4096 N=14336 E=8", ts, bm,
-                              qmoe_bytes(), qmoe_flops(), PEAK["f16"], T=256))
-        del s_
-        torch.cuda.empty_cache()
+            torch.cuda.empty_cache()
 
     out = {
         "metric": METRIC,
@@ -484,7 +574,30 @@ def main():
         "configs": configs,
     }
     if not args.no_cpu_baseline:
-        out["cpu_baseline"] = cpu_baseline([m for m in ms if m <= 256] or ms[:1])
+        cpu, setup = cpu_reference(cpu_jobs(ms, not args.no_configs))
+        for r in sweep + configs:
+            r["cpu"] = cpu.get(r["name"])
+        tot_fl = sum(gemm_flops(M) for M in ms)
+        tot_gt = sum(cpu[f"w4a16 M={M}"]["gt_s"] for M in ms)
+        native = [M for M in ms if cpu[f"w4a16 M={M}"]["native_s"] is not None]
+        out["cpu_baseline"] = {
+            "value": round(tot_fl / tot_gt / 1e12, 4), "unit": "TFLOP/s",
+            "cores": setup["torch_threads"], "affinity_cpus": setup["cores"],
+            "torch_threads": setup["torch_threads"], "kind": "port",
+            "sample": ("the reference Model.forward op sequence of the W4A16 task "
+                       "(oracle/torch_ref.py, reference.py:10-17) in torch on the host, on the "
+                       "grader's fp32-upcast inputs (kb_verifier.py:195-196), at each sweep M "
+                       f"{ms} one warm-up call then the median of up to 3 timed calls (fewer "
+                       "once they pass 1 s); value = the sweep's FLOPs / the summed seconds. "
+                       "The native fp16 "
+                       "path is timed where this host's fp16 GEMM rate allows (per-record 'cpu' "
+                       "entries; every sweep point and configuration carries one)"),
+            "seconds": round(tot_gt, 3),
+            "native_f16_value": (round(sum(gemm_flops(M) for M in native)
+                                       / sum(cpu[f"w4a16 M={M}"]["native_s"] for M in native)
+                                       / 1e12, 6) if native else None),
+            "native_f16_sample_m": native,
+            "f16_gemm_gflops": setup["f16_gemm_gflops"]}
     print(json.dumps(out), flush=True)
 
 

@@ -1,6 +1,9 @@
-"""Summarises a ``rocprofv3 --kernel-trace -f csv`` trace per (kernel, grid, workgroup size).
+"""Summarises a ``rocprofv3 --kernel-trace -f csv`` trace per (kernel, grid, workgroup size), or
+a ``rocprofv3 --pmc`` counter collection per op call.
 
     python -m kernelbench_harbor_amd.rocprof_summary <prefix>_kernel_trace.csv [--match SUBSTR]
+    python -m kernelbench_harbor_amd.rocprof_summary <prefix>_counter_collection.csv \
+        --match kbh:: --pmc-calls N
 
 Launches of one kernel symbol with different grids (for example the W4A16 kernel at several
 M) are reported separately, so the average duration of one configuration can be compared with
@@ -33,11 +36,32 @@ def summarize(path: str, match: str | None = None) -> list[dict]:
     return out
 
 
+def counter_totals(path: str, match: str | None = None) -> dict[str, dict]:
+    """Sums each counter of a ``rocprofv3 --pmc ... -f csv`` run over the dispatches of kernels
+    whose name contains `match`: {counter: {"total": sum, "dispatches": n}}."""
+    out: dict[str, dict] = {}
+    with open(path, newline="") as f:
+        for r in csv.DictReader(f):
+            if match and match not in r["Kernel_Name"]:
+                continue
+            d = out.setdefault(r["Counter_Name"], {"total": 0.0, "dispatches": 0})
+            d["total"] += float(r["Counter_Value"])
+            d["dispatches"] += 1
+    return out
+
+
 def main() -> None:
     ap = argparse.ArgumentParser()
     ap.add_argument("trace")
     ap.add_argument("--match", default=None)
+    ap.add_argument("--pmc-calls", type=int, default=0,
+                    help="the file is a --pmc counter collection: print each counter's sum over "
+                         "the matching dispatches divided by this many op calls")
     a = ap.parse_args()
+    if a.pmc_calls:
+        for name, d in counter_totals(a.trace, a.match).items():
+            print(f"{name} {d['total'] / a.pmc_calls:.1f} per call ({d['dispatches']} dispatches)")
+        return
     rows = summarize(a.trace, a.match)
     print("| kernel | grid (threads x,y) | wg | calls | avg us | median us | min us | max us |")
     print("|---|---|---|---|---|---|---|---|")
