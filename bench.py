@@ -48,11 +48,20 @@ def w4a16_bytes(M, K=K_DIM, N=N_DIM, G=GROUP):
     return K * N // 2 + 2 * (K // G) * N * 2 + 2 * M * K + 2 * M * N
 
 
-# HBM bytes per kbh_w4a16_gemm call at the sweep's two regimes, from rocprofv3 PMC runs:
-# FETCH_SIZE scaled by 2.0 (a plain 256 MiB device copy reads as 131085.4 KiB) plus WRITE_SIZE
-# (exact on the same copy), summed over the call's launches (GEMM + split-K slice sum).
-# Keyed by M; other M report null.
-W4A16_PMC_TRAFFIC = {16: 43_591_066, 2048: 466_528_461}
+# HBM bytes per op call of every record, from rocprofv3 PMC runs (one process per record and
+# counter: `bench.py --only <record> --steps 5 --warmup 2`): FETCH_SIZE scaled by 2.0 (a plain
+# 256 MiB device copy reads as 131084 KiB) plus WRITE_SIZE (exact on the same copy), summed over
+# every kbh:: kernel of the call. Table and commands: profiles/hbm_traffic_all_records.md.
+PMC_TRAFFIC = {
+    "w4a16 M=1": 32_157_994, "w4a16 M=4": 34_446_097, "w4a16 M=16": 43_588_085,
+    "w4a16 M=64": 94_334_871, "w4a16 M=256": 167_619_648, "w4a16 M=1024": 303_572_131,
+    "w4a16 M=2048": 466_521_290, "w8a8 M=16": 68_180_693, "w8a8 M=512": 274_725_693,
+    "mxfp8 M=128": 94_943_156, "mxfp8 M=2048": 291_247_371,
+    "fp8w (reference op) M=16 b128": 70_947_288,
+    "qmoe_ffn T=512 D=4096 F=14336 E=8 top2": 1_245_009_775,
+    "silu_fp8 (reference op) T=512 H=14336 g128": 60_958_806,
+    "qmoe (reference op) T=256 D=4096 N=14336 E=8": 534_838_367,
+}
 
 
 def gemm_flops(M, N=N_DIM, K=K_DIM):
@@ -189,6 +198,7 @@ def record(name, ts, batched, by, fl, peak, **extra):
     med = ts[len(ts) // 2]
     bound, frac = roofline(batched, by, fl, peak)
     out = {"name": name, **extra, "us_median": round(med * 1e6, 2),
+           "traffic": PMC_TRAFFIC.get(name),
            "us_batched": round(batched * 1e6, 2), "tflops": round(fl / batched / 1e12, 2),
            "gbps": round(by / batched / 1e9, 1), "bound": bound, "roofline_frac": round(frac, 4),
            "bytes": by, "flops": fl}
@@ -376,6 +386,47 @@ def cpu_jobs(ms, with_configs):
     return jobs
 
 
+# ---- calibration ---------------------------------------------------------------------------
+def mfma_ceiling(torch, dev, probe_path, blocks=256):
+    """Runs the calibration kernels of kernelbench_harbor_amd/probe/mfma_ceiling.hip (one
+    workgroup of 4 waves per CU): fp16 32x32x16 MFMA TFLOP/s with operands fixed in registers and
+    with fresh random operands from LDS for every MFMA, and LDS ds_read_b128 GB/s per CU. The
+    random-operand rate is the practical ceiling of a GEMM on random data (the MFMAs draw more
+    power when their operands switch, and the chip lowers its clock)."""
+    import ctypes
+    lib = ctypes.CDLL(probe_path)
+    lib.kbh_probe_run.restype = ctypes.c_int
+    lib.kbh_probe_run.argtypes = [ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int,
+                                  ctypes.c_int, ctypes.c_void_p]
+    g = torch.Generator(device=dev).manual_seed(0)
+    src = (torch.randint(0, 2 ** 31, (1 << 18,), generator=g, device=dev, dtype=torch.int64)
+           & 0x3BFF3BFF).to(torch.int32)                 # finite fp16 pairs, |v| < 1
+    out = torch.zeros(blocks * 256, dtype=torch.float32, device=dev)
+    stream = torch.cuda.current_stream().cuda_stream
+
+    def run(which, iters, reps=5):
+        assert lib.kbh_probe_run(which, src.data_ptr(), out.data_ptr(), blocks, iters, stream) == 0
+        torch.cuda.synchronize()
+        ts = []
+        for _ in range(reps):
+            a = torch.cuda.Event(enable_timing=True)
+            b = torch.cuda.Event(enable_timing=True)
+            a.record()
+            lib.kbh_probe_run(which, src.data_ptr(), out.data_ptr(), blocks, iters, stream)
+            b.record()
+            b.synchronize()
+            ts.append(a.elapsed_time(b) * 1e-3)
+        return sorted(ts)[reps // 2]
+    res = {"workgroups": blocks, "waves_per_workgroup": 4}
+    for which, key in ((0, "mfma_f16_fixed_operands_tflops"), (1, "mfma_f16_random_operands_tflops")):
+        t = run(which, 4000)
+        res[key] = round(blocks * 4 * 8 * 4000 * 32768 / t / 1e12, 1)
+    t = run(2, 4000)
+    res["lds_read_gbps_per_cu"] = round(256 * 16 * 16 * 4000 / t / 1e9, 1)
+    res["peak_datasheet_tflops"] = PEAK["f16"] / 1e12
+    return res
+
+
 # ---- workloads -------------------------------------------------------------------------------
 def config_table(torch, dev, inputs, ops):
     """The BASELINE configurations besides the headline sweep: name -> (make the rotated device
@@ -432,6 +483,10 @@ def main():
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                     help="only run 5 device copies of MIB MiB (calibrates rocprofv3 FETCH_SIZE/"
                          "WRITE_SIZE against a kernel of known traffic) and exit")
+    ap.add_argument("--mfma-ceiling", action="store_true",
+                    help="only run the calibration kernels (kernelbench_harbor_amd/probe): the "
+                         "fp16 MFMA rate with fixed and with random operands, and the LDS read "
+                         "bandwidth, then print one JSON line")
     ap.add_argument("--only", type=str, default="",
                     help="run only the named record ('w4a16 M=<M>' or a configuration name) "
                          "--steps times after --warmup calls, eagerly, and print its call count "
@@ -459,6 +514,9 @@ def main():
             dst.copy_(src)
         torch.cuda.synchronize()
         print(json.dumps({"copy_probe_bytes": n, "copies": 5}))
+        return
+    if args.mfma_ceiling:
+        print(json.dumps(mfma_ceiling(torch, dev, kbuild.PROBE_PATH)), flush=True)
         return
     if args.only:
         table = config_table(torch, dev, inputs, ops)
@@ -538,7 +596,7 @@ def main():
         ach = d["flops"] / mean_s[Md] / 1e12
         roof = {"bound": "mfma", "achieved": round(ach, 1), "peak": PEAK["f16"] / 1e12,
                 "unit": "TFLOP/s", "frac": round(ach / (PEAK["f16"] / 1e12), 4)}
-    roof.update({"traffic": W4A16_PMC_TRAFFIC.get(Md),
+    roof.update({"traffic": PMC_TRAFFIC.get(f"w4a16 M={Md}"),
                  "launch": f"kbh_w4a16_gemm M={Md} K=14336 N=4096 g128 (every kernel of the call)",
                  "avg_launch_us": round(mean_s[Md] * 1e6, 2),
                  "timing": "mean of the HIP-event-bracketed calls of the timed steps, on the "

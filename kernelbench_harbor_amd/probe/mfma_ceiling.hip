@@ -1,0 +1,106 @@
+// Calibration kernels (measurement infrastructure, not part of the operator library): the MFMA
+// rate gfx950 sustains for fp16 32x32x16 MFMAs, with operands either held in registers (little
+// switching) or read as fresh random fragments from LDS for every MFMA (the switching of a real
+// GEMM), and the LDS read bandwidth. bench.py --mfma-ceiling runs them; the rate with random
+// operands is the practical ceiling the W4A16 GEMM's MFMA utilisation is compared with.
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace {
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+// 8 independent accumulators per wave, A and B fixed per wave (one bit of A flips per round).
+__global__ __launch_bounds__(256) void mfma_fixed_operands(const u32x4* __restrict__ src,
+                                                           float* __restrict__ out, int iters) {
+  const int t = threadIdx.x;
+  u32x4 a = src[(blockIdx.x * 256 + t) & 65535], b = src[(blockIdx.x * 256 + t + 7) & 65535];
+  f32x16 c[8];
+  for (int i = 0; i < 8; ++i)
+    for (int e = 0; e < 16; ++e) c[i][e] = 0.f;
+  for (int it = 0; it < iters; ++it) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+      c[i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a),
+                                                   __builtin_bit_cast(f16x8, b), c[i], 0, 0, 0);
+    a = a ^ u32x4{0x00010001u, 0u, 0u, 0u};
+  }
+  float sum = 0.f;
+  for (int i = 0; i < 8; ++i) sum += c[i][0] + c[i][15];
+  out[blockIdx.x * 256 + t] = sum;
+}
+
+// Fresh random A (2 fragments) and B (4 fragments) from LDS for every 8 MFMAs: 0.75 KB of LDS
+// reads per MFMA and operand switching like a GEMM on random data. LDS holds 64 KB of the
+// random source; every offset stays inside it.
+__global__ __launch_bounds__(256) void mfma_random_operands(const u32x4* __restrict__ src,
+                                                            float* __restrict__ out, int iters) {
+  __shared__ __attribute__((aligned(16))) uint8_t s[65536];
+  const int t = threadIdx.x;
+  for (int i = t; i < 65536 / 16; i += 256)
+    reinterpret_cast<u32x4*>(s)[i] = src[(blockIdx.x * 4096 + i) & 65535];
+  __syncthreads();
+  const int lane = t & 63, wave = t >> 6;
+  f32x16 c[8];
+  for (int i = 0; i < 8; ++i)
+    for (int e = 0; e < 16; ++e) c[i][e] = 0.f;
+  for (int it = 0; it < iters; ++it) {
+    u32x4 a[2], b[4];
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+      a[j] = *reinterpret_cast<const u32x4*>(s + (((it * 6 + j) * 4 + wave) * 1024 + lane * 16) % 32768);
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      b[j] = *reinterpret_cast<const u32x4*>(
+          s + 32768 + (((it * 6 + 2 + j) * 4 + wave) * 1024 + lane * 16) % 32768);
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        c[i * 4 + j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(
+            __builtin_bit_cast(f16x8, a[i]), __builtin_bit_cast(f16x8, b[j]), c[i * 4 + j], 0, 0, 0);
+  }
+  float sum = 0.f;
+  for (int i = 0; i < 8; ++i) sum += c[i][0] + c[i][15];
+  out[blockIdx.x * 256 + t] = sum;
+}
+
+// ds_read_b128 throughput: every lane reads 16 B per read, consecutive lanes consecutive 16 B
+// (a compiler memory barrier per round of 16 reads keeps the reads inside the loop).
+__global__ __launch_bounds__(256) void lds_read_b128(uint32_t* __restrict__ out, int iters) {
+  __shared__ __attribute__((aligned(16))) uint8_t s[65536];
+  const int t = threadIdx.x;
+  for (int i = t; i < 65536 / 16; i += 256)
+    reinterpret_cast<u32x4*>(s)[i] = u32x4{(uint32_t)i, 1u, 2u, 3u};
+  __syncthreads();
+  u32x4 acc = {0u, 0u, 0u, 0u};
+  const int lane = t & 63, wave = t >> 6;
+  for (int it = 0; it < iters; ++it) {
+#pragma unroll
+    for (int j = 0; j < 16; ++j)
+      acc ^= *reinterpret_cast<const u32x4*>(
+          s + ((((it & 3) * 64 + wave * 16 + j) * 1024 + lane * 16) & 65535));
+    asm volatile("" ::: "memory");  // LDS may have changed: every round reads it again
+  }
+  if ((acc[0] ^ acc[1] ^ acc[2] ^ acc[3]) == 0x12345678u) out[blockIdx.x] = 1u;
+}
+}  // namespace
+
+// which: 0 fixed-operand MFMAs, 1 random-operand MFMAs, 2 LDS reads. src: >= 1 MiB of random
+// finite fp16 data; out: >= blocks * 256 floats.
+extern "C" int kbh_probe_run(int which, const void* src, void* out, int blocks, int iters,
+                             void* stream) {
+  hipStream_t st = (hipStream_t)stream;
+  if (which == 0)
+    hipLaunchKernelGGL(mfma_fixed_operands, dim3(blocks), dim3(256), 0, st, (const u32x4*)src,
+                       (float*)out, iters);
+  else if (which == 1)
+    hipLaunchKernelGGL(mfma_random_operands, dim3(blocks), dim3(256), 0, st, (const u32x4*)src,
+                       (float*)out, iters);
+  else if (which == 2)
+    hipLaunchKernelGGL(lds_read_b128, dim3(blocks), dim3(256), 0, st, (uint32_t*)out, iters);
+  else
+    return 2;
+  return hipGetLastError() == hipSuccess ? 0 : 6;
+}
