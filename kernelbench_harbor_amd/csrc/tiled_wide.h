@@ -352,6 +352,10 @@ __global__ __launch_bounds__(256) void wide_reduce_kernel(const typename E::Part
   ep.emit4(r, (int)(e - (size_t)r * N), v);
 }
 
+// Split-K plans keep their partial-sum slices within this many bytes (the writes and reads of
+// more cost more than the extra splits gain, and it bounds the scratch a call needs).
+constexpr size_t kWideMaxSliceBytes = (size_t)64 << 20;
+
 // Launch geometry: tiles ordered (row block, split, column block) so that consecutive ids,
 // which share an XCD, share rows of x and a K range.
 struct WidePlan {
@@ -361,18 +365,23 @@ struct WidePlan {
   int grid;
 };
 
-// Picks the tile height and the split count. Up to 128 rows the tiles are tm_small rows high;
+// Picks the tile height and the split count. Up to small_upto rows (default 128) the tiles are
+// tm_small rows high;
 // above, 256 rows, or (choose_tm) tm_small rows when the cost estimate favours them, i.e. when
 // 256-row tiles would leave CUs idle. `slots` is the number of workgroups the GPU runs at once
 // (256 CUs x workgroups per CU). A split count is valid when it divides the K slabs into ranges
 // of at least 8 slabs that are a multiple of `unroll`; among those, the plan minimises (waves of
 // workgroups) x (slabs per workgroup), preferring fewer splits on a tie.
 inline bool plan_wide(int M, int N, int K, int tn, int slab_k, int unroll, int slots,
-                      WidePlan* p, int tm_small = 128, bool choose_tm = false) {
+                      WidePlan* p, int tm_small = 128, bool choose_tm = false,
+                      int small_upto = 128) {
   if (N % tn != 0 || K % (unroll * slab_k) != 0 || M < 1) return false;
   const int KT = K / slab_k;
   // Plan for tile height tm; returns the estimated time in units of a third of a 128-row slab
-  // (a 256-row slab measures about 4/3 of a 128-row one).
+  // (a 256-row slab measures about 4/3 of a 128-row one, ~1 us at the BASELINE shapes), plus
+  // the split-K slices: s slices of M x N 4-byte partial sums are written and read back, about
+  // one unit per 2^18 of them (2 MiB of traffic at ~5 TB/s). Without that term the plan chose
+  // 56 splits at M=384 (336 MiB of slices).
   auto plan_tm = [&](int tm, WidePlan* q) {
     q->tm = tm;
     const int tiles = ((M + tm - 1) / tm) * (N / tn);
@@ -381,8 +390,10 @@ inline bool plan_wide(int M, int N, int K, int tn, int slab_k, int unroll, int s
       if (KT % s != 0) continue;
       const int spp = KT / s;
       if (spp % unroll != 0 || (spp < 8 && s > 1)) continue;
+      if (s > 1 && (size_t)s * M * N * 4u > kWideMaxSliceBytes) continue;
       const long waves = ((long)tiles * s + slots - 1) / slots;
-      const long cost = waves * spp;
+      const long slices = s > 1 ? (long)s * M * N >> 18 : 0;
+      const long cost = waves * spp * (tm == 256 ? 4 : 3) + slices;
       if (best < 0 || cost < best) {
         best = cost;
         q->splits = s;
@@ -390,9 +401,9 @@ inline bool plan_wide(int M, int N, int K, int tn, int slab_k, int unroll, int s
       }
     }
     q->grid = tiles * q->splits;
-    return best * (tm == 256 ? 4 : 3);
+    return best;
   };
-  if (M <= 128) {
+  if (M <= small_upto) {
     plan_tm(tm_small, p);
     return true;
   }

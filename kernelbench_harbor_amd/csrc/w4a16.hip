@@ -269,11 +269,16 @@ bool plan_w4_wide(int M, int N, int K, int group, W4Wide* w) {
   if (!small && w->tn != 256) return false;
   const int pd = w4_wide_pd(w->tn);
   const int unroll = 2 * w->spg > pd ? 2 * w->spg : pd;  // the kernel's slabs per iteration
-  // Up to 64 rows with 256-column tiles: 64 x 256 tiles (2 x 2 waves of 32 x 128, two
-  // workgroups per CU); a 128-row tile would spend half its MFMAs and A loads on padding.
+  // Up to 64 rows with 256-column tiles: 64 x 256 tiles (2 x 2 waves of 32 x 128); a 128-row
+  // tile would spend half its MFMAs and A loads on padding. The split count is planned for one
+  // workgroup per CU: more splits (two per CU) measured slower, their fp32 slices outweighing
+  // the extra parallelism (K=14336 N=4096 M=64: 14 splits 31.2 us, 28 splits 34.4 us).
+  // 128-row tiles (one workgroup per CU) up to 384 rows: fewer K splits, so fewer fp32 slices
+  // to write and sum, than 256-row tiles (M=256: 57.9 against 63.3 us; M=384: 85.4 against
+  // 91.7 us); 256-row tiles above (M=512: 99.9 against 104.6 us).
   const bool rows64 = M <= 64 && w->tn == 256;
-  return plan_wide(M, N, K, w->tn, 32, unroll, (w->tn == 128 || rows64) ? 512 : 256, &w->plan,
-                   rows64 ? 64 : 128, w->tn == 256);
+  return plan_wide(M, N, K, w->tn, 32, unroll, w->tn == 128 ? 512 : 256, &w->plan,
+                   rows64 ? 64 : 128, w->tn == 256, w->tn == 256 ? 384 : 128);
 }
 
 template <bool BF16, int TM, int TN, int SPG>

@@ -12,7 +12,7 @@ from kernelbench_harbor_amd import _lib, inputs, ops
 pytestmark = pytest.mark.gpu
 
 # (M, K, N): M=2048 fills the 64 MiB array exactly (two K splits of 2048 x 4096 fp32), M=64 takes
-# 28 K splits on 64 x 256 tiles, M=160 with N=384 the LDS-staged kernel (no scratch), M=16 and
+# 14 K splits on 64 x 256 tiles, M=160 with N=384 the LDS-staged kernel (no scratch), M=16 and
 # M=1 the split-K decode kernel.
 CASES = [(2048, 14336, 4096), (64, 14336, 4096), (160, 2048, 384), (16, 4096, 512), (1, 1024, 256)]
 
@@ -42,8 +42,11 @@ def test_noalloc_matches_workspace_entry_point(dev, dtype):
 
 def test_noalloc_rejects_oversize_before_launch(dev):
     lib = _lib.load()
-    M, K, N = 128, 14336, 12288          # 14 K splits of 128 x 12288 fp32 = 84 MiB
-    x, qw, s, z = [t.to(dev) for t in inputs.w4a16(1, K, N, seed=9)]
+    M, K, N = 24, 65536, 12288           # decode kernel: K splits of 24 x 12288 fp32 = 72 MiB
+    assert lib.kbh_w4a16_workspace_bytes(M, N, K, 128) > _lib.W4A16_NOALLOC_SCRATCH_BYTES
+    qw = torch.empty(K // 8, N, dtype=torch.int32, device=dev)      # never read: no launch
+    s = torch.empty(K // 128, N, dtype=torch.float16, device=dev)
+    z = torch.empty(K // 128, N, dtype=torch.float16, device=dev)
     x = torch.zeros(M, K, dtype=torch.float16, device=dev)
     y = torch.zeros(M, N, dtype=torch.float16, device=dev)
     assert _noalloc(lib, x, qw, s, z, y, 128) == _lib.KBH_ERR_SCRATCH_LIMIT
