@@ -23,8 +23,11 @@
 //    register copies are needed.
 //  * Split-K (splits > 1): partial tiles go to per-split slices of a workspace (plain stores of
 //    E::Part: fp32, or int32 which sums exactly), summed in split order by wide_reduce_kernel.
-//  * Workgroup ids are remapped so that each XCD runs consecutive tiles of the same rows of x
-//    and K range (its L2 then serves the shared x fragments).
+//  * Workgroup ids are remapped so that each XCD runs consecutive ids, which are the column
+//    tiles of consecutive row blocks in one K range: its L2 then serves both the x rows the
+//    column tiles share and the weight slabs the row blocks share (the order (split, row block,
+//    column block) measured 65 vs 71 us on W8A8 M=512 and 288 vs 299 us on W4A16 M=2048 against
+//    (row block, split, column block), whose weight slabs each XCD fetched separately).
 //
 // Output policy (EP): void emit(int r, int n, E::Part v) const; one output element, and
 //   void emit4(int r, int n, vec4 v) const; four consecutive outputs of one row (n % 4 == 0).
@@ -162,8 +165,9 @@ tiled_wide_gemm(
   const int id = xcd_remap(blockIdx.x, gridDim.x);
   const int nb = id % NB;
   const int rest = id / NB;
-  const int split = rest % splits;
-  const int mb = rest / splits;
+  const int MB = gridDim.x / (NB * splits);  // row blocks (tile-table entries)
+  const int mb = rest % MB;
+  const int split = rest / MB;
   const int n0 = nb * TN;
   const int kt0 = split * slabs_per_split;
   const int KT = slabs_per_split;
@@ -356,8 +360,8 @@ __global__ __launch_bounds__(256) void wide_reduce_kernel(const typename E::Part
 // more cost more than the extra splits gain, and it bounds the scratch a call needs).
 constexpr size_t kWideMaxSliceBytes = (size_t)64 << 20;
 
-// Launch geometry: tiles ordered (row block, split, column block) so that consecutive ids,
-// which share an XCD, share rows of x and a K range.
+// Launch geometry: grid = row blocks x column blocks x splits, ids ordered (split, row block,
+// column block) so that consecutive ids, which share an XCD, share a K range.
 struct WidePlan {
   int tm;               // 128 or 256
   int splits;           // K ranges

@@ -285,8 +285,8 @@ struct W8WidePolicy {
   __device__ void load(Raw& r, int k0, int n0, int t) const {
     const int8_t* p = w + (size_t)(k0 + 8 * rb_of(t)) * N + n0 + 8 * cb_of(t);
 #pragma unroll
-    for (int i = 0; i < 8; ++i)
-      r.r[i] = __builtin_nontemporal_load(reinterpret_cast<const kbh_u32x2*>(p + (size_t)i * N));
+    for (int i = 0; i < 8; ++i)  // cached: the row blocks of a K range share them in L2
+      r.r[i] = *reinterpret_cast<const kbh_u32x2*>(p + (size_t)i * N);
   }
   __device__ void load_group(Grp&, int, int, int) const {}
   __device__ void store_part(const Raw& r, const Grp&, uint8_t* Bs, int t, int p) const {

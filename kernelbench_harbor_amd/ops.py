@@ -27,23 +27,28 @@ class _WorkspacePool:
     size of the current one."""
 
     def __init__(self):
-        self._bufs: dict[tuple[int, int], torch.Tensor] = {}
+        self._bufs: dict[tuple[int, int], tuple[torch.Tensor, int]] = {}
         self._retired: list[torch.Tensor] = []
         self._lock = threading.Lock()
 
-    def get(self, nbytes: int, device: torch.device) -> torch.Tensor:
-        stream = torch.cuda.current_stream(device).cuda_stream
-        key = (device.index if device.index is not None else torch.cuda.current_device(), stream)
+    def get(self, nbytes: int, device: torch.device, stream: int | None = None) -> torch.Tensor:
+        """A buffer of at least `nbytes` for calls on `stream` (default: the current stream of
+        `device`)."""
+        idx = device.index if device.index is not None else torch.cuda.current_device()
+        key = (idx, _stream_ptr(device) if stream is None else stream)
+        hit = self._bufs.get(key)            # a dict read is atomic; only growth takes the lock
+        if hit is not None and hit[1] >= nbytes:
+            return hit[0]
         with self._lock:
-            buf = self._bufs.get(key)
-            if buf is None or buf.numel() < nbytes:
+            hit = self._bufs.get(key)
+            if hit is None or hit[1] < nbytes:
                 size = max(nbytes, 256)
-                if buf is not None:
-                    self._retired.append(buf)
-                    size = max(size, 2 * buf.numel())
-                buf = torch.empty(size, dtype=torch.uint8, device=device)
-                self._bufs[key] = buf
-            return buf
+                if hit is not None:
+                    self._retired.append(hit[0])
+                    size = max(size, 2 * hit[1])
+                hit = (torch.empty(size, dtype=torch.uint8, device=device), size)
+                self._bufs[key] = hit
+            return hit[0]
 
 
 workspaces = _WorkspacePool()
@@ -55,8 +60,17 @@ def _require(cond: bool, msg: str) -> None:
         raise ValueError(msg)
 
 
+# torch's current-stream handle as a plain integer: the raw accessor costs ~0.1 us where
+# torch.cuda.current_stream(...).cuda_stream builds a Stream object (~2 us), a large share of a
+# decode-sized call.
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
 def _stream_ptr(device: torch.device) -> int:
-    return torch.cuda.current_stream(device).cuda_stream
+    idx = device.index if device.index is not None else torch.cuda.current_device()
+    if _raw_stream is not None:
+        return _raw_stream(idx)
+    return torch.cuda.current_stream(idx).cuda_stream
 
 
 def _check_device(*tensors: torch.Tensor) -> torch.device:
@@ -75,49 +89,55 @@ def w4a16_gemm(x: torch.Tensor, qweight: torch.Tensor, scales: torch.Tensor,
     reference.py:10-17: qweight [K, N/8] int32 with nibble i of word [k, j] = column 8j+i,
     scales/zeros [K/G, N] in x.dtype; the group size G is K / scales.shape[0].
     """
-    _require(x.dtype in _DT_CODE, f"x must be float16 or bfloat16, got {x.dtype}")
+    # Shapes and dtypes are read once into locals: each tensor attribute access costs ~0.1-0.2 us
+    # and a reshape ~1.5 us, a large share of a decode-sized call.
+    xd = x.dtype
+    code = _DT_CODE.get(xd)
+    _require(code is not None, f"x must be float16 or bfloat16, got {xd}")
     _require(qweight.dtype == torch.int32, f"qweight must be int32, got {qweight.dtype}")
-    _require(qweight.dim() == 2 and scales.dim() == 2 and zeros.dim() == 2,
+    xs, qs, ss, zs = x.shape, qweight.shape, scales.shape, zeros.shape
+    _require(len(qs) == 2 and len(ss) == 2 and len(zs) == 2,
              "qweight, scales and zeros must be 2-D")
-    K, NP = qweight.shape
+    K, NP = qs
     N = NP * 8
-    _require(x.shape[-1] == K, f"x last dim {x.shape[-1]} != qweight rows {K}")
-    _require(scales.shape[1] == N and zeros.shape == scales.shape,
-             f"scales/zeros must be [K/G, {N}], got {tuple(scales.shape)} / {tuple(zeros.shape)}")
-    _require(scales.shape[0] > 0 and K % scales.shape[0] == 0,
-             f"K={K} not divisible by scales rows {scales.shape[0]}")
-    group = K // scales.shape[0]
-    _require(scales.dtype == x.dtype and zeros.dtype == x.dtype,
-             "scales and zeros must have x's dtype")
+    _require(len(xs) >= 1 and xs[-1] == K, f"x last dim {tuple(xs)[-1:]} != qweight rows {K}")
+    _require(ss[1] == N and zs == ss,
+             f"scales/zeros must be [K/G, {N}], got {tuple(ss)} / {tuple(zs)}")
+    _require(ss[0] > 0 and K % ss[0] == 0, f"K={K} not divisible by scales rows {ss[0]}")
+    group = K // ss[0]
+    _require(scales.dtype == xd and zeros.dtype == xd, "scales and zeros must have x's dtype")
     dev = _check_device(x, qweight, scales, zeros)
-    lead = x.shape[:-1]
-    x2 = x.reshape(-1, K).contiguous()
-    M = x2.shape[0]
-    y = torch.empty((M, N), dtype=x.dtype, device=dev)
-    if M == 0:
-        return y.reshape(*lead, N)
-    qweight = qweight.contiguous()
-    scales = scales.contiguous()
-    zeros = zeros.contiguous()
-    lib = _lib.load()
-    ws = workspaces.get(lib.kbh_w4a16_workspace_bytes(M, N, K, group), dev)
-    sc = scratches.get(lib.kbh_w4a16_scratch_bytes(M, N, K, group), dev)
-    st = lib.kbh_w4a16_gemm(x2.data_ptr(), qweight.data_ptr(), scales.data_ptr(),
-                            zeros.data_ptr(), y.data_ptr(), ws.data_ptr(), ws.numel(),
-                            sc.data_ptr(), sc.numel(), M, N, K, group, _DT_CODE[x.dtype],
-                            _stream_ptr(dev))
-    _lib.check(st, "kbh_w4a16_gemm")
-    return y.reshape(*lead, N)
+    flat = len(xs) == 2
+    x2 = x.contiguous() if flat else x.reshape(-1, K).contiguous()
+    M = xs[0] if flat else x2.shape[0]
+    y = torch.empty((M, N), dtype=xd, device=dev)
+    if M > 0:
+        qweight = qweight.contiguous()
+        scales = scales.contiguous()
+        zeros = zeros.contiguous()
+        st = _stream_ptr(dev)
+        lib = _lib.load()
+        ws = workspaces.get(lib.kbh_w4a16_workspace_bytes(M, N, K, group), dev, st)
+        sc = scratches.get(lib.kbh_w4a16_scratch_bytes(M, N, K, group), dev, st)
+        _lib.check(lib.kbh_w4a16_gemm(x2.data_ptr(), qweight.data_ptr(), scales.data_ptr(),
+                                      zeros.data_ptr(), y.data_ptr(), ws.data_ptr(), ws.numel(),
+                                      sc.data_ptr(), sc.numel(), M, N, K, group, code, st),
+                   "kbh_w4a16_gemm")
+    return y if flat else y.reshape(*xs[:-1], N)
 
 
 def _w8a8_args(x_int8, w_int8):
+    """(x as [M, K], M, N, K, whether x was already 2-D)."""
     _require(x_int8.dtype == torch.int8 and w_int8.dtype == torch.int8,
              f"x_int8/w_int8 must be int8, got {x_int8.dtype}/{w_int8.dtype}")
-    _require(w_int8.dim() == 2, "w_int8 must be [K, N]")
-    K, N = w_int8.shape
-    _require(x_int8.shape[-1] == K, f"x_int8 last dim {x_int8.shape[-1]} != K={K}")
+    xs, wsh = x_int8.shape, w_int8.shape
+    _require(len(wsh) == 2, "w_int8 must be [K, N]")
+    K, N = wsh
+    _require(len(xs) >= 1 and xs[-1] == K, f"x_int8 last dim {tuple(xs)[-1:]} != K={K}")
+    if len(xs) == 2:
+        return x_int8, xs[0], N, K, True
     x2 = x_int8.reshape(-1, K)
-    return x2, x2.shape[0], N, K
+    return x2, x2.shape[0], N, K, False
 
 
 def w8a8_gemm(x_int8: torch.Tensor, w_int8: torch.Tensor, x_scale: torch.Tensor,
@@ -126,42 +146,41 @@ def w8a8_gemm(x_int8: torch.Tensor, w_int8: torch.Tensor, x_scale: torch.Tensor,
 
     Follows tasks/w8a8_smoothquant/w8a8_smoothquant__llama3_8b_down__M16/environment/
     reference.py:7-9: x_int8 [M, K], w_int8 [K, N], x_scale [M, 1] fp16, w_scale [1, N] fp16."""
-    x2, M, N, K = _w8a8_args(x_int8, w_int8)
+    x2, M, N, K, flat = _w8a8_args(x_int8, w_int8)
     _require(x_scale.dtype == torch.float16 and w_scale.dtype == torch.float16,
              "x_scale and w_scale must be float16")
     _require(x_scale.numel() == M and w_scale.numel() == N,
              f"x_scale must hold {M} values and w_scale {N}")
     dev = _check_device(x_int8, w_int8, x_scale, w_scale)
-    x2, w = x2.contiguous(), w_int8.contiguous()
-    lead = x_int8.shape[:-1]
     y = torch.empty((M, N), dtype=torch.float16, device=dev)
-    if M == 0:
-        return y.reshape(*lead, N)
-    xs = x_scale.reshape(M).contiguous()
-    ws_ = w_scale.reshape(N).contiguous()
-    lib = _lib.load()
-    ws = workspaces.get(lib.kbh_w8a8_workspace_bytes(M, N, K), dev)
-    sc = scratches.get(lib.kbh_w8a8_scratch_bytes(M, N, K), dev)
-    st = lib.kbh_w8a8_gemm(x2.data_ptr(), w.data_ptr(), xs.data_ptr(), ws_.data_ptr(),
-                           y.data_ptr(), ws.data_ptr(), ws.numel(), sc.data_ptr(), sc.numel(),
-                           M, N, K, _stream_ptr(dev))
-    _lib.check(st, "kbh_w8a8_gemm")
-    return y.reshape(*lead, N)
+    if M > 0:
+        # the scales are read as flat vectors: [M, 1] / [1, N] in place when contiguous
+        x2, w = x2.contiguous(), w_int8.contiguous()
+        xsc, wsc = x_scale.contiguous(), w_scale.contiguous()
+        st = _stream_ptr(dev)
+        lib = _lib.load()
+        ws = workspaces.get(lib.kbh_w8a8_workspace_bytes(M, N, K), dev, st)
+        sc = scratches.get(lib.kbh_w8a8_scratch_bytes(M, N, K), dev, st)
+        _lib.check(lib.kbh_w8a8_gemm(x2.data_ptr(), w.data_ptr(), xsc.data_ptr(), wsc.data_ptr(),
+                                     y.data_ptr(), ws.data_ptr(), ws.numel(), sc.data_ptr(),
+                                     sc.numel(), M, N, K, st), "kbh_w8a8_gemm")
+    return y if flat else y.reshape(*x_int8.shape[:-1], N)
 
 
 def w8a8_gemm_i32(x_int8: torch.Tensor, w_int8: torch.Tensor) -> torch.Tensor:
     """The exact int32 accumulators x_int8 @ w_int8 (reference.py:8 before the scales)."""
-    x2, M, N, K = _w8a8_args(x_int8, w_int8)
+    x2, M, N, K, _ = _w8a8_args(x_int8, w_int8)
     dev = _check_device(x_int8, w_int8)
     x2, w = x2.contiguous(), w_int8.contiguous()
     acc = torch.empty((M, N), dtype=torch.int32, device=dev)
     if M == 0:
         return acc
+    st = _stream_ptr(dev)
     lib = _lib.load()
-    ws = workspaces.get(lib.kbh_w8a8_workspace_bytes(M, N, K), dev)
-    sc = scratches.get(lib.kbh_w8a8_scratch_bytes(M, N, K), dev)
+    ws = workspaces.get(lib.kbh_w8a8_workspace_bytes(M, N, K), dev, st)
+    sc = scratches.get(lib.kbh_w8a8_scratch_bytes(M, N, K), dev, st)
     st = lib.kbh_w8a8_gemm_i32(x2.data_ptr(), w.data_ptr(), acc.data_ptr(), ws.data_ptr(),
-                               ws.numel(), sc.data_ptr(), sc.numel(), M, N, K, _stream_ptr(dev))
+                               ws.numel(), sc.data_ptr(), sc.numel(), M, N, K, st)
     _lib.check(st, "kbh_w8a8_gemm_i32")
     return acc
 
@@ -172,39 +191,38 @@ def fp8w_gemm(x: torch.Tensor, w_fp8: torch.Tensor, scales: torch.Tensor) -> tor
     Follows tasks/fp8_microscale/fp8_microscale__llama3_8b_down__b128__fp16/environment/
     reference.py:9-12: w_fp8 [K, N] float8_e4m3fn, scales [K/B, N] fp16; the block size B is
     K / scales.shape[0]."""
-    _require(x.dtype in _DT_CODE, f"x must be float16 or bfloat16, got {x.dtype}")
+    xd = x.dtype
+    code = _DT_CODE.get(xd)
+    _require(code is not None, f"x must be float16 or bfloat16, got {xd}")
     _require(w_fp8.dtype in (torch.float8_e4m3fn, torch.uint8),
              f"w_fp8 must be float8_e4m3fn (or its uint8 bits), got {w_fp8.dtype}")
-    _require(w_fp8.dim() == 2 and scales.dim() == 2, "w_fp8 and scales must be 2-D")
-    K, N = w_fp8.shape
-    _require(x.shape[-1] == K, f"x last dim {x.shape[-1]} != K={K}")
+    xs, wsh, ss = x.shape, w_fp8.shape, scales.shape
+    _require(len(wsh) == 2 and len(ss) == 2, "w_fp8 and scales must be 2-D")
+    K, N = wsh
+    _require(len(xs) >= 1 and xs[-1] == K, f"x last dim {tuple(xs)[-1:]} != K={K}")
     _require(scales.dtype == torch.float16, f"scales must be float16, got {scales.dtype}")
-    _require(scales.shape[1] == N and scales.shape[0] > 0 and K % scales.shape[0] == 0,
-             f"scales must be [K/B, {N}], got {tuple(scales.shape)}")
-    block = K // scales.shape[0]
+    _require(ss[1] == N and ss[0] > 0 and K % ss[0] == 0,
+             f"scales must be [K/B, {N}], got {tuple(ss)}")
+    block = K // ss[0]
     dev = _check_device(x, w_fp8, scales)
-    lead = x.shape[:-1]
-    x2 = x.reshape(-1, K).contiguous()
-    M = x2.shape[0]
-    y = torch.empty((M, N), dtype=x.dtype, device=dev)
-    if M == 0:
-        return y.reshape(*lead, N)
-    w8 = w_fp8.contiguous().view(torch.uint8)
-    sc = scales.contiguous()
-    lib = _lib.load()
-    ws = workspaces.get(lib.kbh_fp8w_workspace_bytes(M, N, K, block), dev)
-    st = lib.kbh_fp8w_gemm(x2.data_ptr(), w8.data_ptr(), sc.data_ptr(), y.data_ptr(),
-                           ws.data_ptr(), ws.numel(), M, N, K, block, _DT_CODE[x.dtype],
-                           _stream_ptr(dev))
-    _lib.check(st, "kbh_fp8w_gemm")
-    return y.reshape(*lead, N)
+    flat = len(xs) == 2
+    x2 = x.contiguous() if flat else x.reshape(-1, K).contiguous()
+    M = xs[0] if flat else x2.shape[0]
+    y = torch.empty((M, N), dtype=xd, device=dev)
+    if M > 0:
+        w8 = w_fp8.contiguous()             # 1-byte elements: the pointer is the same as uint8
+        sc = scales.contiguous()
+        st = _stream_ptr(dev)
+        lib = _lib.load()
+        ws = workspaces.get(lib.kbh_fp8w_workspace_bytes(M, N, K, block), dev, st)
+        _lib.check(lib.kbh_fp8w_gemm(x2.data_ptr(), w8.data_ptr(), sc.data_ptr(), y.data_ptr(),
+                                     ws.data_ptr(), ws.numel(), M, N, K, block, code, st),
+                   "kbh_fp8w_gemm")
+    return y if flat else y.reshape(*xs[:-1], N)
 
 
 _BYTE_DTYPES = (torch.uint8, torch.float8_e4m3fn)
-
-
-def _as_bytes(t: torch.Tensor) -> torch.Tensor:
-    return t.contiguous().view(torch.uint8)
+_SCALE_DTYPES = (torch.uint8,) + ((torch.float8_e8m0fnu,) if hasattr(torch, "float8_e8m0fnu") else ())
 
 
 def mxfp8_gemm(a: torch.Tensor, a_scale: torch.Tensor, b: torch.Tensor, b_scale: torch.Tensor,
@@ -216,24 +234,27 @@ def mxfp8_gemm(a: torch.Tensor, a_scale: torch.Tensor, b: torch.Tensor, b_scale:
     _require(out_dtype in _DT_CODE, f"out_dtype must be float16 or bfloat16, got {out_dtype}")
     _require(a.dtype in _BYTE_DTYPES and b.dtype in _BYTE_DTYPES,
              f"a and b must be float8_e4m3fn or uint8, got {a.dtype}/{b.dtype}")
-    sdt = (torch.uint8,) + ((torch.float8_e8m0fnu,) if hasattr(torch, "float8_e8m0fnu") else ())
-    _require(a_scale.dtype in sdt and b_scale.dtype in sdt, "scales must be e8m0 codes (uint8)")
-    _require(a.dim() == 2 and b.dim() == 2, "a and b must be 2-D")
-    M, K = a.shape
-    N = b.shape[0]
-    _require(b.shape[1] == K, f"b must be [N, {K}], got {tuple(b.shape)}")
+    _require(a_scale.dtype in _SCALE_DTYPES and b_scale.dtype in _SCALE_DTYPES,
+             "scales must be e8m0 codes (uint8)")
+    ash, bsh = a.shape, b.shape
+    _require(len(ash) == 2 and len(bsh) == 2, "a and b must be 2-D")
+    M, K = ash
+    N = bsh[0]
+    _require(bsh[1] == K, f"b must be [N, {K}], got {tuple(bsh)}")
     _require(K % 32 == 0 and a_scale.shape == (M, K // 32) and b_scale.shape == (N, K // 32),
              f"scales must be [M, K/32] and [N, K/32]")
     dev = _check_device(a, a_scale, b, b_scale)
     y = torch.empty((M, N), dtype=out_dtype, device=dev)
     if M == 0:
         return y
+    st = _stream_ptr(dev)
     lib = _lib.load()
-    ws = workspaces.get(lib.kbh_mxfp8_workspace_bytes(M, N, K), dev)
-    a8, b8, as8, bs8 = _as_bytes(a), _as_bytes(b), _as_bytes(a_scale), _as_bytes(b_scale)
+    ws = workspaces.get(lib.kbh_mxfp8_workspace_bytes(M, N, K), dev, st)
+    # 1-byte elements: contiguous tensors of any of the accepted dtypes are the byte arrays
+    a8, b8, as8, bs8 = a.contiguous(), b.contiguous(), a_scale.contiguous(), b_scale.contiguous()
     st = lib.kbh_mxfp8_gemm(a8.data_ptr(), as8.data_ptr(), b8.data_ptr(), bs8.data_ptr(),
                             y.data_ptr(), ws.data_ptr(), ws.numel(), M, N, K, _DT_CODE[out_dtype],
-                            _stream_ptr(dev))
+                            st)
     _lib.check(st, "kbh_mxfp8_gemm")
     return y
 
@@ -262,11 +283,12 @@ def moe_route_top2(router_logits: torch.Tensor, dtype: torch.dtype = torch.float
     topw = torch.empty((T, 2), dtype=dtype, device=dev)
     if T == 0:
         return topi, topw
+    st = _stream_ptr(dev)
     lib = _lib.load()
-    ws = scratches.get(lib.kbh_qmoe_workspace_bytes(T, 0, 0, E), dev)
+    ws = scratches.get(lib.kbh_qmoe_workspace_bytes(T, 0, 0, E), dev, st)
     st = lib.kbh_moe_route_top2(router_logits.contiguous().data_ptr(), _LOGIT_CODE[router_logits.dtype],
                                 topi.data_ptr(), topw.data_ptr(), ws.data_ptr(), ws.numel(), T, E,
-                                _DT_CODE[dtype], _stream_ptr(dev))
+                                _DT_CODE[dtype], st)
     _lib.check(st, "kbh_moe_route_top2")
     return topi, topw
 
@@ -291,12 +313,13 @@ def qmoe(x: torch.Tensor, qweight: torch.Tensor, scales: torch.Tensor,
     y = torch.empty((T, N), dtype=x.dtype, device=dev)
     if T == 0:
         return y
+    st = _stream_ptr(dev)
     lib = _lib.load()
-    ws = scratches.get(lib.kbh_qmoe_workspace_bytes(T, D, N, E), dev)
+    ws = scratches.get(lib.kbh_qmoe_workspace_bytes(T, D, N, E), dev, st)
     st = lib.kbh_qmoe(x.contiguous().data_ptr(), qweight.contiguous().data_ptr(),
                       scales.contiguous().data_ptr(), router_logits.contiguous().data_ptr(),
                       _LOGIT_CODE[router_logits.dtype], y.data_ptr(), ws.data_ptr(), ws.numel(),
-                      T, D, N, E, group, _DT_CODE[x.dtype], _stream_ptr(dev))
+                      T, D, N, E, group, _DT_CODE[x.dtype], st)
     _lib.check(st, "kbh_qmoe")
     return y
 
@@ -332,13 +355,14 @@ def qmoe_ffn(x, router_logits, gate_qweight, gate_scales, gate_zeros, up_qweight
     y = torch.empty((T, D), dtype=x.dtype, device=dev)
     if T == 0:
         return y
+    st = _stream_ptr(dev)
     lib = _lib.load()
-    ws = scratches.get(lib.kbh_qmoe_ffn_workspace_bytes(T, D, F, E), dev)
+    ws = scratches.get(lib.kbh_qmoe_ffn_workspace_bytes(T, D, F, E), dev, st)
     ts = [t_.contiguous() for t_ in ts]
     st = lib.kbh_qmoe_ffn(ts[0].data_ptr(), router_logits.contiguous().data_ptr(),
                           _LOGIT_CODE[router_logits.dtype], *[t_.data_ptr() for t_ in ts[1:]],
                           y.data_ptr(), ws.data_ptr(), ws.numel(), T, D, F, E, group,
-                          _DT_CODE[x.dtype], _stream_ptr(dev))
+                          _DT_CODE[x.dtype], st)
     _lib.check(st, "kbh_qmoe_ffn")
     return y
 
@@ -367,12 +391,13 @@ def silu_fp8_quant(y: torch.Tensor, group: int = 128, return_codes: bool = False
         codes = torch.empty((T, H), dtype=torch.uint8, device=dev)
         scales = torch.empty((T, H // group), dtype=torch.float32, device=dev)
     if T > 0 and H > 0:
+        st = _stream_ptr(dev)
         lib = _lib.load()
         yc = y.contiguous()
         st = lib.kbh_silu_fp8_quant(yc.data_ptr(), out.data_ptr(),
                                     codes.data_ptr() if return_codes else None,
                                     scales.data_ptr() if return_codes else None,
-                                    T, H, group, _DT_CODE[y.dtype], _stream_ptr(dev))
+                                    T, H, group, _DT_CODE[y.dtype], st)
         _lib.check(st, "kbh_silu_fp8_quant")
     if return_codes:
         return out, codes.view(torch.float8_e4m3fn), scales
@@ -392,12 +417,13 @@ def moe_route_topk(router_logits: torch.Tensor, topk: int, dtype: torch.dtype = 
     topw = torch.empty((T, topk), dtype=dtype, device=dev)
     if T == 0:
         return topi, topw
+    st = _stream_ptr(dev)
     lib = _lib.load()
-    ws = scratches.get(lib.kbh_moe_workspace_bytes(T, 0, 0, E, topk), dev)
+    ws = scratches.get(lib.kbh_moe_workspace_bytes(T, 0, 0, E, topk), dev, st)
     st = lib.kbh_moe_route_topk(router_logits.contiguous().data_ptr(),
                                 _LOGIT_CODE[router_logits.dtype], topi.data_ptr(), topw.data_ptr(),
                                 ws.data_ptr(), ws.numel(), T, E, topk, _DT_CODE[dtype],
-                                _stream_ptr(dev))
+                                st)
     _lib.check(st, "kbh_moe_route_topk")
     return topi, topw
 
@@ -421,12 +447,13 @@ def moe(x: torch.Tensor, w: torch.Tensor, router_logits: torch.Tensor, topk: int
     y = torch.empty((T, H), dtype=x.dtype, device=dev)
     if T == 0:
         return y
+    st = _stream_ptr(dev)
     lib = _lib.load()
-    ws = scratches.get(lib.kbh_moe_workspace_bytes(T, D, H, E, topk), dev)
+    ws = scratches.get(lib.kbh_moe_workspace_bytes(T, D, H, E, topk), dev, st)
     xc, wc = x.contiguous(), w.contiguous()
     st = lib.kbh_moe(xc.data_ptr(), wc.data_ptr(), router_logits.contiguous().data_ptr(),
                      _LOGIT_CODE[router_logits.dtype], y.data_ptr(), ws.data_ptr(), ws.numel(),
-                     T, D, H, E, topk, _DT_CODE[x.dtype], _stream_ptr(dev))
+                     T, D, H, E, topk, _DT_CODE[x.dtype], st)
     _lib.check(st, "kbh_moe")
     return y
 
@@ -462,12 +489,13 @@ def lora_qgemm(x: torch.Tensor, qweight: torch.Tensor, scales: torch.Tensor, A: 
     y = torch.empty((T, N), dtype=x.dtype, device=dev)
     if T == 0:
         return y
+    st = _stream_ptr(dev)
     lib = _lib.load()
-    ws = workspaces.get(lib.kbh_lora_qgemm_workspace_bytes(T, D, N, r), dev)
+    ws = workspaces.get(lib.kbh_lora_qgemm_workspace_bytes(T, D, N, r), dev, st)
     ts = [t_.contiguous() for t_ in (x, qweight, scales, A, B)]
     ids = lora_ids.to(torch.int64).contiguous()
     st = lib.kbh_lora_qgemm(*[t_.data_ptr() for t_ in ts], ids.data_ptr(), y.data_ptr(),
                             ws.data_ptr(), ws.numel(), T, D, N, r, L, group, _DT_CODE[x.dtype],
-                            _stream_ptr(dev))
+                            st)
     _lib.check(st, "kbh_lora_qgemm")
     return y

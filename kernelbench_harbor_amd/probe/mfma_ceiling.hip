@@ -2,7 +2,8 @@
 // rate gfx950 sustains for fp16 32x32x16 MFMAs, with operands either held in registers (little
 // switching) or read as fresh random fragments from LDS for every MFMA (the switching of a real
 // GEMM), and the LDS read bandwidth. bench.py --mfma-ceiling runs them; the rate with random
-// operands is the practical ceiling the W4A16 GEMM's MFMA utilisation is compared with.
+// operands is the practical ceiling the W4A16 GEMM's MFMA utilisation is compared with. A plain
+// HBM read stream gives the practical bandwidth of a read of a given size.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -85,10 +86,31 @@ __global__ __launch_bounds__(256) void lds_read_b128(uint32_t* __restrict__ out,
   }
   if ((acc[0] ^ acc[1] ^ acc[2] ^ acc[3]) == 0x12345678u) out[blockIdx.x] = 1u;
 }
+
+// HBM read stream: thread t of workgroup b reads the 16-byte chunks (i * blocks + b) * 256 + t,
+// i < iters, of src (blocks * 256 * iters * 16 bytes), eight loads in flight per lane, and folds
+// them into one word so that no load is dead.
+__global__ __launch_bounds__(256) void hbm_read(const u32x4* __restrict__ src,
+                                                uint32_t* __restrict__ out, int iters) {
+  const size_t stride = (size_t)gridDim.x * 256;
+  const u32x4* p = src + (size_t)blockIdx.x * 256 + threadIdx.x;
+  u32x4 acc = {0u, 0u, 0u, 0u};
+  int i = 0;
+  for (; i + 8 <= iters; i += 8) {
+    u32x4 v[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) v[j] = __builtin_nontemporal_load(p + (size_t)(i + j) * stride);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) acc ^= v[j];
+  }
+  for (; i < iters; ++i) acc ^= p[(size_t)i * stride];
+  if ((acc[0] ^ acc[1] ^ acc[2] ^ acc[3]) == 0x12345678u) out[blockIdx.x] = 1u;
+}
 }  // namespace
 
-// which: 0 fixed-operand MFMAs, 1 random-operand MFMAs, 2 LDS reads. src: >= 1 MiB of random
-// finite fp16 data; out: >= blocks * 256 floats.
+// which: 0 fixed-operand MFMAs, 1 random-operand MFMAs, 2 LDS reads, 3 HBM read of
+// blocks * 256 * iters * 16 bytes of src. src: >= 1 MiB of random finite fp16 data (which < 3);
+// out: >= blocks * 256 floats.
 extern "C" int kbh_probe_run(int which, const void* src, void* out, int blocks, int iters,
                              void* stream) {
   hipStream_t st = (hipStream_t)stream;
@@ -100,6 +122,9 @@ extern "C" int kbh_probe_run(int which, const void* src, void* out, int blocks, 
                        (float*)out, iters);
   else if (which == 2)
     hipLaunchKernelGGL(lds_read_b128, dim3(blocks), dim3(256), 0, st, (uint32_t*)out, iters);
+  else if (which == 3)
+    hipLaunchKernelGGL(hbm_read, dim3(blocks), dim3(256), 0, st, (const u32x4*)src,
+                       (uint32_t*)out, iters);
   else
     return 2;
   return hipGetLastError() == hipSuccess ? 0 : 6;
