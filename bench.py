@@ -421,9 +421,66 @@ def mfma_ceiling(torch, dev, probe_path, blocks=256):
     for which, key in ((0, "mfma_f16_fixed_operands_tflops"), (1, "mfma_f16_random_operands_tflops")):
         t = run(which, 4000)
         res[key] = round(blocks * 4 * 8 * 4000 * 32768 / t / 1e12, 1)
+    # 8-bit operands: finite e4m3 codes (the mask clears the NaN pattern), unit block scales
+    src.copy_(src & 0x3B3B3B3B)
+    t = run(4, 4000)
+    res["mfma_i8_random_operands_tops"] = round(blocks * 4 * 8 * 4000 * 65536 / t / 1e12, 1)
+    t = run(5, 2000)
+    res["mfma_f8_scaled_random_operands_tflops"] = round(blocks * 4 * 8 * 2000 * 131072 / t / 1e12, 1)
     t = run(2, 4000)
     res["lds_read_gbps_per_cu"] = round(256 * 16 * 16 * 4000 / t / 1e9, 1)
-    res["peak_datasheet_tflops"] = PEAK["f16"] / 1e12
+    res["hbm_read"] = hbm_read_ceiling(torch, dev, lib)
+    res["peak_datasheet_tflops"] = {"f16": PEAK["f16"] / 1e12, "i8": PEAK["i8"] / 1e12,
+                                    "f8": PEAK["f8"] / 1e12}
+    return res
+
+
+def hbm_read_ceiling(torch, dev, lib):
+    """GB/s of the plain HBM read stream (probe kernel 3: 16-byte loads, eight in flight per
+    lane) for reads of the W4A16 decode's weight bytes and larger, over a grid-size sweep: each
+    timed call reads a fresh window of a 1 GiB buffer (well past the Infinity Cache), 20 calls
+    per graph replay, median of 5 replays. The best rate at 29.4 MB is the practical ceiling of
+    a decode-sized call."""
+    buf = torch.empty(1 << 30, dtype=torch.uint8, device=dev)
+    buf.random_(0, 256)
+    out = torch.zeros(1 << 16, dtype=torch.int32, device=dev)
+    base = buf.data_ptr()
+    res = []
+    for target in (K_DIM * N_DIM // 2, 4 * K_DIM * N_DIM // 2, 16 * K_DIM * N_DIM // 2):
+        best = None
+        for blocks in (256, 512, 1024, 2048):
+            iters = max(1, round(target / (blocks * 256 * 16)))
+            nbytes = blocks * 256 * iters * 16
+            nwin = (1 << 30) // nbytes
+            s = torch.cuda.Stream()
+            s.wait_stream(torch.cuda.current_stream())
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.stream(s):
+                for i in range(3):
+                    assert lib.kbh_probe_run(3, base + (i % nwin) * nbytes, out.data_ptr(), blocks,
+                                             iters, s.cuda_stream) == 0
+                torch.cuda.synchronize()
+                with torch.cuda.graph(g, stream=s):
+                    for i in range(20):
+                        lib.kbh_probe_run(3, base + (i % nwin) * nbytes, out.data_ptr(), blocks,
+                                          iters, torch.cuda.current_stream().cuda_stream)
+            ts = []
+            for _ in range(5):
+                a = torch.cuda.Event(enable_timing=True)
+                b = torch.cuda.Event(enable_timing=True)
+                a.record()
+                g.replay()
+                b.record()
+                b.synchronize()
+                ts.append(a.elapsed_time(b) * 1e-3 / 20)
+            t = sorted(ts)[2]
+            if best is None or nbytes / t > best["gbps"] * 1e9:
+                best = {"bytes": nbytes, "workgroups": blocks, "us": round(t * 1e6, 2),
+                        "gbps": round(nbytes / t / 1e9, 1)}
+        best["frac_of_8tbs"] = round(best["gbps"] / 8000, 3)
+        res.append(best)
+        print(f"[calib] HBM read {best}", file=sys.stderr, flush=True)
+    del buf
     return res
 
 
@@ -485,8 +542,9 @@ def main():
                          "WRITE_SIZE against a kernel of known traffic) and exit")
     ap.add_argument("--mfma-ceiling", action="store_true",
                     help="only run the calibration kernels (kernelbench_harbor_amd/probe): the "
-                         "fp16 MFMA rate with fixed and with random operands, and the LDS read "
-                         "bandwidth, then print one JSON line")
+                         "fp16 MFMA rate with fixed and with random operands, the int8 and "
+                         "block-scaled fp8 rates with random operands, the LDS read bandwidth "
+                         "and the HBM read-stream rate, then print one JSON line")
     ap.add_argument("--only", type=str, default="",
                     help="run only the named record ('w4a16 M=<M>' or a configuration name) "
                          "--steps times after --warmup calls, eagerly, and print its call count "

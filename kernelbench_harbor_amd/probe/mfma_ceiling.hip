@@ -67,6 +67,65 @@ __global__ __launch_bounds__(256) void mfma_random_operands(const u32x4* __restr
   out[blockIdx.x * 256 + t] = sum;
 }
 
+// The same random-operand loop for int8 (32x32x32, 16 bytes per lane per operand) and for the
+// block-scaled fp8 MFMA (32x32x64 e4m3, 32 bytes per lane per operand, unit e8m0 scales).
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+typedef int i32x8 __attribute__((ext_vector_type(8)));
+typedef int i32x16 __attribute__((ext_vector_type(16)));
+template <bool FP8>
+__global__ __launch_bounds__(256) void mfma_random_operands_8bit(const u32x4* __restrict__ src,
+                                                                 float* __restrict__ out,
+                                                                 int iters) {
+  __shared__ __attribute__((aligned(16))) uint8_t s[65536];
+  const int t = threadIdx.x;
+  for (int i = t; i < 65536 / 16; i += 256)
+    reinterpret_cast<u32x4*>(s)[i] = src[(blockIdx.x * 4096 + i) & 65535];
+  __syncthreads();
+  const int lane = t & 63, wave = t >> 6;
+  f32x16 c[8];
+  i32x16 ci[8];
+  for (int i = 0; i < 8; ++i)
+    for (int e = 0; e < 16; ++e) c[i][e] = 0.f, ci[i][e] = 0;
+  constexpr int NF = FP8 ? 2 : 1;  // 16-byte chunks per lane per operand
+  for (int it = 0; it < iters; ++it) {
+    u32x4 a[2][NF], b[4][NF];
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int h = 0; h < NF; ++h)
+        a[j][h] = *reinterpret_cast<const u32x4*>(
+            s + (((it * 12 + j * NF + h) * 4 + wave) * 1024 + lane * 16) % 32768);
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int h = 0; h < NF; ++h)
+        b[j][h] = *reinterpret_cast<const u32x4*>(
+            s + 32768 + (((it * 12 + 4 + j * NF + h) * 4 + wave) * 1024 + lane * 16) % 32768);
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        if constexpr (FP8) {
+          const i32x8 av = {(int)a[i][0][0], (int)a[i][0][1], (int)a[i][0][2], (int)a[i][0][3],
+                            (int)a[i][NF - 1][0], (int)a[i][NF - 1][1], (int)a[i][NF - 1][2],
+                            (int)a[i][NF - 1][3]};
+          const i32x8 bv = {(int)b[j][0][0], (int)b[j][0][1], (int)b[j][0][2], (int)b[j][0][3],
+                            (int)b[j][NF - 1][0], (int)b[j][NF - 1][1], (int)b[j][NF - 1][2],
+                            (int)b[j][NF - 1][3]};
+          c[i * 4 + j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(
+              av, bv, c[i * 4 + j], 0, 0, 0, 127, 0, 127);
+        } else {
+          ci[i * 4 + j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(
+              __builtin_bit_cast(i32x4, a[i][0]), __builtin_bit_cast(i32x4, b[j][0]),
+              ci[i * 4 + j], 0, 0, 0);
+        }
+      }
+  }
+  float sum = 0.f;
+  for (int i = 0; i < 8; ++i) sum += c[i][0] + c[i][15] + (float)(ci[i][0] ^ ci[i][15]);
+  out[blockIdx.x * 256 + t] = sum;
+}
+
 // ds_read_b128 throughput: every lane reads 16 B per read, consecutive lanes consecutive 16 B
 // (a compiler memory barrier per round of 16 reads keeps the reads inside the loop).
 __global__ __launch_bounds__(256) void lds_read_b128(uint32_t* __restrict__ out, int iters) {
@@ -109,7 +168,8 @@ __global__ __launch_bounds__(256) void hbm_read(const u32x4* __restrict__ src,
 }  // namespace
 
 // which: 0 fixed-operand MFMAs, 1 random-operand MFMAs, 2 LDS reads, 3 HBM read of
-// blocks * 256 * iters * 16 bytes of src. src: >= 1 MiB of random finite fp16 data (which < 3);
+// blocks * 256 * iters * 16 bytes of src, 4 random-operand int8 MFMAs, 5 random-operand
+// block-scaled fp8 MFMAs. src: >= 1 MiB of random finite fp16 data (which < 3);
 // out: >= blocks * 256 floats.
 extern "C" int kbh_probe_run(int which, const void* src, void* out, int blocks, int iters,
                              void* stream) {
@@ -122,6 +182,12 @@ extern "C" int kbh_probe_run(int which, const void* src, void* out, int blocks, 
                        (float*)out, iters);
   else if (which == 2)
     hipLaunchKernelGGL(lds_read_b128, dim3(blocks), dim3(256), 0, st, (uint32_t*)out, iters);
+  else if (which == 4)
+    hipLaunchKernelGGL(mfma_random_operands_8bit<false>, dim3(blocks), dim3(256), 0, st,
+                       (const u32x4*)src, (float*)out, iters);
+  else if (which == 5)
+    hipLaunchKernelGGL(mfma_random_operands_8bit<true>, dim3(blocks), dim3(256), 0, st,
+                       (const u32x4*)src, (float*)out, iters);
   else if (which == 3)
     hipLaunchKernelGGL(hbm_read, dim3(blocks), dim3(256), 0, st, (const u32x4*)src,
                        (uint32_t*)out, iters);
