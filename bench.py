@@ -53,14 +53,14 @@ def w4a16_bytes(M, K=K_DIM, N=N_DIM, G=GROUP):
 # 256 MiB device copy reads as 131084 KiB) plus WRITE_SIZE (exact on the same copy), summed over
 # every kbh:: kernel of the call. Table and commands: profiles/hbm_traffic_all_records.md.
 PMC_TRAFFIC = {
-    "w4a16 M=1": 32_157_994, "w4a16 M=4": 34_446_097, "w4a16 M=16": 43_588_085,
-    "w4a16 M=64": 94_334_871, "w4a16 M=256": 167_619_648, "w4a16 M=1024": 303_572_131,
-    "w4a16 M=2048": 466_521_290, "w8a8 M=16": 68_180_693, "w8a8 M=512": 274_725_693,
-    "mxfp8 M=128": 94_943_156, "mxfp8 M=2048": 291_247_371,
-    "fp8w (reference op) M=16 b128": 70_947_288,
-    "qmoe_ffn T=512 D=4096 F=14336 E=8 top2": 1_245_009_775,
-    "silu_fp8 (reference op) T=512 H=14336 g128": 60_958_806,
-    "qmoe (reference op) T=256 D=4096 N=14336 E=8": 534_838_367,
+    "w4a16 M=1": 32_167_648, "w4a16 M=4": 34_454_252, "w4a16 M=16": 43_596_898,
+    "w4a16 M=64": 64_031_899, "w4a16 M=256": 108_180_696, "w4a16 M=1024": 240_722_352,
+    "w4a16 M=2048": 340_853_600, "w8a8 M=16": 68_182_320, "w8a8 M=512": 210_728_956,
+    "mxfp8 M=128": 94_936_720, "mxfp8 M=2048": 290_080_130,
+    "fp8w (reference op) M=16 b128": 70_943_466,
+    "qmoe_ffn T=512 D=4096 F=14336 E=8 top2": 1_229_346_633,
+    "silu_fp8 (reference op) T=512 H=14336 g128": 61_112_077,
+    "qmoe (reference op) T=256 D=4096 N=14336 E=8": 534_829_326,
 }
 
 
