@@ -1,9 +1,10 @@
-"""The reference modules' forward op sequences as torch CPU code — TEST AND MEASUREMENT
-INFRASTRUCTURE ONLY (bench.py's cpu_baseline leg times them; nothing in the product imports
-this module).
+"""The reference modules' forward op sequences as torch code — TEST AND MEASUREMENT
+INFRASTRUCTURE ONLY (bench.py's cpu_baseline leg times them on the host; the grader-protocol GPU
+test computes its ground truth with them on the device, as the reference grader does; nothing in
+the product imports this module).
 
 Each function repeats the torch op sequence of one reference ``Model.forward`` (cited per
-function) on CPU tensors, in the dtype of its inputs: called on the task's fp16/bf16 inputs it
+function) on tensors of any device, in the dtype of its inputs: called on the task's fp16/bf16 inputs it
 is the reference's native path, called on fp32-upcast floating inputs (integer tensors left
 alone, common/kb_verifier.py:195-196) it is the grader's fp32 ground truth. The two
 BASELINE-only configurations without a reference module (MXFP8, the SiLU FFN) are written in
