@@ -244,10 +244,10 @@ void dispatch_decode(const DecodePlan& p, const void* x, const int32_t* qw, cons
 // Large-M kernels
 // ======================================================================================
 // Above kWideMinM rows the wide-tile kernel (tiled_wide.h) takes over from the split-K decode
-// kernel: up to 64 rows, 64 x 256 tiles with two workgroups per CU; up to 128 rows, 128 x 256
-// tiles with one workgroup per CU (128 x 128 tiles, two per CU, when N is not a multiple of
-// 256); 256 x 256 tiles above. The 256-column tiles run with a
-// 4-slab prefetch ring. The older 256 x 128 LDS-staged kernel remains for shapes the wide kernel
+// kernel: up to 64 rows, 64 x 256 tiles; up to 384 rows, 128 x 256 tiles with one workgroup per
+// CU (128 x 128 tiles, two per CU, up to 128 rows when N is not a multiple of 256); 256 x 256
+// tiles above unless the planner's estimate prefers 128-row tiles. The 256-column tiles run
+// with a 4-slab prefetch ring. The older 256 x 128 LDS-staged kernel remains for shapes the wide kernel
 // does not cover.
 constexpr int kWideMinM = 33;
 constexpr int kTiledMinM = 128;
