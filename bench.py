@@ -14,8 +14,8 @@ Inputs are synthetic (seeded, BASELINE distributions) and resident in HBM before
 configuration rotates over enough input copies (> 2x the 256 MB Infinity Cache) that every call
 streams its weights from HBM. Per configuration two timings are reported: the median of 100
 event-bracketed single calls after 25 warm-up calls (`us_median`, the reference grader's
-protocol, common/kb_verifier.py:132-143, through harness.bench; it includes ~4-5 us of event
-overhead per call) and the mean of a batch of back-to-back calls replayed from a HIP graph
+protocol, common/kb_verifier.py:132-143, through harness.bench; it includes the host's work
+per call, the Python wrapper and the HIP launches, ~10 us at small M) and the mean of a batch of back-to-back calls replayed from a HIP graph
 (`us_batched`, close to the kernel duration); roofline fractions use the batched time.
 
 Prints ONE JSON line. The CPU baseline times the reference modules' own torch op sequences
@@ -290,11 +290,16 @@ def run_grid(torch, dev, inputs, ops, families=None):
 
 
 # ---- CPU baseline ----------------------------------------------------------------------------
-def cpu_time(fn, ins, max_calls=3, budget_s=1.0):
-    """Host seconds per call of fn(*ins): one warm-up call (the first call also pays for faulting
-    in its fresh working memory), then timed calls until their sum passes budget_s or max_calls
-    are done; returns the median and the number of timed calls."""
+def cpu_time(fn, ins, max_calls=5, budget_s=9.0, warmups=2):
+    """Host seconds per call of fn(*ins): `warmups` warm-up calls (one when the first takes over
+    2 s; the first call also pays for faulting in its fresh working memory), then timed calls
+    until their sum passes budget_s or max_calls are done; returns the median and the number of
+    timed calls."""
+    t0 = time.perf_counter()
     fn(*ins)
+    if time.perf_counter() - t0 < 2.0:
+        for _ in range(warmups - 1):
+            fn(*ins)
     ts = []
     while len(ts) < max_calls and sum(ts) < budget_s:
         t0 = time.perf_counter()
@@ -345,7 +350,7 @@ def cpu_reference(jobs, native_budget_s=1.0):
                 f"predicted {predicted:.0f} s per call at this host's measured fp16 GEMM rate "
                 f"({f16_rate / 1e9:.2f} GFLOP/s)")})
         else:
-            t, n = cpu_time(fn, ins)
+            t, n = cpu_time(fn, ins, max_calls=3, budget_s=native_budget_s, warmups=1)
             r.update({"native_s": round(t, 4), "native_calls": n,
                       "native_tflops": round(fl / t / 1e12, 4) if fl else None})
         res[name] = r
@@ -703,8 +708,8 @@ def main():
             "sample": ("the reference Model.forward op sequence of the W4A16 task "
                        "(oracle/torch_ref.py, reference.py:10-17) in torch on the host, on the "
                        "grader's fp32-upcast inputs (kb_verifier.py:195-196), at each sweep M "
-                       f"{ms} one warm-up call then the median of up to 3 timed calls (fewer "
-                       "once they pass 1 s); value = the sweep's FLOPs / the summed seconds. "
+                       f"{ms} two warm-up calls then the median of 5 timed calls (fewer "
+                       "once they pass 9 s); value = the sweep's FLOPs / the summed seconds. "
                        "The native fp16 "
                        "path is timed where this host's fp16 GEMM rate allows (per-record 'cpu' "
                        "entries; every sweep point and configuration carries one)"),
