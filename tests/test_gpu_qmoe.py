@@ -138,6 +138,37 @@ def test_qmoe_ffn_native_rounding(dev, T, D, F, E, dtype):
     assert (y == want).mean() >= 0.9, (y == want).mean()
 
 
+def _routed_logits(counts, seed):
+    """fp32 logits whose top-2 experts give each expert exactly counts[e] of the 2T slots:
+    token t picks experts L[t] and L[t + T] of the sorted slot list L (distinct, since no count
+    reaches T), with random distinct margins."""
+    L = np.repeat(np.arange(len(counts)), counts)
+    T = len(L) // 2
+    rng = np.random.default_rng(seed)
+    lg = rng.normal(size=(T, len(counts))).astype(np.float32) - 4.0
+    first, second = L[:T], L[T:]
+    lg[np.arange(T), first] = 3.0 + rng.uniform(0, 1, T)
+    lg[np.arange(T), second] = 1.0 + rng.uniform(0, 1, T)
+    return torch.from_numpy(lg)
+
+
+@pytest.mark.parametrize("F,dtype", [(512, torch.float16), (512, torch.bfloat16),
+                                     (256, torch.float16)])
+def test_qmoe_ffn_tile_overflow_rows(dev, F, dtype):
+    """Experts whose rows overflow a 128-row expert tile by a few (140, 144 and 145 routed
+    rows: a second tile of 12, 16 and 17 rows) beside one that fits (123), with the down
+    projection split over K (F=512) and unsplit (F=256)."""
+    counts = [140, 144, 145, 123]
+    T, D, E = sum(counts) // 2, 256, len(counts)
+    ins = inputs.qmoe_ffn(T, D, F, E, dtype=dtype, seed=F + 7)
+    ins[1] = _routed_logits(counts, F)
+    topi, _ = oq.route_top2(ins[1].numpy())
+    assert np.bincount(topi.ravel(), minlength=E).tolist() == counts
+    y = ops.qmoe_ffn(*[t.to(dev) for t in ins])
+    cmp = compare(y, oq.ffn_forward(*_np(ins)))
+    assert cmp.ok, cmp
+
+
 def test_qmoe_ffn_full_size_all_experts(dev):
     """BASELINE configuration 4 (T=512, D=4096, F=14336, E=8): the whole layer runs on the GPU;
     the oracle checks every token (so all eight experts' gate, up and down matrices) on two
