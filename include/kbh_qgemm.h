@@ -64,8 +64,10 @@ int kbh_last_hip_error(void);
  * stream (results are identical from call to call). Calls that share a workspace must be
  * ordered (same stream); concurrent calls on one workspace race.
  * scratch: >= kbh_w4a16_scratch_bytes(M, N, K, group) bytes (may be 0, then NULL is accepted)
- * of device memory with no content requirement (split-K partial sums of the large-M kernel);
- * it must not overlap the workspace, and calls that share it must be ordered like workspace.
+ * of device memory with no content requirement (split-K partial sums of the large-M kernel,
+ * never more than 64 MiB); calls that share it must be ordered like workspace. A call uses
+ * either the workspace (M <= 32) or the scratch (M > 32), never both, so one buffer of the
+ * larger size may be passed as both.
  */
 size_t kbh_w4a16_workspace_bytes(int M, int N, int K, int group);
 size_t kbh_w4a16_scratch_bytes(int M, int N, int K, int group);
