@@ -38,8 +38,8 @@ CASES = [
     (513, 4096, 256, 128, torch.float16, "reference"),
     # K not a multiple of 64 -> split-K path even for large M
     (96, 1056, 256, 32, torch.float16, "baseline"),
-    # wide-tile kernel: 128x128 tiles (33 <= M <= 128), 256x256 tiles (M > 128, N % 256 == 0),
-    # every group size, split-K and not, ragged M
+    # wide-tile kernel: 128x128 tiles (33 <= M <= 128, N % 256 != 0), 128x256 tiles
+    # (64 < M <= 384), 256x256 tiles (M > 384), every group size, split-K and not, ragged M
     (33, 2048, 256, 64, torch.float16, "baseline"),
     (128, 4096, 384, 256, torch.bfloat16, "reference"),
     (129, 2048, 512, 32, torch.float16, "reference"),
