@@ -81,7 +81,7 @@ int kbh_w4a16_gemm(const void* x, const int32_t* qweight, const void* scales, co
  * in a fixed array inside the library, KBH_W4A16_NOALLOC_SCRATCH_BYTES per GPU, held from the
  * first call on that GPU until the process ends. The wide-tile kernel (M > 32) plans its K
  * splits within that size for every shape; the decode kernel (M <= 32) can need more for very
- * large N x K (e.g. M=24, N=12288, K=65536: 72 MiB of K-split partial sums), and such calls
+ * large N x K (e.g. M=24, N=12288, K=65536, group 64: 72 MiB of K-split partial sums), and such calls
  * return KBH_ERR_SCRATCH_LIMIT without launching. The array needs no
  * particular content. All calls on one GPU share it: calls that may overlap in time on the same
  * GPU (different streams, or host threads) race and must be ordered by the caller. Runs on the

@@ -195,22 +195,70 @@ struct DecodePlan {
   int nw, spw, spg, waves, ntiles, splits, mblocks;
 };
 
-// Chooses column width (NW), K steps per wave (SPW) and waves per workgroup so that the K steps
-// divide evenly and the grid is close to one workgroup per CU (256).
+// The (NW, SPW, SPG) instantiations of w4a16_decode_kernel; plan_decode picks only from these.
+// NW = 2 takes at most two quantization groups per wave (SPW / SPG <= 2): more groups' constants
+// on top of 256 columns' accumulators spill. SPW = 8 exists only with NW = 2 (NW = 1 was measured
+// slower with it on every shape swept).
+#define KBH_DECODE_VARIANTS(X)                                                                   \
+  X(2, 8, 8) X(2, 8, 4) X(2, 4, 4) X(2, 4, 2) X(2, 2, 2) X(2, 2, 1) X(2, 1, 1) X(1, 4, 4)         \
+  X(1, 4, 2) X(1, 4, 1) X(1, 2, 2) X(1, 2, 1) X(1, 1, 1)
+
+bool decode_variant_built(int nw, int spw, int spg) {
+#define KBH_DEC_IS(NW_, SPW_, SPG_) if (nw == NW_ && spw == SPW_ && spg == SPG_) return true;
+  KBH_DECODE_VARIANTS(KBH_DEC_IS)
+#undef KBH_DEC_IS
+  return false;
+}
+
+// Estimated duration (µs, up to a constant) of a decode launch plus its split-K sum. Every load
+// of a workgroup is in flight at once, so a CU's time is set by the weight bytes of the
+// workgroups it runs one after another (KB = 2 per K step per 128 columns) plus a fixed cost per
+// workgroup (halved when two fit on a CU: NW = 1 needs half the LDS), and fewer waves issue
+// those bytes more slowly; the split-K slices add a write and a read of splits x M x N fp32.
+// The constants are a least-squares fit to a sweep of every (NW, SPW, waves) plan on MI355X
+// over the shapes K x N = 4096 x 14336, 14336 x 4096, 8192 x 28672, 28672 x 8192,
+// 3584 x 18944, 18944 x 3584, 8192 x 29568 and 29568 x 8192 at M = 1 and 16 (group 128): the
+// plan it picks is within 2% of the sweep's fastest NW = 2 plan on all 16, where the former
+// "grid closest to one workgroup per CU" rule lost up to 28%.
+float decode_cost(int M, int N, int nw, int spw, int waves, int splits, int grid) {
+  const float kb = 2.0f * spw * waves * nw;
+  const float slowdown = 1.0f + 0.53f * (8 - waves) / 8.0f;
+  const int per_cu = (grid + 255) / 256;
+  float t = per_cu * ((nw == 1 ? 0.9f : 1.8f) + kb * slowdown / 23.3f);
+  if (splits > 1) t += (float)splits * M * N * 8.0f / 1024.0f / 2540.0f;
+  return t;
+}
+
+// Chooses column width (NW: 128*NW columns per workgroup), K steps per wave (SPW) and waves per
+// workgroup (the K steps divide evenly) by decode_cost. NW = 2 whenever N allows it (NW = 1 plans
+// that the cost prefers there were measured slower on most shapes: half-width rows per load),
+// except with 32-row groups, where NW = 2 holds at most SPW = 2 and NW = 1 with SPW = 4
+// measured 4-11% faster.
 bool plan_decode(int M, int N, int K, int group_steps_, DecodePlan* p) {
   const int nsteps = K / 32;
-  p->spw = (nsteps % 4 == 0) ? 4 : (nsteps % 2 == 0 ? 2 : 1);
-  // Wave ranges start at multiples of SPW steps, so they stay inside one group when the group
-  // spans a multiple of SPW steps; otherwise the group (1 or 2 steps) divides SPW.
-  const int gsteps = group_steps_;
-  p->spg = (gsteps % p->spw == 0) ? p->spw : gsteps;
-  // 256 columns per wave, except with four groups per wave (32-row groups): their constants on
-  // top of 256 columns' accumulators would spill.
-  p->nw = (N % 256 == 0 && 2 * p->spg >= p->spw) ? 2 : 1;
-  p->ntiles = N / (128 * p->nw);
-  p->mblocks = (M + 15) / 16;
-  const int units = nsteps / p->spw;  // wave-sized K units per column tile
-  p->waves = splitk_pick_waves(units, p->ntiles * p->mblocks, &p->splits);
+  const int gsteps = group_steps_;  // 1, 2, 4 or 8 (group 32..256); divides nsteps
+  const int nw = (N % 256 == 0 && gsteps > 1) ? 2 : 1;
+  const int ntiles = N / (128 * nw);
+  const int mblocks = (M + 15) / 16;
+  float best = 0.0f;
+  p->waves = 0;
+  for (int spw = 8; spw >= 1; spw >>= 1) {
+    if (nsteps % spw != 0) continue;
+    // Wave ranges start at multiples of SPW steps, so they stay inside one group when the group
+    // spans a multiple of SPW steps; otherwise the group (1, 2 or 4 steps) divides SPW.
+    const int spg = (gsteps % spw == 0) ? spw : gsteps;
+    if (!decode_variant_built(nw, spw, spg)) continue;
+    const int units = nsteps / spw;
+    for (int w = kSplitKMaxWaves; w >= 1; --w) {
+      if (units % w != 0) continue;
+      const int splits = units / w;
+      const float c = decode_cost(M, N, nw, spw, w, splits, ntiles * splits * mblocks);
+      if (p->waves == 0 || c < best) {
+        best = c;
+        *p = DecodePlan{nw, spw, spg, w, ntiles, splits, mblocks};
+      }
+    }
+  }
   return p->waves > 0;
 }
 
@@ -234,9 +282,7 @@ void dispatch_decode(const DecodePlan& p, const void* x, const int32_t* qw, cons
 #define KBH_DEC(NW_, SPW_, SPG_)                                                                 \
   if (p.nw == NW_ && p.spw == SPW_ && p.spg == SPG_)                                             \
     return launch_decode<NW_, SPW_, SPG_, BF16>(p, x, qw, s, z, y, acc, M, N, K, group, st);
-  KBH_DEC(2, 4, 4) KBH_DEC(2, 4, 2) KBH_DEC(2, 2, 2) KBH_DEC(2, 2, 1)
-  KBH_DEC(2, 1, 1) KBH_DEC(1, 4, 4) KBH_DEC(1, 4, 2) KBH_DEC(1, 4, 1) KBH_DEC(1, 2, 2)
-  KBH_DEC(1, 2, 1) KBH_DEC(1, 1, 1)
+  KBH_DECODE_VARIANTS(KBH_DEC)
 #undef KBH_DEC
 }
 

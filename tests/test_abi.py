@@ -58,7 +58,7 @@ def test_host_checks_run_without_gpu():
     # before any HIP call
     assert lib.kbh_w4a16_gemm_noalloc(None, p, p, p, p, 16, 4096, 4096, 128, 0, None) == _lib.KBH_ERR_NULL
     assert lib.kbh_w4a16_gemm_noalloc(p, p, p, p, p, 16, 4096, 4100, 128, 0, None) == _lib.KBH_ERR_SHAPE
-    assert lib.kbh_w4a16_gemm_noalloc(p, p, p, p, p, 24, 12288, 65536, 128, 0, None) == _lib.KBH_ERR_SCRATCH_LIMIT
+    assert lib.kbh_w4a16_gemm_noalloc(p, p, p, p, p, 24, 12288, 65536, 64, 0, None) == _lib.KBH_ERR_SCRATCH_LIMIT
     assert b"fixed scratch" in lib.kbh_status_string(_lib.KBH_ERR_SCRATCH_LIMIT)
     assert lib.kbh_w4a16_scratch_bytes(2048, 4096, 14336, 128) <= _lib.W4A16_NOALLOC_SCRATCH_BYTES
     # the wide-tile planner keeps its K-split partial sums within the fixed scratch for any M

@@ -42,13 +42,13 @@ def test_noalloc_matches_workspace_entry_point(dev, dtype):
 
 def test_noalloc_rejects_oversize_before_launch(dev):
     lib = _lib.load()
-    M, K, N = 24, 65536, 12288           # decode kernel: K splits of 24 x 12288 fp32 = 72 MiB
-    assert lib.kbh_w4a16_workspace_bytes(M, N, K, 128) > _lib.W4A16_NOALLOC_SCRATCH_BYTES
-    qw = torch.empty(K // 8, N, dtype=torch.int32, device=dev)      # never read: no launch
-    s = torch.empty(K // 128, N, dtype=torch.float16, device=dev)
-    z = torch.empty(K // 128, N, dtype=torch.float16, device=dev)
+    M, K, N, G = 24, 65536, 12288, 64    # decode kernel: K splits of 24 x 12288 fp32 = 72 MiB
+    assert lib.kbh_w4a16_workspace_bytes(M, N, K, G) > _lib.W4A16_NOALLOC_SCRATCH_BYTES
+    qw = torch.empty(K, N // 8, dtype=torch.int32, device=dev)      # never read: no launch
+    s = torch.empty(K // G, N, dtype=torch.float16, device=dev)
+    z = torch.empty(K // G, N, dtype=torch.float16, device=dev)
     x = torch.zeros(M, K, dtype=torch.float16, device=dev)
     y = torch.zeros(M, N, dtype=torch.float16, device=dev)
-    assert _noalloc(lib, x, qw, s, z, y, 128) == _lib.KBH_ERR_SCRATCH_LIMIT
+    assert _noalloc(lib, x, qw, s, z, y, G) == _lib.KBH_ERR_SCRATCH_LIMIT
     torch.cuda.synchronize()
     assert bool((y == 0).all())          # nothing was launched
