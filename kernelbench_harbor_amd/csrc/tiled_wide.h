@@ -8,8 +8,10 @@
 // and one K range (split-K); the tile is sized so that two workgroups fit on a CU (<= 128
 // accumulator and <= 128 other VGPRs per lane), which lets one workgroup's MFMAs run while the
 // other waits on memory or a barrier:
-//  * x never passes through LDS: each wave loads its own rows' MFMA A fragments straight from
-//    global memory (16 bytes per lane per 32x16 fragment), two slabs ahead of their use.
+//  * x is not shared through LDS: each wave loads its own rows' MFMA A fragments straight from
+//    global memory (16 bytes per lane per 32x16 fragment), PD slabs ahead of their use; int8
+//    (WideI8) loads the same rows in a coalesced pattern and reorders them through a private
+//    LDS buffer of the wave (XS in the kernel).
 //  * The weight slab is dequantized once per workgroup into LDS in MFMA B-fragment order
 //    (wide_b_offset), so a fragment read is one conflict-free ds_read_b128 per wave.
 //  * WM x (4/WM) waves, each (TM/WM) x (TN*WM/4) with 32x32x16 MFMAs; accumulators in AGPRs.
@@ -64,6 +66,7 @@ struct WideHalf {
   using Part = float;
   using Part4 = kbh_f32x4;
   static constexpr int kSlabK = 32;  // K elements per slab
+  static constexpr bool kStageX = false;  // x fragments straight from global memory
   __device__ static Acc mma(kbh_u32x4 a, kbh_u32x4 b, Acc c) { return mfma32x32x16<BF16>(a, b, c); }
 };
 struct WideI8 {
@@ -71,6 +74,7 @@ struct WideI8 {
   using Part = int;
   using Part4 = kbh_i32x4;
   static constexpr int kSlabK = 64;
+  static constexpr bool kStageX = true;  // x through a per-wave LDS buffer (XS below)
   // 32x32x32 int8: lane l holds A[row l%32][k 16(l/32)..+16], B[k 16(l/32)..+16][col l%32].
   __device__ static Acc mma(kbh_u32x4 a, kbh_u32x4 b, Acc c) {
     return __builtin_amdgcn_mfma_i32_32x32x32_i8(__builtin_bit_cast(kbh_i32x4, a),
@@ -178,19 +182,66 @@ tiled_wide_gemm(
   // A fragments: lane (r = lane%32, g = lane/32) of row block rb holds tile row
   // wm*TM/WM + 32rb + r, bytes 32*step + 16g .. +16 of the slab's 64-byte K run.
   const int fr = lane & 31, fg = lane >> 5;
-  const uint8_t* xrow[RB];
+  // XS (E::kStageX, one wave per row stripe): x reaches the fragments through a private LDS
+  // double buffer of the wave. Its global loads cover 16 rows x 64 bytes each (four lanes per
+  // row) instead of a fragment's 32 rows x 32 bytes, halving the cache lines per load; the wave
+  // then writes the rows into its LDS slot and reads them back in fragment order. Row q of the
+  // slot keeps 16-byte chunk c at q*64 + 16*(c ^ ((q >> 1) & 3)): the writes (4 lanes per row)
+  // and the fragment reads (one chunk of 8 consecutive rows per 8 lanes) are both conflict free.
+  // Measured: int8 W8A8 M=512 65 -> 60 us; fp16 W4A16 M=256..2048 and the MoE FFN 0-3% slower
+  // (their 32-deep slabs carry half the x bytes per MFMA), so only WideI8 stages.
+  constexpr bool XS = WN == 1 && E::kStageX;
+  constexpr int XR = TM / WM;                  // rows of one wave's stripe
+  constexpr int XSLOT = XR * WSLAB_BYTES;      // LDS bytes of one slab of the stripe
+  __shared__ __attribute__((aligned(16))) uint8_t Xs[XS ? 4 * 2 * XSLOT : 16];
+  uint8_t* const xw = Xs + (XS ? wave * 2 * XSLOT : 0);
+  const uint8_t* xrow[2 * RB];
 #pragma unroll
-  for (int rb = 0; rb < RB; ++rb) {
-    const int r = wm * (TM / WM) + rb * 32 + fr;  // rows past the tile re-read its last row
-    xrow[rb] = (const uint8_t*)x + (size_t)rm.a_row(ti, r) * K * EB + fg * 16;
+  for (int q = 0; q < 2 * RB; ++q) {
+    if constexpr (XS) {
+      if (q >= XR / 16) continue;
+      const int r = wm * XR + 16 * q + (lane >> 2);  // rows past the tile re-read its last row
+      xrow[q] = (const uint8_t*)x + (size_t)rm.a_row(ti, r) * K * EB + 16 * (lane & 3);
+    } else {
+      if (q >= RB) continue;
+      const int r = wm * (TM / WM) + q * 32 + fr;
+      xrow[q] = (const uint8_t*)x + (size_t)rm.a_row(ti, r) * K * EB + fg * 16;
+    }
   }
   struct AStage {
-    kbh_u32x4 a[RB][2];
+    kbh_u32x4 a[RB][2];  // XS: a[rb][s] = 16-row load 2rb + s of the stripe
   };
   auto load_a_step = [&](AStage& st, int kt, int s) {
-    const size_t b0 = (size_t)(kt0 + kt) * WSLAB_BYTES + 32 * s;
+    if constexpr (XS) {
+      const size_t b0 = (size_t)(kt0 + kt) * WSLAB_BYTES;
 #pragma unroll
-    for (int rb = 0; rb < RB; ++rb) st.a[rb][s] = *reinterpret_cast<const kbh_u32x4*>(xrow[rb] + b0);
+      for (int rb = 0; rb < RB; ++rb)
+        st.a[rb][s] = *reinterpret_cast<const kbh_u32x4*>(xrow[2 * rb + s] + b0);
+    } else {
+      const size_t b0 = (size_t)(kt0 + kt) * WSLAB_BYTES + 32 * s;
+#pragma unroll
+      for (int rb = 0; rb < RB; ++rb)
+        st.a[rb][s] = *reinterpret_cast<const kbh_u32x4*>(xrow[rb] + b0);
+    }
+  };
+  auto xs_chunk = [](int q, int c) { return q * WSLAB_BYTES + 16 * (c ^ ((q >> 1) & 3)); };
+  // XS: one slab of the stripe from the load ring into LDS slot `slot`.
+  auto stage_a = [&](const AStage& st, int slot) {
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+        *reinterpret_cast<kbh_u32x4*>(xw + slot * XSLOT + xs_chunk(16 * (2 * rb + h) + (lane >> 2), lane & 3)) = st.a[rb][h];
+  };
+  // Fragments of k16 step s of the slab in registers (no XS) or in LDS slot `slot` (XS).
+  auto frag_a = [&](kbh_u32x4 (&af)[RB], const AStage& st, int slot, int s) {
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) {
+      if constexpr (XS)
+        af[rb] = *reinterpret_cast<const kbh_u32x4*>(xw + slot * XSLOT + xs_chunk(32 * rb + fr, 2 * s + fg));
+      else
+        af[rb] = st.a[rb][s];
+    }
   };
   auto load_b = [&](typename BP::Raw& r, int kt) { bp.load(r, (kt0 + kt) * SK, n0, t); };
   auto load_g = [&](typename BP::Grp& g, int kt) { bp.load_group(g, (kt0 + kt) * SK, n0, t); };
@@ -214,18 +265,18 @@ tiled_wide_gemm(
 #pragma unroll
       for (int e = 0; e < 16; ++e) acc[i][j][e] = 0;
 
-  auto mma = [&](const AStage& st, int s, const kbh_u32x4 (&bf)[CB]) {
+  auto mma = [&](const kbh_u32x4 (&af)[RB], const kbh_u32x4 (&bf)[CB]) {
 #pragma unroll
     for (int i = 0; i < RB; ++i)
 #pragma unroll
-      for (int j = 0; j < CB; ++j) acc[i][j] = E::mma(st.a[i][s], bf[j], acc[i][j]);
+      for (int j = 0; j < CB; ++j) acc[i][j] = E::mma(af[i], bf[j], acc[i][j]);
   };
   // MFMAs q in [lo, hi) of a k16 step (q = CB*i + j).
-  auto mma_range = [&](const AStage& st, int s, const kbh_u32x4 (&bf)[CB], int lo, int hi) {
+  auto mma_range = [&](const kbh_u32x4 (&af)[RB], const kbh_u32x4 (&bf)[CB], int lo, int hi) {
 #pragma unroll
     for (int q = 0; q < RB * CB; ++q)
       if (q >= lo && q < hi)
-        acc[q / CB][q % CB] = E::mma(st.a[q / CB][s], bf[q % CB], acc[q / CB][q % CB]);
+        acc[q / CB][q % CB] = E::mma(af[q / CB], bf[q % CB], acc[q / CB][q % CB]);
   };
 
   // Prologue: slab 0 in LDS, step-0 fragments of slab 0 in registers, A of slabs 0..PD-1, raw
@@ -246,9 +297,12 @@ tiled_wide_gemm(
 #pragma unroll
   for (int i = 1; i <= PD; ++i) load_b(R[i % PD], min(i, last));
   load_g(G[1], min(SPG, last));
+  kbh_u32x4 a0[RB], a1[RB];  // A fragments of step 0 (of the slab after next's barrier) / 1
+  if constexpr (XS) stage_a(A[0], 0);
   __syncthreads();
   kbh_u32x4 b0[CB], b1[CB];
   read_b(b0, 0, 0);
+  frag_a(a0, A[0], 0, 0);
 
   // Steady state: KT is a multiple of U; loads past the end re-read the last slab or group
   // (never used), so the loop body is branch-free. Slab s+1, dequantized during slab s, belongs
@@ -267,10 +321,11 @@ tiled_wide_gemm(
       const bool new_group = (u + 1) % SPG == 0;  // slab s+1 starts a group
       const int gsel = ((u + 1) / SPG) & 1;
       read_b(b1, cur, 1);
+      frag_a(a1, A[ra], u & 1, 1);
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int p = 0; p < NP; ++p) {
-        mma_range(A[ra], 0, b0, p * NMF / NP, (p + 1) * NMF / NP);
+        mma_range(a0, b0, p * NMF / NP, (p + 1) * NMF / NP);
         __builtin_amdgcn_sched_barrier(0);
         bp.store_part(R[rr], G[gsel], Bs[1 - cur], t, p);  // slab s+1 (after last: unused)
         __builtin_amdgcn_sched_barrier(0);
@@ -278,7 +333,11 @@ tiled_wide_gemm(
       __syncthreads();  // s_barrier alone does not stop MFMAs moving across: fenced both sides
       __builtin_amdgcn_sched_barrier(0);
       read_b(b0, 1 - cur, 0);  // step 0 of slab s+1
-      mma(A[ra], 1, b1);
+      // XS: slab s+1 from its ring slot into the wave's other LDS slot (slab s-1's, read in the
+      // previous iteration), then its step-0 fragments.
+      if constexpr (XS) stage_a(A[(u + 1) % PD], (u + 1) & 1);
+      frag_a(a0, A[(u + 1) % PD], (u + 1) & 1, 0);
+      mma(a1, b1);
       load_a_step(A[ra], min(s + PD, last), 0);
       load_b(R[rr], min(s + 1 + PD, last));
       if (new_group) load_g(G[gsel ^ 1], min(s + 1 + SPG, last));
