@@ -53,9 +53,9 @@ def w4a16_bytes(M, K=K_DIM, N=N_DIM, G=GROUP):
 # 256 MiB device copy reads as 131084 KiB) plus WRITE_SIZE (exact on the same copy), summed over
 # every kbh:: kernel of the call. Table and commands: profiles/hbm_traffic_all_records.md.
 PMC_TRAFFIC = {
-    "w4a16 M=1": 32_167_648, "w4a16 M=4": 34_454_252, "w4a16 M=16": 43_596_898,
+    "w4a16 M=1": 32_167_648, "w4a16 M=4": 34_454_252, "w4a16 M=16": 42_545_554,
     "w4a16 M=64": 64_031_899, "w4a16 M=256": 108_180_696, "w4a16 M=1024": 240_722_352,
-    "w4a16 M=2048": 340_853_600, "w8a8 M=16": 68_182_320, "w8a8 M=512": 210_728_956,
+    "w4a16 M=2048": 340_853_600, "w8a8 M=16": 68_182_320, "w8a8 M=512": 210_735_483,
     "mxfp8 M=128": 94_936_720, "mxfp8 M=2048": 290_080_130,
     "fp8w (reference op) M=16 b128": 70_943_466,
     "qmoe_ffn T=512 D=4096 F=14336 E=8 top2": 1_229_346_633,

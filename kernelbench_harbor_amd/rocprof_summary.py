@@ -82,7 +82,8 @@ def main() -> None:
           " calls | avg us | median us | min us | max us |")
     print("|---|---|---|" + ("---|" if nx else "") + "---|---|---|---|---|")
     for r in rows:
-        short = r["kernel"].replace("(anonymous namespace)::", "").replace("void ", "")
+        short = (r["kernel"].replace("(anonymous namespace)::", "").replace("void ", "")
+                 .replace("kbh::", ""))
         # drop the argument list: the last top-level "(...)" (template arguments may hold
         # parentheses, as in "float __vector(4)")
         depth, cut = 0, len(short)
