@@ -543,18 +543,28 @@ struct W4PairPolicy {
   // Word w of the tile: chunk c = w / 16, matrix (w / 8) % 2, real column n0/2 + 64c + 8(w % 8).
   // Half::load reads word w at column n0' + 8w, so n0' = n0/2 - 64c - 64 * matrix.
   __device__ static int shift(int w) { return 4 * (w & 16) + 8 * (w & 8); }
+  // The matrix of lane t's word is selected per lane by pointer (a uniform instruction stream).
   __device__ void load(Raw& r, int k0, int n0, int t) const {
     const int w = Half::word_of(t);
-    const Half& m = (w & 8) ? u : g;  // per-lane matrix, uniform instruction
-    m.load(r, k0, n0 / 2 - shift(w), t);
+    g.load_from(r, (w & 8) ? u.qw : g.qw, k0, n0 / 2 - shift(w), t);
   }
   __device__ void load_group(Grp& gr, int k0, int n0, int t) const {
     const int w = Half::word_of(t);
-    const Half& m = (w & 8) ? u : g;
-    m.load_group(gr, k0, n0 / 2 - shift(w), t);
+    const bool up = (w & 8) != 0;
+    g.load_group_from(gr, up ? u.scales : g.scales, up ? u.zeros : g.zeros, k0, n0 / 2 - shift(w), t);
   }
+  static constexpr bool kHasFast = Half::kHasFast;
+  // Tile columns n0 .. n0 + TN are real columns n0/2 .. n0/2 + TN/2 of both matrices.
+  __device__ bool scan_fast(int k_begin, int k_end, int n0, int t) const {
+    return g.scan_cols(k_begin, k_end, n0 / 2, TN / 2, t) &&
+           u.scan_cols(k_begin, k_end, n0 / 2, TN / 2, t);
+  }
+  template <bool FAST>
+  __device__ void prepare_group(Grp& gr) const { g.template prepare_group<FAST>(gr); }
+  template <bool FAST>
   __device__ void store_part(const Raw& r, const Grp& gr, uint8_t* Bs, int t, int p) const {
-    g.store_part(r, gr, Bs, t, p);  // dequantisation and LDS layout do not depend on the matrix
+    // dequantisation and LDS layout do not depend on the matrix
+    g.template store_part<FAST>(r, gr, Bs, t, p);
   }
 };
 

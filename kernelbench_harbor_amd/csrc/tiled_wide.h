@@ -47,6 +47,8 @@
 //   static constexpr int kTN, kParts;
 //   void load(Raw&, int k0, int n0, int t) const;       issue the slab's global loads
 //   void load_group(Grp&, int k0, int n0, int t) const; constants of the group holding row k0
+//   void prepare_group(Grp&) const;                     once per group, before its first slab's
+//                                                       store_part (its loads have arrived)
 //   void store_part(const Raw&, const Grp&, uint8_t* Bs, int t, int p) const;
 //                                                       part p < kParts of the slab into LDS
 //   The LDS byte offset of byte kb (= k * element size) of column n of the slab is
@@ -58,6 +60,11 @@
 namespace kbh {
 
 constexpr int WSLAB_BYTES = 64;  // bytes of K per row per slab
+
+template <bool B>
+struct WideFlag {
+  static constexpr bool value = B;
+};
 
 // Element traits: MFMA and accumulator types of the two operand families.
 template <bool BF16>
@@ -279,77 +286,97 @@ tiled_wide_gemm(
         acc[q / CB][q % CB] = E::mma(af[q / CB], bf[q % CB], acc[q / CB][q % CB]);
   };
 
-  // Prologue: slab 0 in LDS, step-0 fragments of slab 0 in registers, A of slabs 0..PD-1, raw
-  // weights of slabs 1..PD and the constants of the second group in flight. Ring slot s % PD
-  // holds the A fragments of slab s and the raw weights of slab s (consumed during slab s - 1).
-  AStage A[PD];
-  typename BP::Raw R[PD];
-  typename BP::Grp G[2];  // constants of groups with even / odd index within the K range
-  const int last = KT - 1;
-  load_b(R[0], 0);
-  load_g(G[0], 0);
+  // FAST: the policy's faster producer path, valid when every weight constant of this
+  // workgroup's K range and columns allows it (one check before the loop, then a separate copy
+  // of the loop, so the loop itself has no branch). Only the 128-row tiles take it: there the
+  // producer is on the critical path (W4A16 M=256 57 -> 55 us, MoE FFN 993 -> 974 us); with
+  // 256-row tiles the second copy of the loop spilled registers and ran no faster, and 64-row
+  // tiles (few slabs per workgroup) measured 2% slower.
+  constexpr bool kFast = BP::kHasFast && TM == 128 && WM == 4;
+  bool fast = false;
+  if constexpr (kFast) fast = __syncthreads_and(bp.scan_fast(kt0 * SK, (kt0 + KT) * SK, n0, t)) != 0;
+  auto run = [&](auto fast_tag) {
+    constexpr bool FAST = decltype(fast_tag)::value;
+    // Prologue: slab 0 in LDS, step-0 fragments of slab 0 in registers, A of slabs 0..PD-1, raw
+    // weights of slabs 1..PD and the constants of the second group in flight. Ring slot s % PD
+    // holds the A fragments of slab s and the raw weights of slab s (consumed during slab s - 1).
+    AStage A[PD];
+    typename BP::Raw R[PD];
+    typename BP::Grp G[2];  // constants of groups with even / odd index within the K range
+    const int last = KT - 1;
+    load_b(R[0], 0);
+    load_g(G[0], 0);
 #pragma unroll
-  for (int i = 0; i < PD; ++i)
+    for (int i = 0; i < PD; ++i)
 #pragma unroll
-    for (int st = 0; st < 2; ++st) load_a_step(A[i], min(i, last), st);
+      for (int st = 0; st < 2; ++st) load_a_step(A[i], min(i, last), st);
+    bp.template prepare_group<FAST>(G[0]);
 #pragma unroll
-  for (int p = 0; p < BP::kParts; ++p) bp.store_part(R[0], G[0], Bs[0], t, p);
+    for (int p = 0; p < BP::kParts; ++p) bp.template store_part<FAST>(R[0], G[0], Bs[0], t, p);
 #pragma unroll
-  for (int i = 1; i <= PD; ++i) load_b(R[i % PD], min(i, last));
-  load_g(G[1], min(SPG, last));
-  kbh_u32x4 a0[RB], a1[RB];  // A fragments of step 0 (of the slab after next's barrier) / 1
-  if constexpr (XS) stage_a(A[0], 0);
-  __syncthreads();
-  kbh_u32x4 b0[CB], b1[CB];
-  read_b(b0, 0, 0);
-  frag_a(a0, A[0], 0, 0);
+    for (int i = 1; i <= PD; ++i) load_b(R[i % PD], min(i, last));
+    load_g(G[1], min(SPG, last));
+    kbh_u32x4 a0[RB], a1[RB];  // A fragments of step 0 (of the slab after next's barrier) / 1
+    if constexpr (XS) stage_a(A[0], 0);
+    __syncthreads();
+    kbh_u32x4 b0[CB], b1[CB];
+    read_b(b0, 0, 0);
+    frag_a(a0, A[0], 0, 0);
 
-  // Steady state: KT is a multiple of U; loads past the end re-read the last slab or group
-  // (never used), so the loop body is branch-free. Slab s+1, dequantized during slab s, belongs
-  // to group (u+1)/SPG of the iteration (register set ((u+1)/SPG) & 1); when it starts a group,
-  // the set of the group just finished is reloaded with the group after next. The order inside
-  // a slab is fixed with scheduling barriers (the scheduler otherwise clusters the
-  // dequantisation and moves MFMAs across s_barrier).
-  constexpr int NMF = RB * CB;  // MFMAs per k16 step
-  constexpr int NP = BP::kParts;
-  for (int kt = 0; kt < KT; kt += U) {
+    // Steady state: KT is a multiple of U; loads past the end re-read the last slab or group
+    // (never used), so the loop body is branch-free. Slab s+1, dequantized during slab s, belongs
+    // to group (u+1)/SPG of the iteration (register set ((u+1)/SPG) & 1); when it starts a group,
+    // the set of the group just finished is reloaded with the group after next. The order inside
+    // a slab is fixed with scheduling barriers (the scheduler otherwise clusters the
+    // dequantisation and moves MFMAs across s_barrier).
+    constexpr int NMF = RB * CB;  // MFMAs per k16 step
+    constexpr int NP = BP::kParts;
+    for (int kt = 0; kt < KT; kt += U) {
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int s = kt + u;  // slab in registers / LDS buffer u&1
-      const int cur = u & 1;
-      const int ra = u % PD, rr = (u + 1) % PD;  // ring slots of slab s (A) and s+1 (raw)
-      const bool new_group = (u + 1) % SPG == 0;  // slab s+1 starts a group
-      const int gsel = ((u + 1) / SPG) & 1;
-      read_b(b1, cur, 1);
-      frag_a(a1, A[ra], u & 1, 1);
-      __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-      for (int p = 0; p < NP; ++p) {
-        mma_range(a0, b0, p * NMF / NP, (p + 1) * NMF / NP);
+      for (int u = 0; u < U; ++u) {
+        const int s = kt + u;  // slab in registers / LDS buffer u&1
+        const int cur = u & 1;
+        const int ra = u % PD, rr = (u + 1) % PD;  // ring slots of slab s (A) and s+1 (raw)
+        const bool new_group = (u + 1) % SPG == 0;  // slab s+1 starts a group
+        const int gsel = ((u + 1) / SPG) & 1;
+        read_b(b1, cur, 1);
+        frag_a(a1, A[ra], u & 1, 1);
+        if (new_group) bp.template prepare_group<FAST>(G[gsel]);  // slab s+1 starts set gsel's group
         __builtin_amdgcn_sched_barrier(0);
-        bp.store_part(R[rr], G[gsel], Bs[1 - cur], t, p);  // slab s+1 (after last: unused)
+#pragma unroll
+        for (int p = 0; p < NP; ++p) {
+          mma_range(a0, b0, p * NMF / NP, (p + 1) * NMF / NP);
+          __builtin_amdgcn_sched_barrier(0);
+          bp.template store_part<FAST>(R[rr], G[gsel], Bs[1 - cur], t, p);  // slab s+1 (after last: unused)
+          __builtin_amdgcn_sched_barrier(0);
+        }
+        __syncthreads();  // s_barrier alone does not stop MFMAs moving across: fenced both sides
+        __builtin_amdgcn_sched_barrier(0);
+        read_b(b0, 1 - cur, 0);  // step 0 of slab s+1
+        // XS: slab s+1 from its ring slot into the wave's other LDS slot (slab s-1's, read in the
+        // previous iteration), then its step-0 fragments.
+        if constexpr (XS) stage_a(A[(u + 1) % PD], (u + 1) & 1);
+        frag_a(a0, A[(u + 1) % PD], (u + 1) & 1, 0);
+        mma(a1, b1);
+        load_a_step(A[ra], min(s + PD, last), 0);
+        load_b(R[rr], min(s + 1 + PD, last));
+        if (new_group) load_g(G[gsel ^ 1], min(s + 1 + SPG, last));
+        load_a_step(A[ra], min(s + PD, last), 1);
+        __builtin_amdgcn_sched_group_barrier(0x100, CB, 1);
+#pragma unroll
+        for (int i = 0; i < NMF; ++i) {
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);
+          __builtin_amdgcn_sched_group_barrier(0x020, 1, 1);
+        }
         __builtin_amdgcn_sched_barrier(0);
       }
-      __syncthreads();  // s_barrier alone does not stop MFMAs moving across: fenced both sides
-      __builtin_amdgcn_sched_barrier(0);
-      read_b(b0, 1 - cur, 0);  // step 0 of slab s+1
-      // XS: slab s+1 from its ring slot into the wave's other LDS slot (slab s-1's, read in the
-      // previous iteration), then its step-0 fragments.
-      if constexpr (XS) stage_a(A[(u + 1) % PD], (u + 1) & 1);
-      frag_a(a0, A[(u + 1) % PD], (u + 1) & 1, 0);
-      mma(a1, b1);
-      load_a_step(A[ra], min(s + PD, last), 0);
-      load_b(R[rr], min(s + 1 + PD, last));
-      if (new_group) load_g(G[gsel ^ 1], min(s + 1 + SPG, last));
-      load_a_step(A[ra], min(s + PD, last), 1);
-      __builtin_amdgcn_sched_group_barrier(0x100, CB, 1);
-#pragma unroll
-      for (int i = 0; i < NMF; ++i) {
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);
-        __builtin_amdgcn_sched_group_barrier(0x020, 1, 1);
-      }
-      __builtin_amdgcn_sched_barrier(0);
     }
+  };
+  if constexpr (kFast) {
+    if (fast) run(WideFlag<true>{});
+    else run(WideFlag<false>{});
+  } else {
+    run(WideFlag<false>{});
   }
 
   // Accumulator element e of tile (i, j): row 8(e/4) + 4(lane/32) + e%4, column lane%32.

@@ -132,9 +132,14 @@ struct W4WidePolicy {
   struct Raw {
     uint32_t w[kRows];
   };
+  // s, z: the group's scales and zero points of the thread's 8 columns (two per dword).
+  // zm = 1024 + z of the same columns, for the one-step fp16 path (FAST below).
   struct Grp {
     kbh_u32x4 s, z;
+    kbh_u32x4 zm;
+    uint32_t magic;
   };
+  static constexpr bool kHasFast = !BF16;
   // TN = 256: t = [w bits 0-2][h bit 0][w bits 3-4][h bits 1-2], rows 4h..4h+3.
   // TN = 128: t = [h bits 0-1][w bits 0-2][w bit 3][h bits 2-3], rows 2h, 2h+1.
   // Either way the lanes of one LDS write pass cover distinct banks.
@@ -147,19 +152,68 @@ struct W4WidePolicy {
     else return (t & 3) | ((t >> 6) << 2);
   }
 
-  __device__ void load(Raw& r, int k0, int n0, int t) const {
+  __device__ void load(Raw& r, int k0, int n0, int t) const { load_from(r, qw, k0, n0, t); }
+  // load / load_group from another matrix of the same shape (paired producers select the
+  // matrix per lane by pointer)
+  __device__ void load_from(Raw& r, const uint32_t* qw_, int k0, int n0, int t) const {
     const int w = word_of(t), h = rows_of(t);
     const int NP = N >> 3;
-    const uint32_t* q = qw + (size_t)(k0 + kRows * h) * NP + (n0 >> 3) + w;
+    const uint32_t* q = qw_ + (size_t)(k0 + kRows * h) * NP + (n0 >> 3) + w;
     // Plain (cached) loads: the row blocks of one K range run on one XCD and share these
     // words through its L2 (the non-temporal hint measured 2-7% slower at M=64..2048).
 #pragma unroll
     for (int i = 0; i < kRows; ++i) r.w[i] = q[(size_t)i * NP];
   }
   __device__ void load_group(Grp& g, int k0, int n0, int t) const {
+    load_group_from(g, scales, zeros, k0, n0, t);
+  }
+  __device__ void load_group_from(Grp& g, const uint16_t* scales_, const uint16_t* zeros_, int k0,
+                                  int n0, int t) const {
     const size_t off = (size_t)(k0 / group) * N + n0 + 8 * word_of(t);
-    g.s = *reinterpret_cast<const kbh_u32x4*>(scales + off);
-    g.z = *reinterpret_cast<const kbh_u32x4*>(zeros + off);
+    g.s = *reinterpret_cast<const kbh_u32x4*>(scales_ + off);
+    g.z = *reinterpret_cast<const kbh_u32x4*>(zeros_ + off);
+  }
+  // FAST (fp16 only): every zero point of the workgroup's K range and columns is an integer of
+  // magnitude below 960, as the reference's uint4 zero points are. Then 1024 + z is exact, and
+  // q - z is one exact subtraction from the magic number 1024 + q (low nibble), or an fma and an
+  // add from 1024 + 16q (high nibble), instead of removing the magic number first: the same
+  // values with fewer instructions. scan_cols reports whether this thread's share of the
+  // zero points [k_begin, k_end) x [n0, n0 + cols) allows it; the kernel ANDs the workgroup.
+  __device__ bool scan_cols(int k_begin, int k_end, int n0, int cols, int t) const {
+    if constexpr (BF16) {
+      return false;
+    } else {
+      typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+      const int g0 = k_begin / group, chunks = cols / 8;
+      const int total = ((k_end - 1) / group - g0 + 1) * chunks;
+      bool ok = true;
+      for (int i = t; i < total; i += 256) {
+        const h8 z = __builtin_bit_cast(
+            h8, *reinterpret_cast<const kbh_u32x4*>(zeros + (size_t)(g0 + i / chunks) * N + n0 +
+                                                    8 * (i % chunks)));
+        // z + 1024 rounds to an integer below 2048: the round trip is exact iff z is an integer
+        // in (-1024, 1024); |z| < 960 keeps (64 + q) - (1024 + z) + 960 in range too
+        const h8 bm = (z + (_Float16)1024.0f) - (_Float16)1024.0f;
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+          ok = ok && bm[e] == z[e] && (float)z[e] < 960.0f && (float)z[e] > -960.0f;
+      }
+      return ok;
+    }
+  }
+  __device__ bool scan_fast(int k_begin, int k_end, int n0, int t) const {
+    return scan_cols(k_begin, k_end, n0, TN, t);
+  }
+  // Derived constants of a loaded group, once before its first slab (the loads have landed).
+  template <bool FAST>
+  __device__ void prepare_group(Grp& g) const {
+    if constexpr (FAST) {
+      typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+      g.zm = __builtin_bit_cast(kbh_u32x4, __builtin_bit_cast(h8, g.z) + (_Float16)1024.0f);
+      uint32_t magic = kMagicF16;
+      asm volatile("" : "+v"(magic));  // a VGPR: v_and_or_b32 takes the mask from an SGPR
+      g.magic = magic;
+    }
   }
 
   // Rows (2i, 2i+1) of column c of the thread's word, dequantized: one dword (two values).
@@ -184,12 +238,42 @@ struct W4WidePolicy {
       return __builtin_bit_cast(uint32_t, (q - h2{z, z}) * h2{sc, sc});
     }
   }
+  // The same value as pair<C> under FAST (fp16): (q - z) exactly in one step, then * s.
   template <int C>
+  __device__ uint32_t pair_fast(const Raw& r, const Grp& g, int i) const {
+    typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+    const uint32_t P = pair_bytes<(C >> 1)>(r.w[2 * i], r.w[2 * i + 1]);
+    const uint32_t sw = g.s[C >> 1];
+    const _Float16 sc = __builtin_bit_cast(_Float16, (uint16_t)((C & 1) ? (sw >> 16) : (sw & 0xffffu)));
+    const uint32_t zw = g.zm[C >> 1];
+    const _Float16 zm = __builtin_bit_cast(_Float16, (uint16_t)((C & 1) ? (zw >> 16) : (zw & 0xffffu)));
+    h2 d;
+    if constexpr ((C & 1) == 0) {
+      d = __builtin_bit_cast(h2, (P & mask) | g.magic) - h2{zm, zm};  // (1024 + q) - (1024 + z)
+    } else {
+      // (1024 + 16q) / 16 - (1024 + z) = q - z - 960 and + 960: integers below 2048, exact
+      uint32_t mask_hi = 0x00F000F0u, sixteenth = 0x2C002C00u;  // fp16 {1/16, 1/16}
+      asm("" : "+s"(mask_hi), "+s"(sixteenth));  // SGPR operands (one per VOP3)
+      const h2 k960 = {(_Float16)960.0f, (_Float16)960.0f};
+      d = __builtin_elementwise_fma(__builtin_bit_cast(h2, (P & mask_hi) | g.magic),
+                                    __builtin_bit_cast(h2, sixteenth), -h2{zm, zm}) + k960;
+    }
+    return __builtin_bit_cast(uint32_t, d * h2{sc, sc});
+  }
+  template <bool FAST, int C>
   __device__ void put(const Raw& r, const Grp& g, uint8_t* base, int fw) const {
     uint8_t* p = base + ((C ^ fw) << 4);
-    if constexpr (kRows == 4) *reinterpret_cast<kbh_u32x2*>(p) = kbh_u32x2{pair<C>(r, g, 0), pair<C>(r, g, 1)};
-    else *reinterpret_cast<uint32_t*>(p) = pair<C>(r, g, 0);
+    if constexpr (FAST && !BF16) {
+      if constexpr (kRows == 4)
+        *reinterpret_cast<kbh_u32x2*>(p) = kbh_u32x2{pair_fast<C>(r, g, 0), pair_fast<C>(r, g, 1)};
+      else *reinterpret_cast<uint32_t*>(p) = pair_fast<C>(r, g, 0);
+    } else if constexpr (kRows == 4) {
+      *reinterpret_cast<kbh_u32x2*>(p) = kbh_u32x2{pair<C>(r, g, 0), pair<C>(r, g, 1)};
+    } else {
+      *reinterpret_cast<uint32_t*>(p) = pair<C>(r, g, 0);
+    }
   }
+  template <bool FAST>
   __device__ void store_part(const Raw& r, const Grp& g, uint8_t* Bs, int t, int p) const {
     const int w = word_of(t), h = rows_of(t);
     // Rows kRows*h.. are bytes 2*kRows*h.. of the column's K run:
@@ -197,14 +281,14 @@ struct W4WidePolicy {
     uint8_t* base = Bs + wide_b_offset<TN>(2 * kRows * h, 8 * w) - wide_slot(8 * w) * 16 + w * 128;
     const int fw = (w ^ (w >> 3)) & 7;
     switch (p) {
-      case 0: put<0>(r, g, base, fw); break;
-      case 1: put<1>(r, g, base, fw); break;
-      case 2: put<2>(r, g, base, fw); break;
-      case 3: put<3>(r, g, base, fw); break;
-      case 4: put<4>(r, g, base, fw); break;
-      case 5: put<5>(r, g, base, fw); break;
-      case 6: put<6>(r, g, base, fw); break;
-      default: put<7>(r, g, base, fw); break;
+      case 0: put<FAST, 0>(r, g, base, fw); break;
+      case 1: put<FAST, 1>(r, g, base, fw); break;
+      case 2: put<FAST, 2>(r, g, base, fw); break;
+      case 3: put<FAST, 3>(r, g, base, fw); break;
+      case 4: put<FAST, 4>(r, g, base, fw); break;
+      case 5: put<FAST, 5>(r, g, base, fw); break;
+      case 6: put<FAST, 6>(r, g, base, fw); break;
+      default: put<FAST, 7>(r, g, base, fw); break;
     }
   }
 };

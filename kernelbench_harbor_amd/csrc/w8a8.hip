@@ -289,6 +289,11 @@ struct W8WidePolicy {
       r.r[i] = *reinterpret_cast<const kbh_u32x2*>(p + (size_t)i * N);
   }
   __device__ void load_group(Grp&, int, int, int) const {}
+  static constexpr bool kHasFast = false;
+  __device__ bool scan_fast(int, int, int, int) const { return false; }
+  template <bool FAST>
+  __device__ void prepare_group(Grp&) const {}
+  template <bool FAST>
   __device__ void store_part(const Raw& r, const Grp&, uint8_t* Bs, int t, int p) const {
     const int cb = cb_of(t), rb = rb_of(t);
     uint32_t lo[4], hi[4], clo[4], chi[4];

@@ -74,16 +74,22 @@ def test_w4a16_full_size_decode(dev, M):
     assert cmp.ok, cmp
 
 
-@pytest.mark.parametrize("M,N,frac_zeros", [(16, 512, False), (64, 512, False), (64, 512, True),
-                                             (200, 512, False), (200, 512, True), (160, 384, False)])
+@pytest.mark.parametrize("M,N,zeros", [(16, 512, "uint4"), (64, 512, "uint4"), (64, 512, "frac"),
+                                       (200, 512, "uint4"), (200, 512, "frac"),
+                                       (200, 512, "partial"), (200, 512, "wide"),
+                                       (200, 512, "bound"), (160, 384, "uint4")])
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
-def test_w4a16_dequant_bit_exact(dev, dtype, M, N, frac_zeros):
+def test_w4a16_dequant_bit_exact(dev, dtype, M, N, zeros):
     """One-hot activations select single weight rows, so y[m, :] is the dequantized row
     k_m rounded once to the output dtype: it must equal the reference's own dequantization
     (unpack, subtract zero with one rounding, multiply by scale with one rounding) bit for bit.
-    M=16 exercises the split-K decode kernel, M=64 and M=200 the wide-tile kernel (128- and
-    256-column tiles), N=384 at M=160 the 256 x 128 LDS-staged kernel. Zero points with a
-    fractional part make the subtraction round, which the wide kernel reproduces exactly."""
+    M=16 exercises the split-K decode kernel, M=64 and M=200 the wide-tile kernel (64- and
+    128-row tiles), N=384 at M=160 the 256 x 128 LDS-staged kernel. Zero points with a
+    fractional part make the subtraction round, which the wide kernel reproduces exactly.
+    The 128-row fp16 tiles take a shorter dequantisation when every zero point of a
+    workgroup's K range and columns is an integer below 960 in magnitude: "uint4" and "wide"
+    (integers in [-900, 900]) take it everywhere, "frac" and "bound" (+-960) nowhere, and
+    "partial" (fractional zeros in 4 groups x 100 columns) in some workgroups only."""
     K, G = 4096, 128
     g = torch.Generator().manual_seed(7 + M)
     qw = inputs.random_packed_int4(K, N, g)
@@ -92,8 +98,14 @@ def test_w4a16_dequant_bit_exact(dev, dtype, M, N, frac_zeros):
     x[torch.arange(M), ks] = 1.0
     s = (torch.randn(K // G, N, generator=g) * 0.01).to(dtype)
     z = torch.randint(0, 16, (K // G, N), generator=g).to(torch.float32)
-    if frac_zeros:
+    if zeros == "frac":
         z = z + torch.rand(K // G, N, generator=g) * 0.999
+    elif zeros == "partial":
+        z[8:12, 300:400] += torch.rand(4, 100, generator=g) * 0.999
+    elif zeros == "wide":
+        z = torch.randint(-900, 901, (K // G, N), generator=g).to(torch.float32)
+    elif zeros == "bound":
+        z = torch.where(torch.rand(K // G, N, generator=g) < 0.5, 960.0, -960.0)
     z = z.to(dtype)
     y = ops.w4a16_gemm(x.to(dev), qw.to(dev), s.to(dev), z.to(dev)).float().cpu().numpy()
     dt = "f16" if dtype == torch.float16 else "bf16"
