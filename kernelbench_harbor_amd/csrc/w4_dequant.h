@@ -132,12 +132,10 @@ struct W4WidePolicy {
   struct Raw {
     uint32_t w[kRows];
   };
-  // s, z: the group's scales and zero points of the thread's 8 columns (two per dword).
-  // zm = 1024 + z of the same columns, for the one-step fp16 path (FAST below).
+  // s, z: the group's scales and zero points of the thread's 8 columns (two per dword); on the
+  // one-step fp16 path (FAST below) prepare_group replaces z by 1024 + z.
   struct Grp {
     kbh_u32x4 s, z;
-    kbh_u32x4 zm;
-    uint32_t magic;
   };
   static constexpr bool kHasFast = !BF16;
   // TN = 256: t = [w bits 0-2][h bit 0][w bits 3-4][h bits 1-2], rows 4h..4h+3.
@@ -209,10 +207,7 @@ struct W4WidePolicy {
   __device__ void prepare_group(Grp& g) const {
     if constexpr (FAST) {
       typedef _Float16 h8 __attribute__((ext_vector_type(8)));
-      g.zm = __builtin_bit_cast(kbh_u32x4, __builtin_bit_cast(h8, g.z) + (_Float16)1024.0f);
-      uint32_t magic = kMagicF16;
-      asm volatile("" : "+v"(magic));  // a VGPR: v_and_or_b32 takes the mask from an SGPR
-      g.magic = magic;
+      g.z = __builtin_bit_cast(kbh_u32x4, __builtin_bit_cast(h8, g.z) + (_Float16)1024.0f);
     }
   }
 
@@ -245,17 +240,19 @@ struct W4WidePolicy {
     const uint32_t P = pair_bytes<(C >> 1)>(r.w[2 * i], r.w[2 * i + 1]);
     const uint32_t sw = g.s[C >> 1];
     const _Float16 sc = __builtin_bit_cast(_Float16, (uint16_t)((C & 1) ? (sw >> 16) : (sw & 0xffffu)));
-    const uint32_t zw = g.zm[C >> 1];
+    const uint32_t zw = g.z[C >> 1];  // 1024 + z (prepare_group<true>)
     const _Float16 zm = __builtin_bit_cast(_Float16, (uint16_t)((C & 1) ? (zw >> 16) : (zw & 0xffffu)));
+    uint32_t magic = kMagicF16;
+    asm("" : "+v"(magic));  // a VGPR: v_and_or_b32 takes the mask from an SGPR
     h2 d;
     if constexpr ((C & 1) == 0) {
-      d = __builtin_bit_cast(h2, (P & mask) | g.magic) - h2{zm, zm};  // (1024 + q) - (1024 + z)
+      d = __builtin_bit_cast(h2, (P & mask) | magic) - h2{zm, zm};  // (1024 + q) - (1024 + z)
     } else {
       // (1024 + 16q) / 16 - (1024 + z) = q - z - 960 and + 960: integers below 2048, exact
       uint32_t mask_hi = 0x00F000F0u, sixteenth = 0x2C002C00u;  // fp16 {1/16, 1/16}
       asm("" : "+s"(mask_hi), "+s"(sixteenth));  // SGPR operands (one per VOP3)
       const h2 k960 = {(_Float16)960.0f, (_Float16)960.0f};
-      d = __builtin_elementwise_fma(__builtin_bit_cast(h2, (P & mask_hi) | g.magic),
+      d = __builtin_elementwise_fma(__builtin_bit_cast(h2, (P & mask_hi) | magic),
                                     __builtin_bit_cast(h2, sixteenth), -h2{zm, zm}) + k960;
     }
     return __builtin_bit_cast(uint32_t, d * h2{sc, sc});
