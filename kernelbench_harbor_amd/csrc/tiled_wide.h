@@ -288,11 +288,11 @@ tiled_wide_gemm(
 
   // FAST: the policy's faster producer path, valid when every weight constant of this
   // workgroup's K range and columns allows it (one check before the loop, then a separate copy
-  // of the loop, so the loop itself has no branch). Only the 128-row tiles take it: there the
-  // producer is on the critical path (W4A16 M=256 57 -> 55 us, MoE FFN 993 -> 974 us); with
-  // 256-row tiles the second copy of the loop spilled registers and ran no faster, and 64-row
-  // tiles (few slabs per workgroup) measured 2% slower.
-  constexpr bool kFast = BP::kHasFast && TM == 128 && WM == 4;
+  // of the loop, so the loop itself has no branch). The 64- and 128-row tiles take it: there
+  // the producer is on the critical path (W4A16 M=256 57 -> 55 us, M=64 31 -> 30 us, MoE FFN
+  // 993 -> 974 us); with 256-row tiles the second copy of the loop spilled registers and ran
+  // no faster.
+  constexpr bool kFast = BP::kHasFast && (TM == 64 || TM == 128);
   bool fast = false;
   if constexpr (kFast) fast = __syncthreads_and(bp.scan_fast(kt0 * SK, (kt0 + KT) * SK, n0, t)) != 0;
   auto run = [&](auto fast_tag) {

@@ -75,6 +75,7 @@ def test_w4a16_full_size_decode(dev, M):
 
 
 @pytest.mark.parametrize("M,N,zeros", [(16, 512, "uint4"), (64, 512, "uint4"), (64, 512, "frac"),
+                                       (64, 512, "partial"),
                                        (200, 512, "uint4"), (200, 512, "frac"),
                                        (200, 512, "partial"), (200, 512, "wide"),
                                        (200, 512, "bound"), (160, 384, "uint4")])
@@ -86,7 +87,7 @@ def test_w4a16_dequant_bit_exact(dev, dtype, M, N, zeros):
     M=16 exercises the split-K decode kernel, M=64 and M=200 the wide-tile kernel (64- and
     128-row tiles), N=384 at M=160 the 256 x 128 LDS-staged kernel. Zero points with a
     fractional part make the subtraction round, which the wide kernel reproduces exactly.
-    The 128-row fp16 tiles take a shorter dequantisation when every zero point of a
+    The 64- and 128-row fp16 tiles take a shorter dequantisation when every zero point of a
     workgroup's K range and columns is an integer below 960 in magnitude: "uint4" and "wide"
     (integers in [-900, 900]) take it everywhere, "frac" and "bound" (+-960) nowhere, and
     "partial" (fractional zeros in 4 groups x 100 columns) in some workgroups only."""
