@@ -81,6 +81,30 @@ def _check_device(*tensors: torch.Tensor) -> torch.device:
     return dev
 
 
+# Workspace and scratch sizes per (op, shape): the plans are pure functions of the shape, and
+# the two C calls cost ~0.35 us each per op call (a cached lookup ~0.1 us).
+_sizes: dict[tuple, tuple[int, int]] = {}
+
+
+def _w4a16_sizes(lib, M: int, N: int, K: int, group: int) -> tuple[int, int]:
+    key = ("w4a16", M, N, K, group)
+    hit = _sizes.get(key)
+    if hit is None:
+        hit = (lib.kbh_w4a16_workspace_bytes(M, N, K, group),
+               lib.kbh_w4a16_scratch_bytes(M, N, K, group))
+        _sizes[key] = hit
+    return hit
+
+
+def _w8a8_sizes(lib, M: int, N: int, K: int) -> tuple[int, int]:
+    key = ("w8a8", M, N, K)
+    hit = _sizes.get(key)
+    if hit is None:
+        hit = (lib.kbh_w8a8_workspace_bytes(M, N, K), lib.kbh_w8a8_scratch_bytes(M, N, K))
+        _sizes[key] = hit
+    return hit
+
+
 def w4a16_gemm(x: torch.Tensor, qweight: torch.Tensor, scales: torch.Tensor,
                zeros: torch.Tensor) -> torch.Tensor:
     """y = x @ ((unpack(qweight) - zeros) * scales), the packed-asymmetric W4A16 linear.
@@ -117,8 +141,9 @@ def w4a16_gemm(x: torch.Tensor, qweight: torch.Tensor, scales: torch.Tensor,
         zeros = zeros.contiguous()
         st = _stream_ptr(dev)
         lib = _lib.load()
-        ws = workspaces.get(lib.kbh_w4a16_workspace_bytes(M, N, K, group), dev, st)
-        sc = scratches.get(lib.kbh_w4a16_scratch_bytes(M, N, K, group), dev, st)
+        ws_bytes, sc_bytes = _w4a16_sizes(lib, M, N, K, group)
+        ws = workspaces.get(ws_bytes, dev, st)
+        sc = scratches.get(sc_bytes, dev, st)
         _lib.check(lib.kbh_w4a16_gemm(x2.data_ptr(), qweight.data_ptr(), scales.data_ptr(),
                                       zeros.data_ptr(), y.data_ptr(), ws.data_ptr(), ws.numel(),
                                       sc.data_ptr(), sc.numel(), M, N, K, group, code, st),
@@ -159,8 +184,9 @@ def w8a8_gemm(x_int8: torch.Tensor, w_int8: torch.Tensor, x_scale: torch.Tensor,
         xsc, wsc = x_scale.contiguous(), w_scale.contiguous()
         st = _stream_ptr(dev)
         lib = _lib.load()
-        ws = workspaces.get(lib.kbh_w8a8_workspace_bytes(M, N, K), dev, st)
-        sc = scratches.get(lib.kbh_w8a8_scratch_bytes(M, N, K), dev, st)
+        ws_bytes, sc_bytes = _w8a8_sizes(lib, M, N, K)
+        ws = workspaces.get(ws_bytes, dev, st)
+        sc = scratches.get(sc_bytes, dev, st)
         _lib.check(lib.kbh_w8a8_gemm(x2.data_ptr(), w.data_ptr(), xsc.data_ptr(), wsc.data_ptr(),
                                      y.data_ptr(), ws.data_ptr(), ws.numel(), sc.data_ptr(),
                                      sc.numel(), M, N, K, st), "kbh_w8a8_gemm")
@@ -177,8 +203,9 @@ def w8a8_gemm_i32(x_int8: torch.Tensor, w_int8: torch.Tensor) -> torch.Tensor:
         return acc
     st = _stream_ptr(dev)
     lib = _lib.load()
-    ws = workspaces.get(lib.kbh_w8a8_workspace_bytes(M, N, K), dev, st)
-    sc = scratches.get(lib.kbh_w8a8_scratch_bytes(M, N, K), dev, st)
+    ws_bytes, sc_bytes = _w8a8_sizes(lib, M, N, K)
+    ws = workspaces.get(ws_bytes, dev, st)
+    sc = scratches.get(sc_bytes, dev, st)
     st = lib.kbh_w8a8_gemm_i32(x2.data_ptr(), w.data_ptr(), acc.data_ptr(), ws.data_ptr(),
                                ws.numel(), sc.data_ptr(), sc.numel(), M, N, K, st)
     _lib.check(st, "kbh_w8a8_gemm_i32")
