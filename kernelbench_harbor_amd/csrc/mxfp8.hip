@@ -15,11 +15,14 @@
 // held in a two-slab register ring, two LDS buffers with 144-byte rows (conflict-free 16-byte
 // fragment reads). Each wave computes 64 x (32*WNT) with 2 x WNT MFMA tiles; per slab the LDS
 // stores of the next slab, the fragment reads of the next K step and the global loads are
-// interleaved with the MFMAs (one barrier per slab). For small M the K
-// range is split over gridDim.z; each split stores its partial tile into its own fp32 workspace
-// slice and splitk_sum_half (splitk.h) adds the slices in split order and converts.
+// interleaved with the MFMAs (one barrier per slab). From 1024 rows mxfp8_dma_kernel takes
+// 256 x 256 tiles instead (below). When the tiles fill fewer than 256 workgroups the K range is
+// split over gridDim.z; each split stores its partial tile into its own fp32 workspace slice and
+// splitk_sum_half (splitk.h) adds the slices in split order and converts.
 #include "kbh_common.h"
 #include "splitk.h"
+
+#include <type_traits>
 
 namespace kbh {
 namespace {
@@ -246,15 +249,217 @@ __global__ __launch_bounds__(256) void mxfp8_kernel(
   for_each([&](int i, int j, int e, size_t o) { slice[o] = accv[i][j][e]; });
 }
 
+
+// ---------------------------------------------------------------------------------------------
+// 256 x 256 tiles for large M (mxfp8_dma_kernel). The operands go from global memory straight
+// into LDS with the buffer loads' LDS mode (lane i of a 16-byte load lands at M0 + 16 i, of a
+// 4-byte load at M0 + 4 i; measured on gfx950), so no register ring stages them and each of the
+// 4 waves holds a 128 x 128 accumulator (4 x 4 MFMA tiles). Per 128-deep slab a workgroup loads
+// 64 KB for 2x the MFMA work of the 128 x 256 tile's 48 KB.
+//
+// LDS per buffer: A and B slabs of 256 rows x 128 bytes without padding, 16-byte chunk c of row
+// r at r * 128 + 16 (c ^ ((r >> 1) & 7)) (the 16 rows one fragment read covers hit 16 different
+// 16-byte bank groups), then the 256 + 256 scale dwords. A load instruction fills one 1 KB
+// block (8 rows): lane i takes row 8 blk + i / 8 and the chunk that the swizzle puts at
+// position i % 8. Two buffers; slab s + 2 is loaded into buffer s & 1 during the second half of
+// slab s, after the barrier that ends every wave's reads of slab s.
+constexpr int DBM = 256;          // tile rows = tile columns
+constexpr int DSLAB = DBM * XBK;  // bytes of one operand slab
+
+template <bool BF16>
+__global__ __launch_bounds__(256) void mxfp8_dma_kernel(
+    const uint8_t* __restrict__ a, const uint8_t* __restrict__ as, const uint8_t* __restrict__ b,
+    const uint8_t* __restrict__ bs, uint16_t* __restrict__ y, float* __restrict__ acc, int M,
+    int N, int K, int slabs_per_split) {
+  // One object per buffer and operand, so that the compiler can tell the LDS writes of the
+  // loads in flight from the fragment reads of the other buffer.
+  __shared__ __attribute__((aligned(16))) uint8_t La0[DSLAB], La1[DSLAB], Lb0[DSLAB], Lb1[DSLAB];
+  __shared__ __attribute__((aligned(16))) uint32_t Ls0[2 * DBM], Ls1[2 * DBM];
+
+  const int t = threadIdx.x;
+  const int lane = t & 63, wave = t >> 6;
+  const int wu = __builtin_amdgcn_readfirstlane(wave);
+  const int wm = wave >> 1, wn = wave & 1;
+  const int ntn = N / DBM;
+  // Tile order as in mxfp8_kernel: groups of up to 8 row blocks, rows fastest in a group.
+  const int id = xcd_remap(blockIdx.x, gridDim.x);
+  const int nmb = gridDim.x / ntn;
+  const int gm0 = nmb < 8 ? nmb : 8;
+  const int grp = id / (gm0 * ntn), first_m = grp * gm0;
+  const int gm = nmb - first_m < gm0 ? nmb - first_m : gm0;
+  const int r_in = id - grp * gm0 * ntn;
+  const int mb = first_m + r_in % gm, nb = r_in / gm;
+  const int m0 = mb * DBM, n0 = nb * DBM;
+  const int splits = gridDim.z, split = blockIdx.z;
+  const int KS = K / 32;
+  const int kt_begin = split * slabs_per_split;
+  const int KT = slabs_per_split;
+
+  const __amdgpu_buffer_rsrc_t ra = make_rsrc(a, (size_t)M * K);  // rows past M read as zero
+  const __amdgpu_buffer_rsrc_t rb = make_rsrc(b, (size_t)N * K);
+  const __amdgpu_buffer_rsrc_t rsa = make_rsrc(as, (size_t)M * KS);
+  const __amdgpu_buffer_rsrc_t rsb = make_rsrc(bs, (size_t)N * KS);
+  // Load-side lane offsets: row 8 blk + lane / 8 of the tile, chunk (lane % 8) ^ ((row >> 1) & 7);
+  // (row >> 1) & 7 = 4 (blk & 1) + lane / 16, so even and odd blocks need one offset each and
+  // the block's 8 blk * K goes into the uniform soffset.
+  const int lr = lane >> 3;
+  const uint32_t ce = (uint32_t)(16 * ((lane & 7) ^ (lane >> 4)));
+  const uint32_t co = (uint32_t)(16 * ((lane & 7) ^ (4 + (lane >> 4))));
+  const uint32_t va_e = (uint32_t)((m0 + lr) * K) + ce, va_o = (uint32_t)((m0 + lr) * K) + co;
+  const uint32_t vb_e = (uint32_t)((n0 + lr) * K) + ce, vb_o = (uint32_t)((n0 + lr) * K) + co;
+  const uint32_t vsa = (uint32_t)((m0 + 64 * wave + lane) * KS);
+  const uint32_t vsb = (uint32_t)((n0 + 64 * wave + lane) * KS);
+
+  typedef __attribute__((address_space(3))) void* lds_t;
+  // Wave w loads A and B blocks 8w .. 8w + 7 and the scale dwords of rows 64w .. 64w + 63.
+  auto issue = [&](uint8_t* LA, uint8_t* LB, uint32_t* LS, int kt) {
+    const int k0 = (kt_begin + kt) * XBK;
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rsa, (lds_t)(LS + 64 * wu), 4, vsa, k0 / 32, 0, 0);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rsb, (lds_t)(LS + DBM + 64 * wu), 4, vsb, k0 / 32, 0, 0);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int blk = 8 * wu + j;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (lds_t)(LA + 1024 * blk), 16, (j & 1) ? va_o : va_e,
+                                               8 * blk * K + k0, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rb, (lds_t)(LB + 1024 * blk), 16, (j & 1) ? vb_o : vb_e,
+                                               8 * blk * K + k0, 0, kBufNT);
+    }
+  };
+
+  // Read-side lane offsets: fragment row r = base + fr (base a multiple of 32), so the swizzle
+  // term is (fr >> 1) & 7; chunk 4 kk + fg (+ 2 for the second 16 bytes).
+  const int fr = lane & 31, fg = lane >> 5;
+  const int sw = (fr >> 1) & 7;
+  int oa[2][2], ob[2][2];
+#pragma unroll
+  for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int c = 16 * ((4 * kk + fg + 2 * h) ^ sw);
+      oa[kk][h] = (wm * 128 + fr) * XBK + c;
+      ob[kk][h] = (wn * 128 + fr) * XBK + c;
+    }
+  struct Frags {
+    kbh_u32x4 a0[4], a1[4], b0[4], b1[4];
+  };
+  struct Scales {
+    uint32_t sa[4], sb[4];
+  };
+  auto read_frags = [&](Frags& f, const uint8_t* LA, const uint8_t* LB, int kk) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      f.a0[i] = *reinterpret_cast<const kbh_u32x4*>(LA + oa[kk][0] + i * 32 * XBK);
+      f.a1[i] = *reinterpret_cast<const kbh_u32x4*>(LA + oa[kk][1] + i * 32 * XBK);
+      f.b0[i] = *reinterpret_cast<const kbh_u32x4*>(LB + ob[kk][0] + i * 32 * XBK);
+      f.b1[i] = *reinterpret_cast<const kbh_u32x4*>(LB + ob[kk][1] + i * 32 * XBK);
+    }
+  };
+  auto read_scales = [&](Scales& sc, const uint32_t* LS) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      sc.sa[i] = LS[wm * 128 + i * 32 + fr];
+      sc.sb[i] = LS[DBM + wn * 128 + i * 32 + fr];
+    }
+  };
+  kbh_f32x16 accv[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) accv[i][j][e] = 0.f;
+  auto mma = [&](const Frags& f, int kk, const Scales& sc) {
+    const int sh = 8 * (2 * kk + fg);
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        accv[i][j] = mfma_mx32(f.a0[i], f.a1[i], f.b0[j], f.b1[j], accv[i][j],
+                               (int)((sc.sa[i] >> sh) & 0xffu), (int)((sc.sb[j] >> sh) & 0xffu));
+  };
+
+  // vmcnt(0) with the other counters left alone (gfx9 s_waitcnt encoding).
+  constexpr int kWaitVm0 = 0x0F70;
+  Frags f0, f1;
+  Scales scur, snext;
+  issue(La0, Lb0, Ls0, 0);
+  issue(La1, Lb1, Ls1, min(1, KT - 1));
+  __builtin_amdgcn_s_waitcnt(kWaitVm0);
+  __syncthreads();
+  read_scales(scur, Ls0);
+  read_frags(f0, La0, Lb0, 0);
+  // Slab kt in buffer P = kt & 1 (Q = the other): read its step-1 fragments, run its step-0
+  // MFMAs, wait for this wave's loads of slab kt + 1 (buffer Q), barrier (every wave is done
+  // with buffer P and slab kt + 1 is complete), read slab kt + 1's scales and step-0 fragments,
+  // start slab kt + 2's loads into buffer P, run step 1.
+  auto slab = [&](auto par, int kt) {
+    constexpr int P = decltype(par)::value;
+    uint8_t* const LAp = P ? La1 : La0;
+    uint8_t* const LBp = P ? Lb1 : Lb0;
+    uint32_t* const LSp = P ? Ls1 : Ls0;
+    const uint8_t* const LAq = P ? La0 : La1;
+    const uint8_t* const LBq = P ? Lb0 : Lb1;
+    const uint32_t* const LSq = P ? Ls0 : Ls1;
+    read_frags(f1, LAp, LBp, 1);
+    mma(f0, 0, scur);
+#pragma unroll
+    for (int q = 0; q < 16; ++q) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // one LDS read
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_waitcnt(kWaitVm0);
+    __syncthreads();
+    __builtin_amdgcn_sched_barrier(0);
+    read_scales(snext, LSq);
+    read_frags(f0, LAq, LBq, 0);
+    issue(LAp, LBp, LSp, min(kt + 2, KT - 1));
+    mma(f1, 1, scur);
+    __builtin_amdgcn_sched_barrier(0);
+    scur = snext;
+  };
+  for (int kt0 = 0; kt0 < KT; kt0 += 2) {
+    slab(std::integral_constant<int, 0>{}, kt0);
+    slab(std::integral_constant<int, 1>{}, kt0 + 1);
+  }
+
+  // Accumulator element e of tile (i, j): row 8(e/4) + 4(l/32) + e%4, column l%32.
+  const bool full = m0 + DBM <= M;  // no row of the tile lies past M
+  auto for_each = [&](auto&& f) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+          const int r = m0 + wm * 128 + i * 32 + 8 * (e >> 2) + 4 * fg + (e & 3);
+          const int n = n0 + wn * 128 + j * 32 + fr;
+          if (full || r < M) f(i, j, e, (size_t)r * N + n);
+        }
+  };
+  if (splits == 1) {
+    for_each([&](int i, int j, int e, size_t o) { y[o] = f32_to_half_bits<BF16>(accv[i][j][e]); });
+    return;
+  }
+  float* slice = acc + (size_t)split * M * N;
+  for_each([&](int i, int j, int e, size_t o) { slice[o] = accv[i][j][e]; });
+}
+
+#ifndef KBH_MX_DMA_MIN_M
+#define KBH_MX_DMA_MIN_M 1024
+#endif
+
 struct MXPlan {
+  bool dma;  // 256 x 256 tiles (mxfp8_dma_kernel)
   int wnt, tiles, splits, slabs_per_split;
 };
 
 MXPlan plan_mx(int M, int N, int K) {
   MXPlan p;
+  p.dma = M >= KBH_MX_DMA_MIN_M && N % DBM == 0;
   const int mblocks = (M + XBM - 1) / XBM;
   p.wnt = (mblocks * (N / 256) >= 128 && N % 256 == 0) ? 4 : 1;
-  p.tiles = mblocks * (N / (64 * p.wnt));
+  p.tiles = p.dma ? ((M + DBM - 1) / DBM) * (N / DBM) : mblocks * (N / (64 * p.wnt));
   const int slabs = K / XBK;
   // Split K only while the grid is below one workgroup per CU; every split keeps a multiple of
   // XDEPTH slabs (branch-free ring) and at least 4 slabs.
@@ -271,7 +476,11 @@ template <bool BF16>
 int mx_launch(const MXPlan& p, const void* a, const void* as, const void* b, const void* bs,
               void* y, float* acc, int M, int N, int K, hipStream_t st) {
   const dim3 grid(p.tiles, 1, p.splits);
-  if (p.wnt == 4)
+  if (p.dma)
+    hipLaunchKernelGGL((mxfp8_dma_kernel<BF16>), grid, dim3(256), 0, st, (const uint8_t*)a,
+                       (const uint8_t*)as, (const uint8_t*)b, (const uint8_t*)bs, (uint16_t*)y,
+                       acc, M, N, K, p.slabs_per_split);
+  else if (p.wnt == 4)
     hipLaunchKernelGGL((mxfp8_kernel<4, BF16>), grid, dim3(256), 0, st, (const uint8_t*)a,
                        (const uint8_t*)as, (const uint8_t*)b, (const uint8_t*)bs, (uint16_t*)y,
                        acc, M, N, K, p.slabs_per_split);

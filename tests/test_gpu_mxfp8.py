@@ -14,8 +14,10 @@ def _gt(a, sa, b, sb, acc=np.float64):
     return om.forward(a.numpy(), sa.numpy(), b.numpy(), sb.numpy(), accumulate=acc)
 
 
+# (1024, 1024, 256) and (1100, 2048, 512) take the 256 x 256 LDS-DMA tiles (the second with a
+# partial last row block); the others the 128-row tiles.
 CASES = [(1, 256, 64), (16, 1024, 256), (100, 2048, 320), (128, 4096, 512), (300, 1024, 1024),
-         (513, 512, 256)]
+         (513, 512, 256), (1024, 1024, 256), (1100, 2048, 512)]
 
 
 @pytest.mark.parametrize("M,K,N", CASES)
@@ -29,10 +31,12 @@ def test_mxfp8_parity(dev, M, K, N, out):
     assert cmp.ok, cmp
 
 
-def test_mxfp8_e8m0_decode_bit_exact(dev):
+@pytest.mark.parametrize("M,N", [(64, 128), (1024, 256)])
+def test_mxfp8_e8m0_decode_bit_exact(dev, M, N):
     """All elements 1.0 with per-block exponents in [124, 128]: every partial sum is exact in
-    fp32, so y must equal the oracle's exactly (tests the e8m0 decode and its block mapping)."""
-    M, N, K = 64, 128, 2048
+    fp32, so y must equal the oracle's exactly (tests the e8m0 decode and its block mapping, on
+    the 128-row and the 256 x 256 tiles)."""
+    K = 2048
     g = torch.Generator().manual_seed(9)
     a = torch.full((M, K), 0x38, dtype=torch.uint8)
     b = torch.full((N, K), 0x38, dtype=torch.uint8)
