@@ -23,7 +23,7 @@ def _capture(fn, args):
     return g, st, out
 
 
-@pytest.mark.parametrize("op", ["w4a16_decode", "w4a16_wide", "w8a8"])
+@pytest.mark.parametrize("op", ["w4a16_decode", "w4a16_wide", "w8a8", "mxfp8_dma"])
 def test_replay_after_pool_growth(dev, op):
     print(f"[graph] {op}", flush=True)
     if op == "w4a16_decode":      # split-K workspace
@@ -34,6 +34,10 @@ def test_replay_after_pool_growth(dev, op):
         small = [t.to(dev) for t in inputs.w4a16(64, 2048, 512, seed=3)]
         big = [t.to(dev) for t in inputs.w4a16(64, 14336, 4096, seed=4)]
         fn = ops.w4a16_gemm
+    elif op == "mxfp8_dma":       # split-K workspace of the 256 x 256 LDS-DMA tiles
+        small = [t.to(dev) for t in inputs.mxfp8(1024, 1024, 256, seed=7)]
+        big = [t.to(dev) for t in inputs.mxfp8(2048, 14336, 4096, seed=8)]
+        fn = ops.mxfp8_gemm
     else:
         small = [t.to(dev) for t in inputs.w8a8(16, 2048, 512, seed=5)]
         big = [t.to(dev) for t in inputs.w8a8(16, 14336, 4096, seed=6)]
