@@ -61,6 +61,10 @@ namespace kbh {
 
 constexpr int WSLAB_BYTES = 64;  // bytes of K per row per slab
 
+#ifndef KBH_WIDE_SPLIT_PRODUCER
+#define KBH_WIDE_SPLIT_PRODUCER 1
+#endif
+
 template <bool B>
 struct WideFlag {
   static constexpr bool value = B;
@@ -293,6 +297,14 @@ tiled_wide_gemm(
   // 993 -> 974 us); with 256-row tiles the second copy of the loop spilled registers and ran
   // no faster.
   constexpr bool kFast = BP::kHasFast && (TM == 64 || TM == 128);
+  // SP (split producer; 64-row tiles): the producer of a slab runs in two halves, the first
+  // beside the step-1 MFMAs of the slab two before it (into the LDS buffer whose step-1
+  // fragments were read before that slab's barrier), the second beside the step-0 MFMAs of the
+  // slab before it, instead of all of it beside the step-0 MFMAs, whose time it doubled. Needs
+  // raw weights two slabs ahead (PD >= 2). Measured: W4A16 M=64 31.1 -> 29.8 us; on 128-row
+  // tiles M=256 55.2 -> 55.9 us and the MoE FFN 982 -> 972 us, so those keep the one-piece
+  // producer.
+  constexpr bool SP = KBH_WIDE_SPLIT_PRODUCER && TM == 64 && PD >= 2 && BP::kParts % 2 == 0;
   bool fast = false;
   if constexpr (kFast) fast = __syncthreads_and(bp.scan_fast(kt0 * SK, (kt0 + KT) * SK, n0, t)) != 0;
   auto run = [&](auto fast_tag) {
@@ -316,6 +328,18 @@ tiled_wide_gemm(
 #pragma unroll
     for (int i = 1; i <= PD; ++i) load_b(R[i % PD], min(i, last));
     load_g(G[1], min(SPG, last));
+    constexpr int NP = BP::kParts, HP = NP / 2;
+    if constexpr (SP) {
+      // First half of slab 1 into buffer 1. With one slab per group, slab 1 starts the second
+      // group (set 1), and set 0 (slab 0's, done) is reloaded with the group of slab 2.
+      if constexpr (SPG == 1) {
+        bp.template prepare_group<FAST>(G[1]);
+        load_g(G[0], min(2, last));
+      }
+#pragma unroll
+      for (int p = 0; p < HP; ++p)
+        bp.template store_part<FAST>(R[1 % PD], G[SPG == 1 ? 1 : 0], Bs[1], t, p);
+    }
     kbh_u32x4 a0[RB], a1[RB];  // A fragments of step 0 (of the slab after next's barrier) / 1
     if constexpr (XS) stage_a(A[0], 0);
     __syncthreads();
@@ -330,10 +354,50 @@ tiled_wide_gemm(
     // a slab is fixed with scheduling barriers (the scheduler otherwise clusters the
     // dequantisation and moves MFMAs across s_barrier).
     constexpr int NMF = RB * CB;  // MFMAs per k16 step
-    constexpr int NP = BP::kParts;
     for (int kt = 0; kt < KT; kt += U) {
 #pragma unroll
       for (int u = 0; u < U; ++u) {
+        if constexpr (SP) {
+          // Slab s: step 0 beside the second half of slab s+1 (buffer 1-cur), barrier, step 1
+          // beside the first half of slab s+2 (buffer cur, whose slab-s fragments are in
+          // registers). Group sets: slab x uses set (x / SPG) & 1 (U is a multiple of 2 SPG);
+          // when slab s+2 starts a group, its set is prepared before its first half and the
+          // other set (slab s+1's group, finished in step 0) is reloaded with the group after.
+          const int s = kt + u;
+          const int cur = u & 1;
+          const int ra = u % PD, rr = (u + 1) % PD, r2 = (u + 2) % PD;
+          const int g1 = ((u + 1) / SPG) & 1, g2 = ((u + 2) / SPG) & 1;
+          const bool new2 = (u + 2) % SPG == 0;
+          read_b(b1, cur, 1);
+          frag_a(a1, A[ra], u & 1, 1);
+          __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+          for (int p = 0; p < HP; ++p) {
+            mma_range(a0, b0, p * NMF / HP, (p + 1) * NMF / HP);
+            __builtin_amdgcn_sched_barrier(0);
+            bp.template store_part<FAST>(R[rr], G[g1], Bs[1 - cur], t, HP + p);
+            __builtin_amdgcn_sched_barrier(0);
+          }
+          __syncthreads();
+          __builtin_amdgcn_sched_barrier(0);
+          read_b(b0, 1 - cur, 0);  // step 0 of slab s+1
+          if constexpr (XS) stage_a(A[(u + 1) % PD], (u + 1) & 1);
+          frag_a(a0, A[(u + 1) % PD], (u + 1) & 1, 0);
+          if (new2) bp.template prepare_group<FAST>(G[g2]);
+          load_a_step(A[ra], min(s + PD, last), 0);
+          load_b(R[rr], min(s + 1 + PD, last));  // slab s+1 is fully produced
+          if (new2) load_g(G[g2 ^ 1], min(s + 2 + SPG, last));
+          load_a_step(A[ra], min(s + PD, last), 1);
+          __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+          for (int p = 0; p < HP; ++p) {
+            mma_range(a1, b1, p * NMF / HP, (p + 1) * NMF / HP);
+            __builtin_amdgcn_sched_barrier(0);
+            bp.template store_part<FAST>(R[r2], G[g2], Bs[cur], t, p);  // slab s+2
+            __builtin_amdgcn_sched_barrier(0);
+          }
+          continue;
+        }
         const int s = kt + u;  // slab in registers / LDS buffer u&1
         const int cur = u & 1;
         const int ra = u % PD, rr = (u + 1) % PD;  // ring slots of slab s (A) and s+1 (raw)
