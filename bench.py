@@ -54,9 +54,9 @@ def w4a16_bytes(M, K=K_DIM, N=N_DIM, G=GROUP):
 # every kbh:: kernel of the call. Table and commands: profiles/hbm_traffic_all_records.md.
 PMC_TRAFFIC = {
     "w4a16 M=1": 32_167_648, "w4a16 M=4": 34_454_252, "w4a16 M=16": 42_545_554,
-    "w4a16 M=64": 64_031_899, "w4a16 M=256": 108_180_696, "w4a16 M=1024": 240_722_352,
+    "w4a16 M=64": 65_934_336, "w4a16 M=256": 108_180_696, "w4a16 M=1024": 240_722_352,
     "w4a16 M=2048": 340_853_600, "w8a8 M=16": 68_182_320, "w8a8 M=512": 210_735_483,
-    "mxfp8 M=128": 94_936_720, "mxfp8 M=2048": 290_080_130,
+    "mxfp8 M=128": 94_936_720, "mxfp8 M=2048": 483_042_099,
     "fp8w (reference op) M=16 b128": 70_943_466,
     "qmoe_ffn T=512 D=4096 F=14336 E=8 top2": 1_229_346_633,
     "silu_fp8 (reference op) T=512 H=14336 g128": 61_112_077,
