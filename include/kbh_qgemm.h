@@ -145,7 +145,8 @@ int kbh_fp8w_gemm(const void* x, const uint8_t* w_fp8, const void* scales, void*
  *   y [M, N] out_dtype,  y[m, n] = sum_k a[m,k] 2^(a_scale[m,k/32]-127) b[n,k] 2^(b_scale[n,k/32]-127)
  * Requirements: M >= 1, N % 64 == 0, K % 256 == 0, M*K and N*K below 2^31 (32-bit buffer
  * offsets), a/b/y 16-byte and scales 4-byte aligned.
- * workspace: used when K is split across workgroups (small M); same contract as for
+ * workspace: used when K is split across workgroups, i.e. when the output tiles alone would fill
+ * fewer than 256 workgroups (at N = 4096: every M up to 2048); same contract as for
  * kbh_w4a16_gemm, size from kbh_mxfp8_workspace_bytes().
  */
 size_t kbh_mxfp8_workspace_bytes(int M, int N, int K);
