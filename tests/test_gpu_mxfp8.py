@@ -14,11 +14,12 @@ def _gt(a, sa, b, sb, acc=np.float64):
     return om.forward(a.numpy(), sa.numpy(), b.numpy(), sb.numpy(), accumulate=acc)
 
 
-# (1024, 1024, 256), (1100, 2048, 512) and (2000, 512, 4096) take the 256 x 256 LDS-DMA tiles
-# (the last two with a partial last row block, the last one without a K split); the others the
-# 128-row tiles.
+# (1024, 1024, 256), (1100, 2048, 512), (2000, 512, 4096) and (1024, 256, 512) take the 256 x 256
+# LDS-DMA tiles (the second and third with a partial last row block, the last two without a K
+# split, the last one with the minimum K: one pair of slabs); the others the 128-row tiles.
 CASES = [(1, 256, 64), (16, 1024, 256), (100, 2048, 320), (128, 4096, 512), (300, 1024, 1024),
-         (513, 512, 256), (1024, 1024, 256), (1100, 2048, 512), (2000, 512, 4096)]
+         (513, 512, 256), (1024, 1024, 256), (1100, 2048, 512), (2000, 512, 4096),
+         (1024, 256, 512)]
 
 
 @pytest.mark.parametrize("M,K,N", CASES)
