@@ -14,7 +14,8 @@
 // the DS partials in order and rounds lo to dtype, sums the GEMM's slices in split order (or
 // reads base from y) and rounds base, and writes dtype(base + dtype(lo @ B)) (four columns per
 // thread). Adapter ids index as torch does (reference.py:14-16, A[lora_ids]): an id in [-L, 0)
-// selects adapter id + L. Ids outside [-L, L), for which torch raises, are clamped to [0, L).
+// selects adapter id + L. An id outside [-L, L), for which torch raises, makes its output row
+// NaN (the adapter reads stay in bounds on adapter 0 or L - 1): no plausible wrong values.
 #include "byte_weight_gemm.h"
 
 namespace kbh {
@@ -24,6 +25,10 @@ constexpr int kLoraMaxRank = 64;
 constexpr int kLoraThreads = 256;
 constexpr int kLoraMaxSplits = 16;  // D ranges of the shrink
 
+__device__ inline bool lora_id_valid(const int64_t* ids, int t, int L) {
+  const int64_t v = ids[t];
+  return v >= -(int64_t)L && v < (int64_t)L;
+}
 __device__ inline int lora_id(const int64_t* ids, int t, int L) {
   int64_t v = ids[t];
   if (v < 0 && v >= -(int64_t)L) v += L;
@@ -135,6 +140,7 @@ __global__ __launch_bounds__(kLoraThreads) void lora_expand_add_kernel(
       for (int c = 0; c < 4; ++c)
         acc[c] += los[j + u] * half_bits_to_f32<BF16>((uint16_t)(b[u][c >> 1] >> (16 * (c & 1))));
   }
+  const float bad = lora_id_valid(ids, t, L) ? 0.f : __builtin_nanf("");
   kbh_u32x2 out;
 #pragma unroll
   for (int h = 0; h < 2; ++h) {
@@ -142,7 +148,7 @@ __global__ __launch_bounds__(kLoraThreads) void lora_expand_add_kernel(
 #pragma unroll
     for (int c = 0; c < 2; ++c) {
       const float e = half_bits_to_f32<BF16>(f32_to_half_bits<BF16>(acc[2 * h + c]));
-      v[c] = keep_f32(bs[2 * h + c] + e);
+      v[c] = keep_f32(bs[2 * h + c] + e) + bad;
     }
     out[h] = (uint32_t)f32_to_half_bits<BF16>(v[0]) | ((uint32_t)f32_to_half_bits<BF16>(v[1]) << 16);
   }
