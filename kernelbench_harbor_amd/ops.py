@@ -55,9 +55,12 @@ workspaces = _WorkspacePool()
 scratches = _WorkspacePool()
 
 
-def _require(cond: bool, msg: str) -> None:
+def _require(cond: bool, msg) -> None:
+    """Raises ValueError(msg) when cond is false; msg may be a callable returning the text, so
+    that a formatted message costs nothing on the passing path (~0.4 us per f-string, several
+    per call of a decode-sized op)."""
     if not cond:
-        raise ValueError(msg)
+        raise ValueError(msg() if callable(msg) else msg)
 
 
 # torch's current-stream handle as a plain integer: the raw accessor costs ~0.1 us where
@@ -75,9 +78,9 @@ def _stream_ptr(device: torch.device) -> int:
 
 def _check_device(*tensors: torch.Tensor) -> torch.device:
     dev = tensors[0].device
-    _require(dev.type == "cuda", f"tensors must be on a HIP device, got {dev}")
+    _require(dev.type == "cuda", lambda: f"tensors must be on a HIP device, got {dev}")
     for t in tensors[1:]:
-        _require(t.device == dev, f"all tensors must be on {dev}, got {t.device}")
+        _require(t.device == dev, lambda: f"all tensors must be on {dev}, got {t.device}")
     return dev
 
 
@@ -117,17 +120,18 @@ def w4a16_gemm(x: torch.Tensor, qweight: torch.Tensor, scales: torch.Tensor,
     # and a reshape ~1.5 us, a large share of a decode-sized call.
     xd = x.dtype
     code = _DT_CODE.get(xd)
-    _require(code is not None, f"x must be float16 or bfloat16, got {xd}")
-    _require(qweight.dtype == torch.int32, f"qweight must be int32, got {qweight.dtype}")
+    _require(code is not None, lambda: f"x must be float16 or bfloat16, got {xd}")
+    _require(qweight.dtype == torch.int32, lambda: f"qweight must be int32, got {qweight.dtype}")
     xs, qs, ss, zs = x.shape, qweight.shape, scales.shape, zeros.shape
     _require(len(qs) == 2 and len(ss) == 2 and len(zs) == 2,
              "qweight, scales and zeros must be 2-D")
     K, NP = qs
     N = NP * 8
-    _require(len(xs) >= 1 and xs[-1] == K, f"x last dim {tuple(xs)[-1:]} != qweight rows {K}")
+    _require(len(xs) >= 1 and xs[-1] == K,
+             lambda: f"x last dim {tuple(xs)[-1:]} != qweight rows {K}")
     _require(ss[1] == N and zs == ss,
-             f"scales/zeros must be [K/G, {N}], got {tuple(ss)} / {tuple(zs)}")
-    _require(ss[0] > 0 and K % ss[0] == 0, f"K={K} not divisible by scales rows {ss[0]}")
+             lambda: f"scales/zeros must be [K/G, {N}], got {tuple(ss)} / {tuple(zs)}")
+    _require(ss[0] > 0 and K % ss[0] == 0, lambda: f"K={K} not divisible by scales rows {ss[0]}")
     group = K // ss[0]
     _require(scales.dtype == xd and zeros.dtype == xd, "scales and zeros must have x's dtype")
     dev = _check_device(x, qweight, scales, zeros)
@@ -154,11 +158,11 @@ def w4a16_gemm(x: torch.Tensor, qweight: torch.Tensor, scales: torch.Tensor,
 def _w8a8_args(x_int8, w_int8):
     """(x as [M, K], M, N, K, whether x was already 2-D)."""
     _require(x_int8.dtype == torch.int8 and w_int8.dtype == torch.int8,
-             f"x_int8/w_int8 must be int8, got {x_int8.dtype}/{w_int8.dtype}")
+             lambda: f"x_int8/w_int8 must be int8, got {x_int8.dtype}/{w_int8.dtype}")
     xs, wsh = x_int8.shape, w_int8.shape
     _require(len(wsh) == 2, "w_int8 must be [K, N]")
     K, N = wsh
-    _require(len(xs) >= 1 and xs[-1] == K, f"x_int8 last dim {tuple(xs)[-1:]} != K={K}")
+    _require(len(xs) >= 1 and xs[-1] == K, lambda: f"x_int8 last dim {tuple(xs)[-1:]} != K={K}")
     if len(xs) == 2:
         return x_int8, xs[0], N, K, True
     x2 = x_int8.reshape(-1, K)
@@ -175,7 +179,7 @@ def w8a8_gemm(x_int8: torch.Tensor, w_int8: torch.Tensor, x_scale: torch.Tensor,
     _require(x_scale.dtype == torch.float16 and w_scale.dtype == torch.float16,
              "x_scale and w_scale must be float16")
     _require(x_scale.numel() == M and w_scale.numel() == N,
-             f"x_scale must hold {M} values and w_scale {N}")
+             lambda: f"x_scale must hold {M} values and w_scale {N}")
     dev = _check_device(x_int8, w_int8, x_scale, w_scale)
     y = torch.empty((M, N), dtype=torch.float16, device=dev)
     if M > 0:
@@ -220,16 +224,16 @@ def fp8w_gemm(x: torch.Tensor, w_fp8: torch.Tensor, scales: torch.Tensor) -> tor
     K / scales.shape[0]."""
     xd = x.dtype
     code = _DT_CODE.get(xd)
-    _require(code is not None, f"x must be float16 or bfloat16, got {xd}")
+    _require(code is not None, lambda: f"x must be float16 or bfloat16, got {xd}")
     _require(w_fp8.dtype in (torch.float8_e4m3fn, torch.uint8),
-             f"w_fp8 must be float8_e4m3fn (or its uint8 bits), got {w_fp8.dtype}")
+             lambda: f"w_fp8 must be float8_e4m3fn (or its uint8 bits), got {w_fp8.dtype}")
     xs, wsh, ss = x.shape, w_fp8.shape, scales.shape
     _require(len(wsh) == 2 and len(ss) == 2, "w_fp8 and scales must be 2-D")
     K, N = wsh
-    _require(len(xs) >= 1 and xs[-1] == K, f"x last dim {tuple(xs)[-1:]} != K={K}")
-    _require(scales.dtype == torch.float16, f"scales must be float16, got {scales.dtype}")
+    _require(len(xs) >= 1 and xs[-1] == K, lambda: f"x last dim {tuple(xs)[-1:]} != K={K}")
+    _require(scales.dtype == torch.float16, lambda: f"scales must be float16, got {scales.dtype}")
     _require(ss[1] == N and ss[0] > 0 and K % ss[0] == 0,
-             f"scales must be [K/B, {N}], got {tuple(ss)}")
+             lambda: f"scales must be [K/B, {N}], got {tuple(ss)}")
     block = K // ss[0]
     dev = _check_device(x, w_fp8, scales)
     flat = len(xs) == 2
@@ -258,18 +262,19 @@ def mxfp8_gemm(a: torch.Tensor, a_scale: torch.Tensor, b: torch.Tensor, b_scale:
 
     a [M, K] and b [N, K] are float8_e4m3fn (or their uint8 bits), K-contiguous; a_scale
     [M, K/32] and b_scale [N, K/32] are e8m0 codes (uint8, or float8_e8m0fnu)."""
-    _require(out_dtype in _DT_CODE, f"out_dtype must be float16 or bfloat16, got {out_dtype}")
+    _require(out_dtype in _DT_CODE,
+             lambda: f"out_dtype must be float16 or bfloat16, got {out_dtype}")
     _require(a.dtype in _BYTE_DTYPES and b.dtype in _BYTE_DTYPES,
-             f"a and b must be float8_e4m3fn or uint8, got {a.dtype}/{b.dtype}")
+             lambda: f"a and b must be float8_e4m3fn or uint8, got {a.dtype}/{b.dtype}")
     _require(a_scale.dtype in _SCALE_DTYPES and b_scale.dtype in _SCALE_DTYPES,
              "scales must be e8m0 codes (uint8)")
     ash, bsh = a.shape, b.shape
     _require(len(ash) == 2 and len(bsh) == 2, "a and b must be 2-D")
     M, K = ash
     N = bsh[0]
-    _require(bsh[1] == K, f"b must be [N, {K}], got {tuple(bsh)}")
+    _require(bsh[1] == K, lambda: f"b must be [N, {K}], got {tuple(bsh)}")
     _require(K % 32 == 0 and a_scale.shape == (M, K // 32) and b_scale.shape == (N, K // 32),
-             f"scales must be [M, K/32] and [N, K/32]")
+             lambda: f"scales must be [M, K/32] and [N, K/32]")
     dev = _check_device(a, a_scale, b, b_scale)
     y = torch.empty((M, N), dtype=out_dtype, device=dev)
     if M == 0:
@@ -291,18 +296,19 @@ _LOGIT_CODE = {torch.float16: 0, torch.bfloat16: 1, torch.float32: 2}
 
 def _check_logits(router_logits, T):
     _require(router_logits.dtype in _LOGIT_CODE,
-             f"router_logits must be float16, bfloat16 or float32, got {router_logits.dtype}")
+             lambda: (f"router_logits must be float16, bfloat16 "
+                      f"or float32, got {router_logits.dtype}"))
     _require(router_logits.dim() == 2 and router_logits.shape[0] == T,
-             f"router_logits must be [{T}, E], got {tuple(router_logits.shape)}")
+             lambda: f"router_logits must be [{T}, E], got {tuple(router_logits.shape)}")
     E = router_logits.shape[1]
-    _require(2 <= E <= 256, f"number of experts must be in [2, 256], got {E}")
+    _require(2 <= E <= 256, lambda: f"number of experts must be in [2, 256], got {E}")
     return E
 
 
 def moe_route_top2(router_logits: torch.Tensor, dtype: torch.dtype = torch.float16):
     """(topi [T, 2] int32, topw [T, 2] dtype): softmax(fp32 logits), top-2, renormalised
     (tasks/fused_qmoe/*/environment/reference.py:14-16)."""
-    _require(dtype in _DT_CODE, f"dtype must be float16 or bfloat16, got {dtype}")
+    _require(dtype in _DT_CODE, lambda: f"dtype must be float16 or bfloat16, got {dtype}")
     T = router_logits.shape[0]
     E = _check_logits(router_logits, T)
     dev = _check_device(router_logits)
@@ -325,15 +331,17 @@ def qmoe(x: torch.Tensor, qweight: torch.Tensor, scales: torch.Tensor,
     """Top-2 quantized MoE of tasks/fused_qmoe/fused_qmoe__mixtral__fp16/environment/
     reference.py:11-21: x [T, D], qweight [E, D, N] int8 (int4 values), scales [E, D/G, N] in
     x.dtype, router_logits [T, E]; G = D / scales.shape[1]."""
-    _require(x.dtype in _DT_CODE, f"x must be float16 or bfloat16, got {x.dtype}")
+    _require(x.dtype in _DT_CODE, lambda: f"x must be float16 or bfloat16, got {x.dtype}")
     _require(x.dim() == 2, "x must be [T, D]")
     T, D = x.shape
     _require(qweight.dtype == torch.int8 and qweight.dim() == 3 and qweight.shape[1] == D,
-             f"qweight must be int8 [E, {D}, N], got {qweight.dtype} {tuple(qweight.shape)}")
+             lambda: (f"qweight must be int8 [E, {D}, N], got "
+                      f"{qweight.dtype} {tuple(qweight.shape)}"))
     E, _, N = qweight.shape
     _require(scales.dtype == x.dtype and scales.dim() == 3 and scales.shape[0] == E and
              scales.shape[2] == N and D % scales.shape[1] == 0,
-             f"scales must be x.dtype [E, D/G, N], got {scales.dtype} {tuple(scales.shape)}")
+             lambda: (f"scales must be x.dtype [E, D/G, N], got "
+                      f"{scales.dtype} {tuple(scales.shape)}"))
     group = D // scales.shape[1]
     _require(_check_logits(router_logits, T) == E, "router_logits must have E columns")
     dev = _check_device(x, qweight, scales, router_logits)
@@ -361,12 +369,12 @@ def qmoe_ffn(x, router_logits, gate_qweight, gate_scales, gate_zeros, up_qweight
     T, D = x.shape
     E = _check_logits(router_logits, T)
     _require(gate_qweight.dtype == torch.int32 and gate_qweight.dim() == 3 and
-             gate_qweight.shape[:2] == (E, D), f"gate_qweight must be int32 [E, D, F/8]")
+             gate_qweight.shape[:2] == (E, D), lambda: f"gate_qweight must be int32 [E, D, F/8]")
     F = gate_qweight.shape[2] * 8
     _require(up_qweight.shape == gate_qweight.shape and up_qweight.dtype == torch.int32,
              "up_qweight must match gate_qweight")
     _require(down_qweight.dtype == torch.int32 and tuple(down_qweight.shape) == (E, F, D // 8),
-             f"down_qweight must be int32 [E, {F}, {D // 8}]")
+             lambda: f"down_qweight must be int32 [E, {F}, {D // 8}]")
     group = D // gate_scales.shape[1]
     for name, t_, shape in [("gate_scales", gate_scales, (E, D // group, F)),
                             ("gate_zeros", gate_zeros, (E, D // group, F)),
@@ -375,7 +383,7 @@ def qmoe_ffn(x, router_logits, gate_qweight, gate_scales, gate_zeros, up_qweight
                             ("down_scales", down_scales, (E, F // group, D)),
                             ("down_zeros", down_zeros, (E, F // group, D))]:
         _require(t_.dtype == x.dtype and tuple(t_.shape) == shape,
-                 f"{name} must be x.dtype {shape}, got {t_.dtype} {tuple(t_.shape)}")
+                 lambda: f"{name} must be x.dtype {shape}, got {t_.dtype} {tuple(t_.shape)}")
     ts = [x, gate_qweight, gate_scales, gate_zeros, up_qweight, up_scales, up_zeros,
           down_qweight, down_scales, down_zeros]
     dev = _check_device(router_logits, *ts)
@@ -403,14 +411,14 @@ def silu_fp8_quant(y: torch.Tensor, group: int = 128, return_codes: bool = False
     returns fp32(q) * scale as float32 [T, H]. With ``return_codes`` also returns the codes
     (torch.float8_e4m3fn [T, H]) and the scales (float32 [T, H / group]).
     """
-    _require(y.dtype in _DT_CODE, f"y must be float16 or bfloat16, got {y.dtype}")
-    _require(y.dim() == 2, f"y must be 2-D [T, 2H], got {tuple(y.shape)}")
+    _require(y.dtype in _DT_CODE, lambda: f"y must be float16 or bfloat16, got {y.dtype}")
+    _require(y.dim() == 2, lambda: f"y must be 2-D [T, 2H], got {tuple(y.shape)}")
     T, H2 = y.shape
-    _require(H2 % 2 == 0, f"y's last dim {H2} must be even (gate and up halves)")
+    _require(H2 % 2 == 0, lambda: f"y's last dim {H2} must be even (gate and up halves)")
     H = H2 // 2
-    _require(group in (32, 64, 128), f"group must be 32, 64 or 128, got {group}")
+    _require(group in (32, 64, 128), lambda: f"group must be 32, 64 or 128, got {group}")
     # the reference's reshape(T, H // GROUP, GROUP) raises for any other H
-    _require(H % group == 0, f"H={H} must be a multiple of the group size {group}")
+    _require(H % group == 0, lambda: f"H={H} must be a multiple of the group size {group}")
     dev = _check_device(y)
     out = torch.empty((T, H), dtype=torch.float32, device=dev)
     codes = scales = None
@@ -435,10 +443,10 @@ def moe_route_topk(router_logits: torch.Tensor, topk: int, dtype: torch.dtype = 
     """(topi [T, topk] int32, topw [T, topk] dtype): softmax(fp32 logits), top-k in descending
     order (lower index first on a tie), weights renormalised and rounded to dtype
     (tasks/moe/*/environment/reference.py:11-13)."""
-    _require(dtype in _DT_CODE, f"dtype must be float16 or bfloat16, got {dtype}")
+    _require(dtype in _DT_CODE, lambda: f"dtype must be float16 or bfloat16, got {dtype}")
     T = router_logits.shape[0]
     E = _check_logits(router_logits, T)
-    _require(1 <= topk <= min(8, E), f"topk must be in [1, min(8, E={E})], got {topk}")
+    _require(1 <= topk <= min(8, E), lambda: f"topk must be in [1, min(8, E={E})], got {topk}")
     dev = _check_device(router_logits)
     topi = torch.empty((T, topk), dtype=torch.int32, device=dev)
     topw = torch.empty((T, topk), dtype=dtype, device=dev)
@@ -465,11 +473,11 @@ def moe(x: torch.Tensor, w: torch.Tensor, router_logits: torch.Tensor, topk: int
     T, D = x.shape
     E = _check_logits(router_logits, T)
     _require(w.dtype == x.dtype and w.dim() == 3 and w.shape[:2] == (E, D),
-             f"w must be x.dtype [{E}, {D}, H], got {w.dtype} {tuple(w.shape)}")
+             lambda: f"w must be x.dtype [{E}, {D}, H], got {w.dtype} {tuple(w.shape)}")
     H = w.shape[2]
-    _require(1 <= topk <= min(8, E), f"topk must be in [1, min(8, E={E})], got {topk}")
-    _require(D % 128 == 0 and D >= 128, f"D={D} must be a positive multiple of 128")
-    _require(H % 128 == 0 and H >= 128, f"H={H} must be a positive multiple of 128")
+    _require(1 <= topk <= min(8, E), lambda: f"topk must be in [1, min(8, E={E})], got {topk}")
+    _require(D % 128 == 0 and D >= 128, lambda: f"D={D} must be a positive multiple of 128")
+    _require(H % 128 == 0 and H >= 128, lambda: f"H={H} must be a positive multiple of 128")
     dev = _check_device(x, w, router_logits)
     y = torch.empty((T, H), dtype=x.dtype, device=dev)
     if T == 0:
@@ -496,22 +504,26 @@ def lora_qgemm(x: torch.Tensor, qweight: torch.Tensor, scales: torch.Tensor, A: 
     _require(x.dtype in _DT_CODE and x.dim() == 2, "x must be a float16/bfloat16 [T, D] tensor")
     T, D = x.shape
     _require(qweight.dtype == torch.int8 and qweight.dim() == 2 and qweight.shape[0] == D,
-             f"qweight must be int8 [{D}, N], got {qweight.dtype} {tuple(qweight.shape)}")
+             lambda: f"qweight must be int8 [{D}, N], got {qweight.dtype} {tuple(qweight.shape)}")
     N = qweight.shape[1]
     _require(scales.dim() == 2 and scales.shape[1] == N and scales.shape[0] > 0 and
-             D % scales.shape[0] == 0, f"scales must be [D/G, {N}], got {tuple(scales.shape)}")
+             D % scales.shape[0] == 0,
+             lambda: f"scales must be [D/G, {N}], got {tuple(scales.shape)}")
     group = D // scales.shape[0]
     _require(A.dim() == 3 and A.shape[1] == D and B.dim() == 3 and B.shape[0] == A.shape[0] and
              B.shape[1] == A.shape[2] and B.shape[2] == N,
-             f"A must be [L, {D}, r] and B [L, r, {N}], got {tuple(A.shape)} / {tuple(B.shape)}")
+             lambda: (f"A must be [L, {D}, r] and B [L, r, {N}], "
+                      f"got {tuple(A.shape)} / {tuple(B.shape)}"))
     L, r = A.shape[0], A.shape[2]
     for name, t_ in (("scales", scales), ("A", A), ("B", B)):
-        _require(t_.dtype == x.dtype, f"{name} must have x's dtype {x.dtype}, got {t_.dtype}")
+        _require(t_.dtype == x.dtype,
+                 lambda: f"{name} must have x's dtype {x.dtype}, got {t_.dtype}")
     _require(lora_ids.dim() == 1 and lora_ids.shape[0] == T and not lora_ids.is_floating_point(),
-             f"lora_ids must be an integer [{T}] tensor")
-    _require(r in (4, 8, 16, 32, 64), f"rank r must be 4, 8, 16, 32 or 64, got {r}")
-    _require(N % 128 == 0 and D % 32 == 0, f"need N % 128 == 0 and D % 32 == 0 (D={D}, N={N})")
-    _require(group in (32, 64, 128, 256), f"group size {group} not supported")
+             lambda: f"lora_ids must be an integer [{T}] tensor")
+    _require(r in (4, 8, 16, 32, 64), lambda: f"rank r must be 4, 8, 16, 32 or 64, got {r}")
+    _require(N % 128 == 0 and D % 32 == 0,
+             lambda: f"need N % 128 == 0 and D % 32 == 0 (D={D}, N={N})")
+    _require(group in (32, 64, 128, 256), lambda: f"group size {group} not supported")
     dev = _check_device(x, qweight, scales, A, B, lora_ids)
     y = torch.empty((T, N), dtype=x.dtype, device=dev)
     if T == 0:
