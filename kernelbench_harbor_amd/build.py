@@ -21,9 +21,6 @@ LIB_DIR = os.path.join(PKG_DIR, "lib")
 OBJ_DIR = os.path.join(REPO_DIR, "_build", "obj")
 LIB_NAME = "libkbh_qgemm.so"
 LIB_PATH = os.path.join(LIB_DIR, LIB_NAME)
-# Calibration kernels of bench.py --mfma-ceiling (measurement only, a separate library).
-PROBE_SRC = os.path.join(PKG_DIR, "probe", "mfma_ceiling.hip")
-PROBE_PATH = os.path.join(LIB_DIR, "libkbh_probe.so")
 
 ARCH = "gfx950"
 HIPCC_FLAGS = [
@@ -76,12 +73,6 @@ def build(verbose: bool = True) -> str:
     if res.returncode != 0:
         raise RuntimeError(f"link failed:\n{res.stderr}")
     os.replace(tmp, LIB_PATH)
-    if os.path.exists(PROBE_SRC):
-        cmd = [_hipcc(), *HIPCC_FLAGS, "-shared", PROBE_SRC, "-o", PROBE_PATH + ".tmp"]
-        res = subprocess.run(cmd, capture_output=True, text=True)
-        if res.returncode != 0:
-            raise RuntimeError(f"hipcc failed for {PROBE_SRC}:\n{res.stderr}")
-        os.replace(PROBE_PATH + ".tmp", PROBE_PATH)
     if verbose:
         print(f"[kbh build] {len(srcs)} sources -> {LIB_PATH}")
     return LIB_PATH
