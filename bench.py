@@ -197,7 +197,7 @@ def time_config(torch, fn, sets, iters=100, batch=20, warmup=25):
 def record(name, ts, batched, by, fl, peak, **extra):
     med = ts[len(ts) // 2]
     bound, frac = roofline(batched, by, fl, peak)
-    out = {"name": name, **extra, "us_median": round(med * 1e6, 2),
+    out = {"name": name, **extra, "seed": 0, "us_median": round(med * 1e6, 2),
            "traffic": PMC_TRAFFIC.get(name),
            "us_batched": round(batched * 1e6, 2), "tflops": round(fl / batched / 1e12, 2),
            "gbps": round(by / batched / 1e9, 1), "bound": bound, "roofline_frac": round(frac, 4),
@@ -293,22 +293,55 @@ def run_grid(torch, dev, inputs, ops, families=None):
 def cpu_time(fn, ins, max_calls=5, budget_s=9.0, warmups=2):
     """Host seconds per call of fn(*ins): `warmups` warm-up calls (one when the first takes over
     2 s; the first call also pays for faulting in its fresh working memory), then timed calls
-    until their sum passes budget_s or max_calls are done; returns the median and the number of
-    timed calls."""
+    until their sum passes budget_s or max_calls are done; returns the median, the number of
+    timed calls and the last call's output."""
     t0 = time.perf_counter()
-    fn(*ins)
+    out = fn(*ins)
     if time.perf_counter() - t0 < 2.0:
         for _ in range(warmups - 1):
-            fn(*ins)
+            out = fn(*ins)
     ts = []
     while len(ts) < max_calls and sum(ts) < budget_s:
         t0 = time.perf_counter()
-        fn(*ins)
+        out = fn(*ins)
         ts.append(time.perf_counter() - t0)
-    return sorted(ts)[len(ts) // 2], len(ts)
+    return sorted(ts)[len(ts) // 2], len(ts), out
 
 
-def cpu_reference(jobs, native_budget_s=1.0):
+# Records whose native-dtype CPU path is always timed, whatever the host's fp16 GEMM rate:
+# BASELINE configuration 0 (the reference W4A16 module on CPU, M=16) is the named CPU baseline.
+NATIVE_ALWAYS = {"w4a16 M=16": 20.0}   # record -> time budget (s) of its timed native calls
+
+
+def check_record(name, chk, ins, gt):
+    """Correctness of the GPU output `chk["y"]` of a record, computed on the same seeded inputs
+    `ins` the CPU leg times, against the fp32 ground truth `gt` (the reference op sequence on
+    fp32-upcast inputs, kb_verifier.py:195-196): the BASELINE gate and the grader's allclose, and
+    the bit-exact integer stages where the record has them (the oracle is the checker here)."""
+    from kernelbench_harbor_amd import harness
+    from oracle import numerics, w4a16 as ow4, w8a8 as ow8
+    cmp = harness.compare(chk["y"], gt)
+    r = {k: (round(v, 8) if isinstance(v, float) else v) for k, v in cmp.as_dict().items()}
+    exact = {}
+    if "onehot_y" in chk:        # int4 unpack: one-hot rows of x, scales 1, zeros 0 -> y = q
+        want = ow4.unpack_int4_along_n(ins[1].numpy()[chk["onehot_k"]]).astype("float32")
+        exact["int4_unpack"] = bool((chk["onehot_y"].float().numpy() == want).all())
+    if "i32" in chk:             # int8 x int8 -> int32, exact (float64 products and sums)
+        acc = ow8.acc_int32(ins[0].numpy(), ins[1].numpy())
+        exact["int32_accumulate"] = bool((chk["i32"].numpy().astype("int64") == acc).all())
+        want = ow8.epilogue(acc, ins[2].float().numpy(), ins[3].float().numpy())
+        exact["fp16_epilogue"] = bool((chk["y"].float().numpy() == want).all())
+    if "e8m0_y" in chk:          # e8m0 decode: unit e4m3 codes on the timed block scales
+        sa = numerics.e8m0_decode(ins[1].numpy()).astype("float64")
+        sb = numerics.e8m0_decode(ins[3].numpy()).astype("float64")
+        want = (32.0 * (sa @ sb.T)).astype("float16").astype("float32")
+        exact["e8m0_decode"] = bool((chk["e8m0_y"].float().numpy() == want).all())
+    if exact:
+        r["int_bitexact"] = exact
+    return r
+
+
+def cpu_reference(jobs, native_budget_s=1.0, checks=None):
     """Times the reference modules' own torch op sequences (oracle/torch_ref.py: W4A16
     reference.py:10-17, W8A8 :7-9, FP8 :9-12, qMoE :11-21, SiLU-FP8 :13-23, and the MXFP8 and
     SiLU FFN restatements) on CPU tensors on this host: the fp32 ground truth (floating inputs
@@ -316,8 +349,10 @@ def cpu_reference(jobs, native_budget_s=1.0):
     dtypes) where it fits the time budget. Some hosts' torch runs fp16 GEMMs without vector
     support (0.4 GFLOP/s measured on the GPU box, against 100+ for fp32): a probe measures this
     host's fp16 GEMM rate, and a native call predicted to take longer than native_budget_s is
-    skipped with that prediction recorded. `jobs` maps a record name to (make_inputs, fn, flops,
-    native_is_fp16_gemm). torch uses the cores of the process's affinity mask, or the host share
+    skipped with that prediction recorded (except the records of NATIVE_ALWAYS). `jobs` maps a
+    record name to (make_inputs, fn, flops, native_is_fp16_gemm). With `checks` (record name ->
+    the GPU outputs on the same inputs), each record's ground truth also grades its GPU output
+    (check_record). torch uses the cores of the process's affinity mask, or the host share
     when the environment states one in OMP_NUM_THREADS. Returns {name: {...}} and the setup."""
     import torch
 
@@ -340,22 +375,27 @@ def cpu_reference(jobs, native_budget_s=1.0):
         print(f"[cpu] {name} ...", file=sys.stderr, flush=True)
         ins = make()
         gt_ins = tr.upcast(ins)
-        tg, ng = cpu_time(fn, gt_ins)
+        tg, ng, gt = cpu_time(fn, gt_ins)
         del gt_ins
         r = {"gt_s": round(tg, 4), "gt_calls": ng,
              "gt_tflops": round(fl / tg / 1e12, 4) if fl else None}
+        if checks and name in checks:
+            r["gpu_check"] = check_record(name, checks[name], ins, gt.float())
+        del gt
         predicted = fl / f16_rate if (f16_gemm and fl) else 0.0
-        if predicted > native_budget_s:
+        if predicted > native_budget_s and name not in NATIVE_ALWAYS:
             r.update({"native_s": None, "native_skipped": (
                 f"predicted {predicted:.0f} s per call at this host's measured fp16 GEMM rate "
                 f"({f16_rate / 1e9:.2f} GFLOP/s)")})
         else:
-            t, n = cpu_time(fn, ins, max_calls=3, budget_s=native_budget_s, warmups=1)
+            budget = NATIVE_ALWAYS.get(name, native_budget_s)
+            t, n, _ = cpu_time(fn, ins, max_calls=3, budget_s=budget, warmups=1)
             r.update({"native_s": round(t, 4), "native_calls": n,
-                      "native_tflops": round(fl / t / 1e12, 4) if fl else None})
+                      "native_tflops": round(fl / t / 1e12, 6) if fl else None})
         res[name] = r
         del ins
-        print(f"[cpu] {name}: fp32 GT {tg:.3f} s, native {r['native_s']} s", file=sys.stderr,
+        print(f"[cpu] {name}: fp32 GT {tg:.3f} s, native {r['native_s']} s"
+              + (f", gpu check {r['gpu_check']}" if "gpu_check" in r else ""), file=sys.stderr,
               flush=True)
     return res, {"cores": cores, "torch_threads": torch.get_num_threads(),
                  "omp_num_threads": share or None, "f16_gemm_gflops": round(f16_rate / 1e9, 3)}
@@ -389,104 +429,6 @@ def cpu_jobs(ms, with_configs):
         jobs["qmoe (reference op) T=256 D=4096 N=14336 E=8"] = (
             lambda: inputs.qmoe(seed=0), tr.qmoe, 2 * 256 * 8 * 4096 * 14336, True)
     return jobs
-
-
-# ---- calibration ---------------------------------------------------------------------------
-def mfma_ceiling(torch, dev, probe_path, blocks=256):
-    """Runs the calibration kernels of kernelbench_harbor_amd/probe/mfma_ceiling.hip (one
-    workgroup of 4 waves per CU): fp16 32x32x16 MFMA TFLOP/s with operands fixed in registers and
-    with fresh random operands from LDS for every MFMA, and LDS ds_read_b128 GB/s per CU. The
-    random-operand rate is the practical ceiling of a GEMM on random data (the MFMAs draw more
-    power when their operands switch, and the chip lowers its clock)."""
-    import ctypes
-    lib = ctypes.CDLL(probe_path)
-    lib.kbh_probe_run.restype = ctypes.c_int
-    lib.kbh_probe_run.argtypes = [ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int,
-                                  ctypes.c_int, ctypes.c_void_p]
-    g = torch.Generator(device=dev).manual_seed(0)
-    src = (torch.randint(0, 2 ** 31, (1 << 18,), generator=g, device=dev, dtype=torch.int64)
-           & 0x3BFF3BFF).to(torch.int32)                 # finite fp16 pairs, |v| < 1
-    out = torch.zeros(blocks * 256, dtype=torch.float32, device=dev)
-    stream = torch.cuda.current_stream().cuda_stream
-
-    def run(which, iters, reps=5):
-        assert lib.kbh_probe_run(which, src.data_ptr(), out.data_ptr(), blocks, iters, stream) == 0
-        torch.cuda.synchronize()
-        ts = []
-        for _ in range(reps):
-            a = torch.cuda.Event(enable_timing=True)
-            b = torch.cuda.Event(enable_timing=True)
-            a.record()
-            lib.kbh_probe_run(which, src.data_ptr(), out.data_ptr(), blocks, iters, stream)
-            b.record()
-            b.synchronize()
-            ts.append(a.elapsed_time(b) * 1e-3)
-        return sorted(ts)[reps // 2]
-    res = {"workgroups": blocks, "waves_per_workgroup": 4}
-    for which, key in ((0, "mfma_f16_fixed_operands_tflops"), (1, "mfma_f16_random_operands_tflops")):
-        t = run(which, 4000)
-        res[key] = round(blocks * 4 * 8 * 4000 * 32768 / t / 1e12, 1)
-    # 8-bit operands: finite e4m3 codes (the mask clears the NaN pattern), unit block scales
-    src.copy_(src & 0x3B3B3B3B)
-    t = run(4, 4000)
-    res["mfma_i8_random_operands_tops"] = round(blocks * 4 * 8 * 4000 * 65536 / t / 1e12, 1)
-    t = run(5, 2000)
-    res["mfma_f8_scaled_random_operands_tflops"] = round(blocks * 4 * 8 * 2000 * 131072 / t / 1e12, 1)
-    t = run(2, 4000)
-    res["lds_read_gbps_per_cu"] = round(256 * 16 * 16 * 4000 / t / 1e9, 1)
-    res["hbm_read"] = hbm_read_ceiling(torch, dev, lib)
-    res["peak_datasheet_tflops"] = {"f16": PEAK["f16"] / 1e12, "i8": PEAK["i8"] / 1e12,
-                                    "f8": PEAK["f8"] / 1e12}
-    return res
-
-
-def hbm_read_ceiling(torch, dev, lib):
-    """GB/s of the plain HBM read stream (probe kernel 3: 16-byte loads, eight in flight per
-    lane) for reads of the W4A16 decode's weight bytes and larger, over a grid-size sweep: each
-    timed call reads a fresh window of a 1 GiB buffer (well past the Infinity Cache), 20 calls
-    per graph replay, median of 5 replays. The best rate at 29.4 MB is the practical ceiling of
-    a decode-sized call."""
-    buf = torch.empty(1 << 30, dtype=torch.uint8, device=dev)
-    buf.random_(0, 256)
-    out = torch.zeros(1 << 16, dtype=torch.int32, device=dev)
-    base = buf.data_ptr()
-    res = []
-    for target in (K_DIM * N_DIM // 2, 4 * K_DIM * N_DIM // 2, 16 * K_DIM * N_DIM // 2):
-        best = None
-        for blocks in (256, 512, 1024, 2048):
-            iters = max(1, round(target / (blocks * 256 * 16)))
-            nbytes = blocks * 256 * iters * 16
-            nwin = (1 << 30) // nbytes
-            s = torch.cuda.Stream()
-            s.wait_stream(torch.cuda.current_stream())
-            g = torch.cuda.CUDAGraph()
-            with torch.cuda.stream(s):
-                for i in range(3):
-                    assert lib.kbh_probe_run(3, base + (i % nwin) * nbytes, out.data_ptr(), blocks,
-                                             iters, s.cuda_stream) == 0
-                torch.cuda.synchronize()
-                with torch.cuda.graph(g, stream=s):
-                    for i in range(20):
-                        lib.kbh_probe_run(3, base + (i % nwin) * nbytes, out.data_ptr(), blocks,
-                                          iters, torch.cuda.current_stream().cuda_stream)
-            ts = []
-            for _ in range(5):
-                a = torch.cuda.Event(enable_timing=True)
-                b = torch.cuda.Event(enable_timing=True)
-                a.record()
-                g.replay()
-                b.record()
-                b.synchronize()
-                ts.append(a.elapsed_time(b) * 1e-3 / 20)
-            t = sorted(ts)[2]
-            if best is None or nbytes / t > best["gbps"] * 1e9:
-                best = {"bytes": nbytes, "workgroups": blocks, "us": round(t * 1e6, 2),
-                        "gbps": round(nbytes / t / 1e9, 1)}
-        best["frac_of_8tbs"] = round(best["gbps"] / 8000, 3)
-        res.append(best)
-        print(f"[calib] HBM read {best}", file=sys.stderr, flush=True)
-    del buf
-    return res
 
 
 # ---- workloads -------------------------------------------------------------------------------
@@ -620,6 +562,42 @@ def vs_torch(torch, dev, inputs, ops, iters=100, warmup=25):
     return out
 
 
+def provenance(torch, dev):
+    """Seed, software versions and device of the run (BASELINE.md record fields)."""
+    p = torch.cuda.get_device_properties(dev)
+    return {"seed": 0, "torch": torch.__version__, "hip": torch.version.hip,
+            "device": p.name, "arch": getattr(p, "gcnArchName", None),
+            "inputs": "seed 0 per record (kernelbench_harbor_amd.inputs), generated on the CPU and "
+                      "copied to the device; the CPU leg times and checks the same tensors"}
+
+
+def w4a16_check(torch, ops, ins, M):
+    """GPU outputs the CPU leg checks for a sweep point: the output on the first timed input
+    set, and (the int4 unpack) the output for one-hot rows of x on the same qweight with unit
+    scales and zero zero-points, where y[m] equals row k_m of the unpacked weights exactly."""
+    x, qw, s, z = ins
+    M_, K = x.shape
+    k = [(m * 9973 + 17) % K for m in range(M_)]
+    oh = torch.zeros_like(x)
+    oh[torch.arange(M_, device=x.device), torch.tensor(k, device=x.device)] = 1.0
+    y1 = ops.w4a16_gemm(oh, qw, torch.ones_like(s), torch.zeros_like(z))
+    return {"y": ops.w4a16_gemm(*ins).cpu(), "onehot_y": y1.cpu(), "onehot_k": k}
+
+
+def config_check(torch, ops, name, fn, ins):
+    """GPU outputs the CPU leg checks for a configuration: the output on the first timed input
+    set, the raw int32 accumulators (W8A8) and, for MXFP8, the output for unit e4m3 codes (0x38)
+    on the timed e8m0 block scales, where every partial sum is an exact power-of-two sum."""
+    chk = {"y": fn(*ins).cpu()}
+    if name.startswith("w8a8"):
+        chk["i32"] = ops.w8a8_gemm_i32(ins[0], ins[1]).cpu()
+    if name.startswith("mxfp8"):
+        a, a_s, b, b_s = ins
+        chk["e8m0_y"] = ops.mxfp8_gemm(torch.full_like(a, 0x38), a_s, torch.full_like(b, 0x38),
+                                       b_s).cpu()
+    return chk
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -636,11 +614,6 @@ def main():
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                     help="only run 5 device copies of MIB MiB (calibrates rocprofv3 FETCH_SIZE/"
                          "WRITE_SIZE against a kernel of known traffic) and exit")
-    ap.add_argument("--mfma-ceiling", action="store_true",
-                    help="only run the calibration kernels (kernelbench_harbor_amd/probe): the "
-                         "fp16 MFMA rate with fixed and with random operands, the int8 and "
-                         "block-scaled fp8 rates with random operands, the LDS read bandwidth "
-                         "and the HBM read-stream rate, then print one JSON line")
     ap.add_argument("--vs-torch", action="store_true",
                     help="only time, per configuration, the reference forward in eager torch and "
                          "under torch.compile(max-autotune) beside the HIP op (the grader's "
@@ -672,9 +645,6 @@ def main():
             dst.copy_(src)
         torch.cuda.synchronize()
         print(json.dumps({"copy_probe_bytes": n, "copies": 5}))
-        return
-    if args.mfma_ceiling:
-        print(json.dumps(mfma_ceiling(torch, dev, kbuild.PROBE_PATH)), flush=True)
         return
     if args.vs_torch:
         print(json.dumps({"vs_torch": vs_torch(torch, dev, inputs, ops), "n_gpus": 1,
@@ -735,7 +705,7 @@ def main():
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
 
-    sweep, step_flops, mean_s = [], 0, {}
+    sweep, step_flops, mean_s, checks = [], 0, {}, {}
     for M in ms:
         ts = sorted(a.elapsed_time(b) * 1e-3 for a, b in ev[M])
         mean_s[M] = sum(ts) / len(ts)
@@ -743,6 +713,7 @@ def main():
         sweep.append(record(f"w4a16 M={M}", grader, batched, w4a16_bytes(M), gemm_flops(M),
                             PEAK["f16"], M=M, us_step_mean=round(mean_s[M] * 1e6, 2)))
         step_flops += gemm_flops(M)
+        checks[f"w4a16 M={M}"] = w4a16_check(torch, ops, sets[M][0], M)
         print(f"[bench] w4a16 M={M}: {sweep[-1]['us_batched']} us batched, "
               f"{sweep[-1]['us_median']} us median", file=sys.stderr, flush=True)
     del sets
@@ -772,6 +743,7 @@ def main():
             s_ = make()
             ts, bm = time_config(torch, fn, s_, 100, 20 if len(s_) > 1 else 10)
             configs.append(record(name, ts, bm, by, fl, peak, **extra))
+            checks[name] = config_check(torch, ops, name, fn, s_[0])
             print(f"[bench] {name}: {configs[-1]['us_batched']} us batched", file=sys.stderr,
                   flush=True)
             del s_
@@ -793,11 +765,19 @@ def main():
         "sweep": sweep,
         "roofline": roof,
         "configs": configs,
+        "provenance": provenance(torch, dev),
     }
     if not args.no_cpu_baseline:
-        cpu, setup = cpu_reference(cpu_jobs(ms, not args.no_configs))
+        cpu, setup = cpu_reference(cpu_jobs(ms, not args.no_configs), checks=checks)
         for r in sweep + configs:
-            r["cpu"] = cpu.get(r["name"])
+            c = cpu.get(r["name"])
+            if c is not None and "gpu_check" in c:
+                r["check"] = c.pop("gpu_check")
+            r["cpu"] = c
+        out["checked"] = {"records": sum("check" in r for r in sweep + configs),
+                          "gate_ok": all(r["check"]["ok"] for r in sweep + configs if "check" in r),
+                          "int_bitexact": all(all(r["check"].get("int_bitexact", {}).values())
+                                              for r in sweep + configs if "check" in r)}
         tot_fl = sum(gemm_flops(M) for M in ms)
         tot_gt = sum(cpu[f"w4a16 M={M}"]["gt_s"] for M in ms)
         native = [M for M in ms if cpu[f"w4a16 M={M}"]["native_s"] is not None]
