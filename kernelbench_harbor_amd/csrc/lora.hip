@@ -140,7 +140,7 @@ __global__ __launch_bounds__(kLoraThreads) void lora_expand_add_kernel(
       for (int c = 0; c < 4; ++c)
         acc[c] += los[j + u] * half_bits_to_f32<BF16>((uint16_t)(b[u][c >> 1] >> (16 * (c & 1))));
   }
-  const float bad = lora_id_valid(ids, t, L) ? 0.f : __builtin_nanf("");
+  const bool valid = lora_id_valid(ids, t, L);
   kbh_u32x2 out;
 #pragma unroll
   for (int h = 0; h < 2; ++h) {
@@ -148,7 +148,7 @@ __global__ __launch_bounds__(kLoraThreads) void lora_expand_add_kernel(
 #pragma unroll
     for (int c = 0; c < 2; ++c) {
       const float e = half_bits_to_f32<BF16>(f32_to_half_bits<BF16>(acc[2 * h + c]));
-      v[c] = keep_f32(bs[2 * h + c] + e) + bad;
+      v[c] = valid ? keep_f32(bs[2 * h + c] + e) : __builtin_nanf("");  // select: keeps -0.0
     }
     out[h] = (uint32_t)f32_to_half_bits<BF16>(v[0]) | ((uint32_t)f32_to_half_bits<BF16>(v[1]) << 16);
   }

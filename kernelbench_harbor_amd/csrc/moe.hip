@@ -44,27 +44,38 @@ __device__ inline float logit_at(const void* p, size_t i) {
 
 struct MoeBuffers {
   int* topi;        // [2T]
-  uint16_t* topw;   // [2T] routing weights in the activation dtype
+  uint16_t* topw;   // [2T] routing weights in the activation dtype (fp32 when wmode == 2)
   int* slot_of;     // [2T] position of (t, k) inside its expert's slot range
   int* perm;        // [2T] slot -> 2t + k
   int* tiles;       // [max_tiles][3] = expert, first slot, rows
+  float* topw32;    // [2T] the same weights unrounded (fp32), when not null
 };
 
-// Top-k routing (k <= kMoeMaxTopk, E <= kMoeMaxExperts) for the fp16/bf16-weight MoE
-// (tasks/moe/<task>/environment/reference.py:11-13), in two kernels:
+// Top-k routing (k <= kMoeMaxTopk, E <= kMoeMaxExperts) for every MoE op here
+// (tasks/fused_qmoe/<task>/environment/reference.py:14-16, tasks/moe/<task>/environment/
+// reference.py:11-13: probs = softmax(fp32 logits); topv, topi = probs.topk(k)), in two kernels:
 //  * moe_topk_select_kernel: one wave per token, lanes across experts (up to 4 each). The
-//    softmax max and sum are wave reductions; the k picks are k rounds of a wave argmax on
-//    (logit descending, index ascending), so the lower expert index wins a tie, each pick
-//    excluded from the later rounds. NaN logits rank as -inf (every id is a distinct expert in
-//    range). Weights p_j / sum_j p_j (summed in k order) rounded to the activation dtype.
+//    softmax max and sum are wave reductions. The ids and their order are those torch.topk
+//    returns on the GPU, in its two steps: the k picks are k rounds of a wave argmax on (logit
+//    descending, index ascending), which selects every value above the k-th largest and, on a
+//    tie at the boundary, the lowest indices; they are then laid out in torch's slot order
+//    (values above the k-th ascending by index, then the k-th value's ties ascending by index)
+//    and put through the 32-slot descending bitonic network of torch's small sort (lane = slot,
+//    invalid slots sink), whose compare-exchange keeps or swaps equal keys by slot position:
+//    e.g. two equal top values come out higher index first. Logits order like the
+//    probabilities (softmax is monotonic; fp16/bf16 logits that differ never round to equal
+//    fp32 probabilities). NaN logits rank as -inf (every id is a distinct expert in range).
+//    Weights p_j / sum_j p_j (summed in output order) are written in the activation dtype
+//    (wmode 0 fp16, 1 bf16) or fp32 (wmode 2), and unrounded to topw32 when it is set.
 //  * moe_route_build_kernel (one workgroup): per-expert slot counts (LDS atomics), offsets,
 //    the permutation perm[slot] = k t + j and the tile table (unused entries: rows = 0).
 constexpr int kMoeMaxTopk = 8;
 constexpr int kTopkWaves = 4;  // tokens per workgroup of the select kernel
+constexpr int kTopkSlots = 32;  // slots of torch's small bitonic sort
 
 template <int LDT>
 __global__ __launch_bounds__(kTopkWaves * 64) void moe_topk_select_kernel(
-    const void* __restrict__ logits, int T, int E, int K, int out_bf16, MoeBuffers mb) {
+    const void* __restrict__ logits, int T, int E, int K, int wmode, MoeBuffers mb) {
   constexpr int EPL = kMoeMaxExperts / 64;
   const int lane = threadIdx.x & 63;
   const int t = blockIdx.x * kTopkWaves + (threadIdx.x >> 6);
@@ -86,6 +97,7 @@ __global__ __launch_bounds__(kTopkWaves * 64) void moe_topk_select_kernel(
     if (lane + 64 * i < E) sum += expf(v[i] - mx);
 #pragma unroll
   for (int o = 32; o >= 1; o >>= 1) sum += __shfl_xor(sum, o, 64);
+  // Selection: k rounds of a wave argmax; every lane ends with all picks (lv, li).
   unsigned taken = 0;
   float lv[kMoeMaxTopk];
   int li[kMoeMaxTopk];
@@ -110,23 +122,55 @@ __global__ __launch_bounds__(kTopkWaves * 64) void moe_topk_select_kernel(
     }
     if ((be & 63) == lane) taken |= 1u << (be >> 6);
     li[j] = be;
-    lv[j] = logit_at<LDT>(logits, row + be);
+    lv[j] = bv;
   }
-  float pk[kMoeMaxTopk], ps = 0.f;
+  // Slot order of torch's gather step: the picks above the k-th value by ascending index, then
+  // the k-th value's ties by ascending index. Lane s (< K) takes the pick of rank s.
+  const int slot = lane & (kTopkSlots - 1);
+  const float vk = lv[K - 1];
+  float sv = -INFINITY;
+  int si = 0, ok = 0;
 #pragma unroll
   for (int j = 0; j < kMoeMaxTopk; ++j) {
-    if (j < K) {
-      pk[j] = keep_f32(expf(lv[j] - mx) / sum);
-      ps = keep_f32(ps + pk[j]);
-    }
-  }
+    if (j >= K) continue;
+    const int kj = (lv[j] > vk ? 0 : kMoeMaxExperts) + li[j];
+    int rank = 0;
 #pragma unroll
-  for (int j = 0; j < kMoeMaxTopk; ++j) {
-    if (j < K && lane == j) {
-      const float w = keep_f32(pk[j] / ps);
-      mb.topi[K * t + j] = li[j];
-      mb.topw[K * t + j] = out_bf16 ? f32_to_bf16_bits(w) : f32_to_f16_bits(w);
-    }
+    for (int i = 0; i < kMoeMaxTopk; ++i)
+      if (i < K && (lv[i] > vk ? 0 : kMoeMaxExperts) + li[i] < kj) ++rank;
+    if (rank == slot) { sv = lv[j]; si = li[j]; ok = 1; }
+  }
+  // torch's small sort: slots a < b = a ^ stride exchange when
+  // ((key[a] > key[b] && a valid) || b invalid) == dir, dir = (a & size) != 0 while building
+  // bitonic sequences, false in the final merge. Both lanes of a pair evaluate it alike.
+  auto cx = [&](int size, int stride) {
+    const float ov = __shfl_xor(sv, stride, 64);
+    const int oi = __shfl_xor(si, stride, 64);
+    const int ook = __shfl_xor(ok, stride, 64);
+    const bool lo = (slot & stride) == 0;
+    const float va = lo ? sv : ov, vb = lo ? ov : sv;
+    const int oka = lo ? ok : ook, okb = lo ? ook : ok;
+    const bool dir = size < kTopkSlots && (((lo ? slot : slot ^ stride) & size) != 0);
+    if ((((va > vb) && oka) || !okb) == dir) { sv = ov; si = oi; ok = ook; }
+  };
+  if (K > 1) {
+#pragma unroll
+    for (int size = 2; size <= kTopkSlots; size *= 2)
+#pragma unroll
+      for (int stride = size / 2; stride > 0; stride /= 2) cx(size, stride);
+  }
+  // Weights in output order: p_s = exp(l_s - max) / sum, renormalised by their sum (slot order).
+  const float pk = keep_f32(expf(sv - mx) / sum);
+  float ps = 0.f;
+#pragma unroll
+  for (int j = 0; j < kMoeMaxTopk; ++j)
+    if (j < K) ps = keep_f32(ps + __shfl(pk, j, 64));
+  if (lane < K) {
+    const float w = keep_f32(pk / ps);
+    mb.topi[K * t + lane] = si;
+    if (wmode == 2) reinterpret_cast<float*>(mb.topw)[K * t + lane] = w;
+    else mb.topw[K * t + lane] = wmode ? f32_to_bf16_bits(w) : f32_to_f16_bits(w);
+    if (mb.topw32) mb.topw32[K * t + lane] = w;
   }
 }
 
@@ -220,35 +264,41 @@ __device__ inline kbh_i16x4 lds_read_tr16(const uint16_t* p) {
       (__attribute__((address_space(3))) kbh_i16x4*)(const_cast<uint16_t*>(p)));
 }
 
-// Slab producer for int8-stored weights [E][K][N] (N contiguous) with scales [E][K/G][N] in the
-// activation dtype: W = dtype(dtype(q) * s), one rounding (q is exact in either dtype). Stored
-// N-major like F16SlabPolicy (read with the transposing LDS read): thread t dequantises 16
-// consecutive columns (16 bytes) of row t / 8, so each pair of neighbouring columns meets its
-// pair of scales in one dword, and writes them as two 16-byte stores. fp16 activations only
-// (bf16 uses I8KSlabPolicy).
-struct I8NSlabPolicy {
+// Slab producer for int8-stored weights [E][K][N] (N contiguous) without their scales: the
+// integers q themselves in the activation dtype (every int8 value is exact in fp16 and bf16).
+// The reference qMoE op applies the scales per quantization group to the fp32 accumulators
+// instead (moe_gemm_kernel with GS > 0), so each expert's weights enter the products exactly,
+// as in the grader's fp32 ground truth (q * s is exact in fp32). Stored N-major (read with the
+// transposing LDS read): thread t converts 16 consecutive columns (16 bytes) of row t / 8 and
+// writes them as two 16-byte stores.
+// fp32 value of the signed byte B (0..3) of v: v_cvt_f32_i32 with a sign-extended SDWA byte
+// select (exact).
+template <int B>
+__device__ inline float sbyte_to_f32(uint32_t v) {
+  float r;
+  asm("v_cvt_f32_i32_sdwa %0, sext(%1) dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_%2"
+      : "=v"(r) : "v"(v), "n"(B));
+  return r;
+}
+
+template <bool BF16>
+struct I8QSlabPolicy {
   static constexpr bool kNMajor = true;
   const int8_t* w;
-  const uint16_t* scales;
-  int N, group;
-  size_t w_stride, s_stride;
-  __device__ I8NSlabPolicy at_expert(int e) const {
-    I8NSlabPolicy p = *this;
+  int N;
+  size_t w_stride;
+  __device__ I8QSlabPolicy at_expert(int e) const {
+    I8QSlabPolicy p = *this;
     p.w += (size_t)e * w_stride;
-    p.scales += (size_t)e * s_stride;
     return p;
   }
   struct Regs {
     kbh_u32x4 q;
-    kbh_u32x4 s[2];
   };
   __device__ void load(Regs& r, int k0, int n0, int t) const {
     const int c = t & 7, k = t >> 3;
     r.q = __builtin_nontemporal_load(
         reinterpret_cast<const kbh_u32x4*>(w + (size_t)(k0 + k) * N + n0 + 16 * c));
-    const uint16_t* sp = scales + (size_t)(k0 / group) * N + n0 + 16 * c;  // slab within a group
-    r.s[0] = *reinterpret_cast<const kbh_u32x4*>(sp);
-    r.s[1] = *reinterpret_cast<const kbh_u32x4*>(sp + 8);
   }
   __device__ void store(const Regs& r, uint16_t* Bs, int t) const {
     const int c = t & 7, k = t >> 3;
@@ -258,13 +308,22 @@ struct I8NSlabPolicy {
       const uint32_t v = r.q[d];
 #pragma unroll
       for (int h = 0; h < 2; ++h) {  // columns 4d + 2h, 4d + 2h + 1
-        const uint32_t sc = r.s[d >> 1][2 * (d & 1) + h];
-        // fp16 magic: (byte ^ 0x80) | 0x6400 is 1024 + (q + 128); minus 1152 gives q exactly.
-        typedef _Float16 h2 __attribute__((ext_vector_type(2)));
-        const _Float16 bias = (_Float16)1152.0f;
-        const uint32_t P = __builtin_amdgcn_perm(0u, v, h ? 0x0c030c02u : 0x0c010c00u);
-        const h2 q = __builtin_bit_cast(h2, (P ^ 0x00800080u) | 0x64006400u) - h2{bias, bias};
-        out[d >> 1][2 * (d & 1) + h] = __builtin_bit_cast(uint32_t, q * __builtin_bit_cast(h2, sc));
+        if constexpr (BF16) {
+          // An int8 value has at most 8 significant bits, so its fp32 image ends in 16 zero bits
+          // and its upper half is the exact bf16. One SDWA conversion per byte, one v_perm_b32
+          // per pair (the compiler's own code took a shift, a v_bfe_i32 and a conversion).
+          const float lo = h ? sbyte_to_f32<2>(v) : sbyte_to_f32<0>(v);
+          const float hi = h ? sbyte_to_f32<3>(v) : sbyte_to_f32<1>(v);
+          out[d >> 1][2 * (d & 1) + h] = __builtin_amdgcn_perm(
+              __builtin_bit_cast(uint32_t, hi), __builtin_bit_cast(uint32_t, lo), 0x07060302u);
+        } else {
+          // fp16 magic: (byte ^ 0x80) | 0x6400 is 1024 + (q + 128); minus 1152 gives q exactly.
+          typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+          const _Float16 bias = (_Float16)1152.0f;
+          const uint32_t P = __builtin_amdgcn_perm(0u, v, h ? 0x0c030c02u : 0x0c010c00u);
+          const h2 q = __builtin_bit_cast(h2, (P ^ 0x00800080u) | 0x64006400u) - h2{bias, bias};
+          out[d >> 1][2 * (d & 1) + h] = __builtin_bit_cast(uint32_t, q);
+        }
       }
     }
     *reinterpret_cast<kbh_u32x4*>(&Bs[k * kBnPitch + 16 * c]) = out[0];
@@ -272,85 +331,20 @@ struct I8NSlabPolicy {
   }
 };
 
-// k-major variant of the int8 producer (a 4x4 byte transpose in registers, Bs[tld_row(n) * TLD +
-// k]): used for bf16, where the N-major one's 16 columns per thread of fp32 dequantisation cost
-// registers and occupancy (measured 1.15-1.8x slower); same values.
-template <bool BF16>
-struct I8KSlabPolicy {
-  const int8_t* w;
-  const uint16_t* scales;
-  int N, group;
-  size_t w_stride, s_stride;
-  __device__ I8KSlabPolicy at_expert(int e) const {
-    I8KSlabPolicy p = *this;
-    p.w += (size_t)e * w_stride;
-    p.scales += (size_t)e * s_stride;
-    return p;
-  }
-  struct Regs {
-    uint32_t b[4];
-    kbh_u32x2 s;
-  };
-  __device__ void load(Regs& r, int k0, int n0, int t) const {
-    const int cq = t & 31, rq = t >> 5;
-    const int8_t* p = w + (size_t)(k0 + 4 * rq) * N + n0 + 4 * cq;
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-      r.b[i] = __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(p + (size_t)i * N));
-    r.s = *reinterpret_cast<const kbh_u32x2*>(scales + (size_t)(k0 / group) * N + n0 + 4 * cq);
-  }
-  __device__ void store(const Regs& r, uint16_t* Bs, int t) const {
-    const int cq = t & 31, rq = t >> 5;
-    // 4x4 byte transpose: column j gets the 4 k values (rows 4rq..4rq+3)
-    const uint32_t t0 = __builtin_amdgcn_perm(r.b[1], r.b[0], 0x05010400u);
-    const uint32_t t1 = __builtin_amdgcn_perm(r.b[1], r.b[0], 0x07030602u);
-    const uint32_t t2 = __builtin_amdgcn_perm(r.b[3], r.b[2], 0x05010400u);
-    const uint32_t t3 = __builtin_amdgcn_perm(r.b[3], r.b[2], 0x07030602u);
-    const uint32_t cols[4] = {__builtin_amdgcn_perm(t2, t0, 0x05040100u),
-                              __builtin_amdgcn_perm(t2, t0, 0x07060302u),
-                              __builtin_amdgcn_perm(t3, t1, 0x05040100u),
-                              __builtin_amdgcn_perm(t3, t1, 0x07060302u)};
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const uint16_t sb = (uint16_t)((j & 1) ? (r.s[j >> 1] >> 16) : (r.s[j >> 1] & 0xffffu));
-      const uint32_t v = cols[j];
-      kbh_u32x2 out;
-      if constexpr (BF16) {
-        const float sf = bf16_bits_to_f32(sb);
-#pragma unroll
-        for (int h = 0; h < 2; ++h) {
-          const float a = (float)(int8_t)(v >> (16 * h)) * sf;
-          const float b = (float)(int8_t)(v >> (16 * h + 8)) * sf;
-          out[h] = (uint32_t)f32_to_bf16_bits(a) | ((uint32_t)f32_to_bf16_bits(b) << 16);
-        }
-      } else {
-        // fp16 magic: (byte ^ 0x80) | 0x6400 is 1024 + (q + 128); minus 1152 gives q exactly.
-        typedef _Float16 h2 __attribute__((ext_vector_type(2)));
-        const _Float16 sc = __builtin_bit_cast(_Float16, sb);
-        const _Float16 bias = (_Float16)1152.0f;
-#pragma unroll
-        for (int h = 0; h < 2; ++h) {
-          const uint32_t sel = h ? 0x0c030c02u : 0x0c010c00u;  // bytes 2h, 2h+1 -> halves
-          const uint32_t P = __builtin_amdgcn_perm(0u, v, sel);
-          const uint32_t hv = (P ^ 0x00800080u) | 0x64006400u;
-          const h2 q = __builtin_bit_cast(h2, hv) - h2{bias, bias};
-          out[h] = __builtin_bit_cast(uint32_t, q * h2{sc, sc});
-        }
-      }
-      *reinterpret_cast<kbh_u32x2*>(&Bs[tld_row(4 * cq + j) * TLD + 4 * rq]) = out;
-    }
-  }
-};
-
 __device__ inline float silu(float v) { return v / (1.0f + expf(-v)); }
 
 // Expert-grouped GEMM. BM = 64 (1x4 waves, 64x32 each) or 128 (2x2 waves, 64x64 each).
-template <bool BF16, int BM, class BP, bool GATHER, bool GATED, bool OUT_PERM>
-__global__ __launch_bounds__(256) void moe_gemm_kernel(const uint16_t* __restrict__ A, int lda,
+// GS > 0 (the reference qMoE op): the producer delivers unscaled integer weights and every GS
+// slabs (one quantization group) the group's fp32 sums are scaled by the group's scales
+// (fscales [E][K/(GS*TBK)][N], x.dtype) into fp32 totals, which are written as fp32 to `out`.
+template <bool BF16, int BM, class BP, bool GATHER, bool GATED, bool OUT_PERM, int GS = 0>
+__global__ __launch_bounds__(256, GS > 0 ? 2 : 1) void moe_gemm_kernel(const uint16_t* __restrict__ A, int lda,
                                                        const int* __restrict__ perm,
                                                        const int* __restrict__ tiles, BP bp,
                                                        BP bp2, uint16_t* __restrict__ out,
-                                                       int ldo, int N, int K, int topk) {
+                                                       int ldo, int N, int K, int topk,
+                                                       const uint16_t* __restrict__ fscales = nullptr,
+                                                       size_t fs_stride = 0) {
   constexpr int BN = 128;
   constexpr int WM = BM / 64, WN = 4 / WM;  // waves along M and N
   constexpr int WNT = BN / WN / 32;         // 32-column MFMA tiles per wave
@@ -439,18 +433,55 @@ __global__ __launch_bounds__(256) void moe_gemm_kernel(const uint16_t* __restric
     }
   };
 
+  // Fold (GS > 0): totals, and the scales of this lane's columns for the current group (loaded
+  // one group ahead of their use).
+  constexpr bool FOLD = GS > 0;
+  constexpr int U = (GS > TDEPTH) ? GS : TDEPTH;  // slabs per loop iteration
+  kbh_f32x16 tot[FOLD ? 2 : 1][FOLD ? WNT : 1];
+  float sc[WNT];
+  const uint16_t* fsc = fscales + (FOLD ? (size_t)e * fs_stride : 0);
+  auto load_scales = [&](int g) {
+#pragma unroll
+    for (int j = 0; j < WNT; ++j)
+      sc[j] = half_bits_to_f32<BF16>(fsc[(size_t)g * N + n0 + wn * 32 * WNT + j * 32 + fr]);
+  };
+  if constexpr (FOLD) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int j = 0; j < WNT; ++j)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) tot[i][j][v] = 0.f;
+    load_scales(0);
+  }
+  auto fold = [&](int g_next) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int j = 0; j < WNT; ++j)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+          tot[i][j][v] = fmaf(sc[j], accv[0][i][j][v], tot[i][j][v]);
+          accv[0][i][j][v] = 0.f;
+        }
+    load_scales(g_next);
+  };
+
   Slab ring[TDEPTH];
 #pragma unroll
   for (int d = 0; d < TDEPTH; ++d) load(ring[d], min(d, KT - 1));
   store(ring[0], 0);
   load(ring[0], min(TDEPTH, KT - 1));
   __syncthreads();
-  for (int kt0 = 0; kt0 < KT; kt0 += TDEPTH) {
+  for (int kt0 = 0; kt0 < KT; kt0 += U) {
 #pragma unroll
-    for (int d = 0; d < TDEPTH; ++d) {
+    for (int d = 0; d < U; ++d) {
       const int kt = kt0 + d;
       const int nxt = (d + 1) % TDEPTH;
       mma(kt & 1);
+      if constexpr (FOLD) {
+        if ((d + 1) % GS == 0) fold(min((kt + 1) / GS, KT / GS - 1));  // a group ends here
+      }
       __builtin_amdgcn_sched_barrier(0);  // phases in order (see tiled_f16.h)
       store(ring[nxt], (kt + 1) & 1);     // after the last slab: unused buffer
       __builtin_amdgcn_sched_barrier(0);
@@ -472,6 +503,10 @@ __global__ __launch_bounds__(256) void moe_gemm_kernel(const uint16_t* __restric
           const int s = s0 + r;
           const int orow = OUT_PERM ? perm[s] : s;
           const int n = n0 + wn * 32 * WNT + j * 32 + fr;
+          if constexpr (FOLD) {
+            reinterpret_cast<float*>(out)[(size_t)orow * ldo + n] = tot[i][j][v];
+            continue;
+          }
           float val = accv[0][i][j][v];
           if constexpr (GATED) val = keep_f32(silu(val)) * accv[1][i][j][v];
           out[(size_t)orow * ldo + n] = f32_to_half_bits<BF16>(val);
@@ -492,6 +527,30 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(const uint16_t* __rest
   const float p1 = half_bits_to_f32<BF16>(f32_to_half_bits<BF16>(keep_f32(
       half_bits_to_f32<BF16>(o[(2 * t + 1) * N + n]) * half_bits_to_f32<BF16>(topw[2 * t + 1]))));
   y[i] = f32_to_half_bits<BF16>(keep_f32(p0 + p1));
+}
+
+// y[t][n] = dtype(fp32(o[2t][n] w[2t]) + fp32(o[2t+1][n] w[2t+1])) with fp32 expert outputs
+// and fp32 routing weights: the reference's (sel * topv).sum(dim=1) (reference.py:20-21)
+// evaluated as in the grader's fp32 ground truth, rounded once. Four columns per thread.
+template <bool BF16>
+__global__ __launch_bounds__(256) void moe_combine_f32_kernel(const float* __restrict__ o,
+                                                              const float* __restrict__ w,
+                                                              uint16_t* __restrict__ y, int T,
+                                                              int N) {
+  const size_t i4 = ((size_t)blockIdx.x * blockDim.x + threadIdx.x) * 4;
+  if (i4 >= (size_t)T * N) return;
+  const size_t t = i4 / N, n = i4 - t * N;
+  const kbh_f32x4 a = *reinterpret_cast<const kbh_f32x4*>(o + (2 * t) * N + n);
+  const kbh_f32x4 b = *reinterpret_cast<const kbh_f32x4*>(o + (2 * t + 1) * N + n);
+  const float w0 = w[2 * t], w1 = w[2 * t + 1];
+  uint16_t r[4];
+#pragma unroll
+  for (int c = 0; c < 4; ++c)
+    r[c] = f32_to_half_bits<BF16>(keep_f32(keep_f32(a[c] * w0) + keep_f32(b[c] * w1)));
+  kbh_u32x2 out;
+  out[0] = (uint32_t)r[0] | ((uint32_t)r[1] << 16);
+  out[1] = (uint32_t)r[2] | ((uint32_t)r[3] << 16);
+  *reinterpret_cast<kbh_u32x2*>(y + i4) = out;
 }
 
 // y[t][n] = dtype(sum_j fp32(dtype(o[k t + j][n] * w[k t + j]))), j = 0..k-1 in order: the
@@ -631,14 +690,15 @@ bool plan_ffn(int T, int E, int D, int F, int group, FfnPlan* p) {
 
 // ---- host side ------------------------------------------------------------------------------
 struct MoeLayout {
-  size_t topi, topw, slot_of, perm, tiles, h, o, part, total;
+  size_t topi, topw, slot_of, perm, tiles, h, o, part, topw32, total;
   int bm, max_tiles, topk;
 };
 
 // Slots: topk per token (slot order grouped by expert). bm: rows per tile-table entry (0: 128
-// when an expert averages more than 48 rows, else 64).
+// when an expert averages more than 48 rows, else 64). f32_out: expert outputs o in fp32 and
+// fp32 routing weights (the reference qMoE op), else in the activation dtype.
 MoeLayout moe_layout(int T, int E, int hidden, int out_cols, int bm = 0, size_t part_bytes = 0,
-                     int topk = 2) {
+                     int topk = 2, bool f32_out = false) {
   MoeLayout L;
   const size_t S = (size_t)topk * T;
   L.topk = topk;
@@ -656,8 +716,9 @@ MoeLayout moe_layout(int T, int E, int hidden, int out_cols, int bm = 0, size_t 
   L.perm = take(S * 4);
   L.tiles = take((size_t)L.max_tiles * 3 * 4);
   L.h = take(S * hidden * 2);
-  L.o = take(S * out_cols * 2);
+  L.o = take(S * out_cols * (f32_out ? 4 : 2));
   L.part = take(part_bytes);
+  L.topw32 = f32_out ? take(S * 4) : 0;
   L.total = o;
   return L;
 }
@@ -665,35 +726,55 @@ MoeLayout moe_layout(int T, int E, int hidden, int out_cols, int bm = 0, size_t 
 MoeBuffers moe_buffers(void* ws, const MoeLayout& L) {
   char* b = (char*)ws;
   return MoeBuffers{(int*)(b + L.topi), (uint16_t*)(b + L.topw), (int*)(b + L.slot_of),
-                    (int*)(b + L.perm), (int*)(b + L.tiles)};
+                    (int*)(b + L.perm), (int*)(b + L.tiles),
+                    L.topw32 ? (float*)(b + L.topw32) : nullptr};
 }
 
-void launch_route_topk(const void* logits, int logits_dtype, int T, int E, bool bf16,
+// wmode: routing weights written to mb.topw as 0 fp16, 1 bf16, 2 fp32.
+void launch_route_topk(const void* logits, int logits_dtype, int T, int E, int wmode,
                        const MoeBuffers& mb, const MoeLayout& L, hipStream_t st) {
   const dim3 g((T + kTopkWaves - 1) / kTopkWaves), b(kTopkWaves * 64);
   const int K = L.topk;
   if (logits_dtype == 0)
-    hipLaunchKernelGGL(moe_topk_select_kernel<0>, g, b, 0, st, logits, T, E, K, (int)bf16, mb);
+    hipLaunchKernelGGL(moe_topk_select_kernel<0>, g, b, 0, st, logits, T, E, K, wmode, mb);
   else if (logits_dtype == 1)
-    hipLaunchKernelGGL(moe_topk_select_kernel<1>, g, b, 0, st, logits, T, E, K, (int)bf16, mb);
+    hipLaunchKernelGGL(moe_topk_select_kernel<1>, g, b, 0, st, logits, T, E, K, wmode, mb);
   else
-    hipLaunchKernelGGL(moe_topk_select_kernel<2>, g, b, 0, st, logits, T, E, K, (int)bf16, mb);
+    hipLaunchKernelGGL(moe_topk_select_kernel<2>, g, b, 0, st, logits, T, E, K, wmode, mb);
   hipLaunchKernelGGL(moe_route_build_kernel, dim3(1), dim3(1024), 0, st, T, E, K, mb, L.max_tiles,
                      L.bm);
 }
 
-template <bool BF16, class BP, bool GATHER, bool GATED, bool OUT_PERM>
+template <bool BF16, class BP, bool GATHER, bool GATED, bool OUT_PERM, int GS = 0>
 void launch_moe_gemm(const MoeLayout& L, const void* A, int lda, const MoeBuffers& mb, const BP& bp,
-                     const BP& bp2, void* out, int ldo, int N, int K, hipStream_t st) {
+                     const BP& bp2, void* out, int ldo, int N, int K, hipStream_t st,
+                     const uint16_t* fscales = nullptr, size_t fs_stride = 0) {
   const dim3 grid(N / 128, L.max_tiles);
   if (L.bm == 64)
-    hipLaunchKernelGGL((moe_gemm_kernel<BF16, 64, BP, GATHER, GATED, OUT_PERM>), grid, dim3(256), 0,
-                       st, (const uint16_t*)A, lda, mb.perm, mb.tiles, bp, bp2, (uint16_t*)out, ldo, N,
-                       K, L.topk);
+    hipLaunchKernelGGL((moe_gemm_kernel<BF16, 64, BP, GATHER, GATED, OUT_PERM, GS>), grid, dim3(256),
+                       0, st, (const uint16_t*)A, lda, mb.perm, mb.tiles, bp, bp2, (uint16_t*)out,
+                       ldo, N, K, L.topk, fscales, fs_stride);
   else
-    hipLaunchKernelGGL((moe_gemm_kernel<BF16, 128, BP, GATHER, GATED, OUT_PERM>), grid, dim3(256), 0,
-                       st, (const uint16_t*)A, lda, mb.perm, mb.tiles, bp, bp2, (uint16_t*)out, ldo, N,
-                       K, L.topk);
+    hipLaunchKernelGGL((moe_gemm_kernel<BF16, 128, BP, GATHER, GATED, OUT_PERM, GS>), grid,
+                       dim3(256), 0, st, (const uint16_t*)A, lda, mb.perm, mb.tiles, bp, bp2,
+                       (uint16_t*)out, ldo, N, K, L.topk, fscales, fs_stride);
+}
+
+// The reference qMoE op's expert GEMM: exact integer weights, the scales folded per group
+// (GS = group / TBK slabs), fp32 outputs per (token, k) row.
+template <bool BF16>
+void launch_qmoe_gemm(const MoeLayout& L, const void* x, const MoeBuffers& mb, const int8_t* q,
+                      const void* scales, void* o, int D, int N, int group, hipStream_t st) {
+  const I8QSlabPolicy<BF16> bp{q, N, (size_t)D * N};
+  const uint16_t* sc = (const uint16_t*)scales;
+  const size_t ss = (size_t)(D / group) * N;
+  using BP = I8QSlabPolicy<BF16>;
+  switch (group / TBK) {
+    case 1: return launch_moe_gemm<BF16, BP, true, false, true, 1>(L, x, D, mb, bp, bp, o, N, N, D, st, sc, ss);
+    case 2: return launch_moe_gemm<BF16, BP, true, false, true, 2>(L, x, D, mb, bp, bp, o, N, N, D, st, sc, ss);
+    case 4: return launch_moe_gemm<BF16, BP, true, false, true, 4>(L, x, D, mb, bp, bp, o, N, N, D, st, sc, ss);
+    default: return launch_moe_gemm<BF16, BP, true, false, true, 8>(L, x, D, mb, bp, bp, o, N, N, D, st, sc, ss);
+  }
 }
 
 template <bool BF16>
@@ -794,7 +875,7 @@ bool moe_shape_ok(int T, int E, int K, int N, int group) {
 extern "C" size_t kbh_qmoe_workspace_bytes(int T, int D, int N, int E) {
   (void)D;
   if (T <= 0 || E <= 0) return 0;
-  return kbh::moe_layout(T, E, 0, N).total;
+  return kbh::moe_layout(T, E, 0, N, 0, 0, 2, true).total;
 }
 
 extern "C" int kbh_moe_route_top2(const void* router_logits, int logits_dtype, int32_t* topi,
@@ -802,14 +883,16 @@ extern "C" int kbh_moe_route_top2(const void* router_logits, int logits_dtype, i
                                   int E, int dtype, void* stream) {
   using namespace kbh;
   if (!router_logits || !topi || !topw || !workspace) return KBH_ERR_NULL;
-  if (logits_dtype < 0 || logits_dtype > 2 || (dtype != KBH_F16 && dtype != KBH_BF16)) return KBH_ERR_DTYPE;
+  if (logits_dtype < 0 || logits_dtype > 2 ||
+      (dtype != KBH_F16 && dtype != KBH_BF16 && dtype != KBH_F32))
+    return KBH_ERR_DTYPE;
   if (T < 1 || E < 2 || E > kMoeMaxExperts) return KBH_ERR_SHAPE;
   const MoeLayout L = moe_layout(T, E, 0, 0);
   if (workspace_bytes < L.total) return KBH_ERR_WORKSPACE;
   MoeBuffers mb = moe_buffers(workspace, L);
   mb.topi = topi;
   mb.topw = (uint16_t*)topw;
-  launch_route_topk(router_logits, logits_dtype, T, E, dtype == KBH_BF16, mb, L, (hipStream_t)stream);
+  launch_route_topk(router_logits, logits_dtype, T, E, dtype, mb, L, (hipStream_t)stream);
   return launch_status();
 }
 
@@ -823,22 +906,23 @@ extern "C" int kbh_qmoe(const void* x, const int8_t* qweight, const void* scales
   if (logits_dtype < 0 || logits_dtype > 2) return KBH_ERR_DTYPE;
   if (!moe_shape_ok(T, E, D, N, group)) return KBH_ERR_SHAPE;
   if (!aligned16(x) || !aligned16(qweight) || !aligned16(scales) || !aligned16(y)) return KBH_ERR_ALIGN;
-  const MoeLayout L = moe_layout(T, E, 0, N);
+  const MoeLayout L = moe_layout(T, E, 0, N, 0, 0, 2, true);
   if (workspace_bytes < L.total) return KBH_ERR_WORKSPACE;
   const MoeBuffers mb = moe_buffers(workspace, L);
   hipStream_t st = (hipStream_t)stream;
   void* o = (char*)workspace + L.o;
   const bool bf = dtype == KBH_BF16;
-  launch_route_topk(router_logits, logits_dtype, T, E, bf, mb, L, st);
-  const size_t ws_ = (size_t)D * N, ss_ = (size_t)(D / group) * N;
+  launch_route_topk(router_logits, logits_dtype, T, E, dtype, mb, L, st);
+  const size_t n = (size_t)T * N;
+  const dim3 cgrid((unsigned)((n / 4 + 255) / 256));
   if (bf) {
-    const I8KSlabPolicy<true> bp{qweight, (const uint16_t*)scales, N, group, ws_, ss_};
-    launch_moe_gemm<true, I8KSlabPolicy<true>, true, false, true>(L, x, D, mb, bp, bp, o, N, N, D, st);
-    launch_combine<true>(o, mb.topw, y, T, N, st);
+    launch_qmoe_gemm<true>(L, x, mb, qweight, scales, o, D, N, group, st);
+    hipLaunchKernelGGL(moe_combine_f32_kernel<true>, cgrid, dim3(256), 0, st, (const float*)o,
+                       mb.topw32, (uint16_t*)y, T, N);
   } else {
-    const I8NSlabPolicy bp{qweight, (const uint16_t*)scales, N, group, ws_, ss_};
-    launch_moe_gemm<false, I8NSlabPolicy, true, false, true>(L, x, D, mb, bp, bp, o, N, N, D, st);
-    launch_combine<false>(o, mb.topw, y, T, N, st);
+    launch_qmoe_gemm<false>(L, x, mb, qweight, scales, o, D, N, group, st);
+    hipLaunchKernelGGL(moe_combine_f32_kernel<false>, cgrid, dim3(256), 0, st, (const float*)o,
+                       mb.topw32, (uint16_t*)y, T, N);
   }
   return launch_status();
 }
@@ -885,7 +969,7 @@ extern "C" int kbh_qmoe_ffn(const void* x, const void* router_logits, int logits
   void* h = (char*)workspace + L.h;
   void* o = (char*)workspace + L.o;
   const bool bf = dtype == KBH_BF16;
-  launch_route_topk(router_logits, logits_dtype, T, E, bf, mb, L, st);
+  launch_route_topk(router_logits, logits_dtype, T, E, dtype, mb, L, st);
   // gate/up: [D -> F] packed along F; down: [F -> D] packed along D
   const size_t gq = (size_t)D * (F / 8), gs = (size_t)(D / group) * F;
   const size_t dq = (size_t)F * (D / 8), ds = (size_t)(F / group) * D;
@@ -929,7 +1013,9 @@ extern "C" int kbh_moe_route_topk(const void* router_logits, int logits_dtype, i
                                   int E, int topk, int dtype, void* stream) {
   using namespace kbh;
   if (!router_logits || !topi || !topw || !workspace) return KBH_ERR_NULL;
-  if (logits_dtype < 0 || logits_dtype > 2 || (dtype != KBH_F16 && dtype != KBH_BF16)) return KBH_ERR_DTYPE;
+  if (logits_dtype < 0 || logits_dtype > 2 ||
+      (dtype != KBH_F16 && dtype != KBH_BF16 && dtype != KBH_F32))
+    return KBH_ERR_DTYPE;
   if (T < 1 || E < 2 || E > kMoeMaxExperts || topk < 1 || topk > kMoeMaxTopk || topk > E)
     return KBH_ERR_SHAPE;
   const MoeLayout L = moe_layout(T, E, 0, 0, 0, 0, topk);
@@ -937,7 +1023,7 @@ extern "C" int kbh_moe_route_topk(const void* router_logits, int logits_dtype, i
   MoeBuffers mb = moe_buffers(workspace, L);
   mb.topi = topi;
   mb.topw = (uint16_t*)topw;
-  launch_route_topk(router_logits, logits_dtype, T, E, dtype == KBH_BF16, mb, L, (hipStream_t)stream);
+  launch_route_topk(router_logits, logits_dtype, T, E, dtype, mb, L, (hipStream_t)stream);
   return launch_status();
 }
 
@@ -957,7 +1043,7 @@ extern "C" int kbh_moe(const void* x, const void* w, const void* router_logits, 
   hipStream_t st = (hipStream_t)stream;
   void* o = (char*)workspace + L.o;
   const bool bf = dtype == KBH_BF16;
-  launch_route_topk(router_logits, logits_dtype, T, E, bf, mb, L, st);
+  launch_route_topk(router_logits, logits_dtype, T, E, dtype, mb, L, st);
   const F16SlabPolicy bp{(const uint16_t*)w, H, (size_t)D * H};
   const size_t n4 = (size_t)T * H / 4;
   const dim3 cgrid((unsigned)((n4 + 255) / 256));

@@ -125,12 +125,13 @@ def qmoe(T: int = 256, D: int = 4096, E: int = 8, N: int = 14336,
          dtype: torch.dtype = torch.float16, seed: int = 0, group: int = 128):
     """[x, qweight, scales, router_logits] with the distributions of the reference qMoE task
     (reference.py:23-29): qweight int8 in [-8, 7], scales N(0,1)*0.01 [E, D/group, N] (the
-    reference's GROUP is 128), logits in x.dtype."""
+    reference's GROUP is 128), logits N(0,1) in x.dtype, drawn as the reference draws them
+    (ties included: the routing follows torch.topk's GPU order on ties)."""
     g = _gen(seed)
     x = torch.randn(T, D, generator=g).to(dtype)
     qweight = torch.randint(-8, 8, (E, D, N), generator=g, dtype=torch.int8)
     scales = (torch.randn(E, D // group, N, generator=g) * 0.01).to(dtype)
-    logits = _distinct_logits(T, E, g, dtype)
+    logits = torch.randn(T, E, generator=g).to(dtype)
     return [x, qweight, scales, logits]
 
 
@@ -157,30 +158,15 @@ def silu_fp8(T: int = 512, H: int = 14336, dtype: torch.dtype = torch.float16, s
     return [torch.randn(T, 2 * H, generator=g).to(dtype)]
 
 
-def _topk_distinct_logits(T: int, E: int, k: int, g: torch.Generator,
-                          dtype: torch.dtype) -> torch.Tensor:
-    """N(0,1) router logits in `dtype` whose k+1 largest per row are distinct (rows with a tie
-    there are re-drawn), so the top-k selection and its order do not depend on tie-breaking."""
-    lg = torch.randn(T, E, generator=g).to(dtype)
-    m = min(k + 1, E)
-    while True:
-        top = lg.float().topk(m, dim=-1).values
-        bad = (top[:, :-1] <= top[:, 1:]).any(dim=-1) if m > 1 else torch.zeros(T, dtype=torch.bool)
-        n = int(bad.sum())
-        if n == 0:
-            return lg
-        lg[bad] = torch.randn(n, E, generator=g).to(dtype)
-
-
 def moe(T: int = 16, D: int = 4096, E: int = 8, H: int = 14336, topk: int = 2,
         dtype: torch.dtype = torch.float16, seed: int = 0):
     """[x, w, router_logits] with the distributions of the reference moe task
     (tasks/moe/*/environment/reference.py:19-24): x N(0,1), w N(0,1)*0.02, logits N(0,1), all in
-    dtype (logits re-drawn per row where the top-(k+1) would tie)."""
+    dtype, drawn as the reference draws them (ties included). `topk` does not change the draw."""
     g = _gen(seed)
     x = torch.randn(T, D, generator=g).to(dtype)
     w = (torch.randn(E, D, H, generator=g) * 0.02).to(dtype)
-    logits = _topk_distinct_logits(T, E, topk, g, dtype)
+    logits = torch.randn(T, E, generator=g).to(dtype)
     return [x, w, logits]
 
 

@@ -292,6 +292,8 @@ def mxfp8_gemm(a: torch.Tensor, a_scale: torch.Tensor, b: torch.Tensor, b_scale:
 
 
 _LOGIT_CODE = {torch.float16: 0, torch.bfloat16: 1, torch.float32: 2}
+# Routing weights may also come back unrounded (fp32): KBH_F32.
+_W_CODE = {torch.float16: _lib.KBH_F16, torch.bfloat16: _lib.KBH_BF16, torch.float32: _lib.KBH_F32}
 
 
 def _check_logits(router_logits, T):
@@ -306,9 +308,10 @@ def _check_logits(router_logits, T):
 
 
 def moe_route_top2(router_logits: torch.Tensor, dtype: torch.dtype = torch.float16):
-    """(topi [T, 2] int32, topw [T, 2] dtype): softmax(fp32 logits), top-2, renormalised
-    (tasks/fused_qmoe/*/environment/reference.py:14-16)."""
-    _require(dtype in _DT_CODE, lambda: f"dtype must be float16 or bfloat16, got {dtype}")
+    """(topi [T, 2] int32, topw [T, 2] dtype): softmax(fp32 logits), top-2 in the order
+    torch.topk returns on the GPU, renormalised (tasks/fused_qmoe/*/environment/
+    reference.py:14-16); dtype float16, bfloat16 or float32 (unrounded weights)."""
+    _require(dtype in _W_CODE, lambda: f"dtype must be float16, bfloat16 or float32, got {dtype}")
     T = router_logits.shape[0]
     E = _check_logits(router_logits, T)
     dev = _check_device(router_logits)
@@ -321,7 +324,7 @@ def moe_route_top2(router_logits: torch.Tensor, dtype: torch.dtype = torch.float
     ws = scratches.get(lib.kbh_qmoe_workspace_bytes(T, 0, 0, E), dev, st)
     st = lib.kbh_moe_route_top2(router_logits.contiguous().data_ptr(), _LOGIT_CODE[router_logits.dtype],
                                 topi.data_ptr(), topw.data_ptr(), ws.data_ptr(), ws.numel(), T, E,
-                                _DT_CODE[dtype], st)
+                                _W_CODE[dtype], st)
     _lib.check(st, "kbh_moe_route_top2")
     return topi, topw
 
@@ -440,10 +443,11 @@ def silu_fp8_quant(y: torch.Tensor, group: int = 128, return_codes: bool = False
 
 
 def moe_route_topk(router_logits: torch.Tensor, topk: int, dtype: torch.dtype = torch.float16):
-    """(topi [T, topk] int32, topw [T, topk] dtype): softmax(fp32 logits), top-k in descending
-    order (lower index first on a tie), weights renormalised and rounded to dtype
+    """(topi [T, topk] int32, topw [T, topk] dtype): softmax(fp32 logits), top-k in the order
+    torch.topk returns on the GPU (descending; the lower indices win a tie at the boundary),
+    weights renormalised and rounded to dtype, or unrounded for float32
     (tasks/moe/*/environment/reference.py:11-13)."""
-    _require(dtype in _DT_CODE, lambda: f"dtype must be float16 or bfloat16, got {dtype}")
+    _require(dtype in _W_CODE, lambda: f"dtype must be float16, bfloat16 or float32, got {dtype}")
     T = router_logits.shape[0]
     E = _check_logits(router_logits, T)
     _require(1 <= topk <= min(8, E), lambda: f"topk must be in [1, min(8, E={E})], got {topk}")
@@ -457,7 +461,7 @@ def moe_route_topk(router_logits: torch.Tensor, topk: int, dtype: torch.dtype = 
     ws = scratches.get(lib.kbh_moe_workspace_bytes(T, 0, 0, E, topk), dev, st)
     st = lib.kbh_moe_route_topk(router_logits.contiguous().data_ptr(),
                                 _LOGIT_CODE[router_logits.dtype], topi.data_ptr(), topw.data_ptr(),
-                                ws.data_ptr(), ws.numel(), T, E, topk, _DT_CODE[dtype],
+                                ws.data_ptr(), ws.numel(), T, E, topk, _W_CODE[dtype],
                                 st)
     _lib.check(st, "kbh_moe_route_topk")
     return topi, topw

@@ -17,14 +17,17 @@ import numpy as np
 
 from .numerics import F32, round_to
 from .qmoe import softmax_fp32
+from .topk import device_topk_ids
 
 
 def route_topk(logits, k: int, dtype: str = F32):
-    """:11-13 — ids [T, k] (descending probability; the lower index first on a tie) and weights
-    topv / sum(topv) (summed in k order) rounded to dtype."""
+    """:11-13 — ids [T, k] in the order torch.topk returns them on the GPU (oracle/topk.py:
+    descending probability; the lower indices win a tie at the boundary, equal selected values
+    in the order of torch's bitonic sort) and weights topv / sum(topv) (summed in that order)
+    rounded to dtype."""
     p = softmax_fp32(logits)
     T = p.shape[0]
-    order = np.argsort(-p, axis=-1, kind="stable")[:, :k]
+    order = device_topk_ids(p, k)
     topv = p[np.arange(T)[:, None], order].astype(np.float32)
     s = np.zeros((T, 1), np.float32)
     for j in range(k):

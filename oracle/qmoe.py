@@ -11,6 +11,7 @@ import numpy as np
 
 from . import w4a16
 from .numerics import F32, round_to
+from .topk import device_topk_ids
 
 
 def softmax_fp32(logits) -> np.ndarray:
@@ -21,11 +22,12 @@ def softmax_fp32(logits) -> np.ndarray:
 
 
 def route_top2(logits, dtype: str = F32):
-    """reference.py:14-16: probabilities, top-2 (descending; the lower index first on a tie),
-    weights topv / sum(topv) rounded to the activation dtype."""
+    """reference.py:14-16: probabilities, top-2 in the order torch.topk returns them on the GPU
+    (oracle/topk.py: the lower indices win a tie at the boundary; two equal selected values come
+    out higher index first), weights topv / sum(topv) rounded to the activation dtype."""
     p = softmax_fp32(logits)
     T = p.shape[0]
-    order = np.argsort(-p, axis=-1, kind="stable")[:, :2]
+    order = device_topk_ids(p, 2)
     topv = p[np.arange(T)[:, None], order]
     w = (topv / topv.sum(axis=-1, keepdims=True)).astype(np.float32)
     return order.astype(np.int64), round_to(w, dtype)

@@ -71,6 +71,30 @@ def test_grade_five_draws(dev, family):
     assert res.correct
 
 
+# The six fused_qmoe tasks (generate_tasks.py:390-394, 617-626): (config, D, E, N) x dtype,
+# T = 256, router logits drawn in x.dtype exactly as get_inputs draws them (no tie filtering).
+FUSED_QMOE = [(n, D, E, N, dt) for (n, D, E, N) in (("deepseek_moe", 2048, 64, 1408),
+                                                     ("mixtral", 4096, 8, 14336),
+                                                     ("qwen_moe", 2048, 60, 1408))
+              for dt in (torch.float16, torch.bfloat16)]
+
+
+@pytest.mark.parametrize("name,D,E,N,dtype", FUSED_QMOE)
+def test_grade_fused_qmoe_tasks(dev, name, D, E, N, dtype):
+    """The reference grader's verdict on every fused_qmoe task: five fresh draws, each within the
+    BASELINE gate and the task's allclose(2e-2, 2e-2) against the ground truth the grader
+    computes (the reference forward on fp32-upcast inputs on the device). The reference's own
+    bf16 path fails that allclose on these shapes; the drop-in's fp32 evaluation does not."""
+    print(f"[grade qmoe] {name} {dtype}", flush=True)
+    make = lambda s: inputs.qmoe(256, D, E, N, dtype, seed=s)
+    res = harness.grade(modules.QMoEModel(), _draws(make, dev), _ref_gt(tr.qmoe), draws=DRAWS,
+                        family="fused_qmoe")
+    assert res.error is None, res.error
+    for d in res.draws:
+        assert d["ok"] and d["task_ok"], (name, dtype, d)
+    assert res.correct
+
+
 def test_bench_protocol_times(dev):
     ins = [t.to(dev) for t in inputs.w4a16(16, 14336, 4096, 128, F16, seed=7)]
     m = modules.W4A16Model()

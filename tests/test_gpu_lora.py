@@ -9,7 +9,6 @@ import pytest
 import torch
 
 from kernelbench_harbor_amd import MultiLoRAQGemmModel, inputs, ops
-from _grader import grader_ok
 from kernelbench_harbor_amd.harness import compare
 from oracle import lora as ol
 
@@ -34,8 +33,7 @@ def test_reference_task(dev, name, D, N, r, L, dtype):
     gt = ol.forward(*_np(ins))
     cmp = compare(y, gt)
     assert cmp.ok, cmp
-    dt = "f16" if dtype == torch.float16 else "bf16"
-    assert grader_ok(cmp, "multi_lora_qgemm", gt, lambda: ol.forward(*_np(ins), dtype=dt)), cmp
+    assert cmp.task_ok("multi_lora_qgemm"), cmp
     assert torch.equal(y, MultiLoRAQGemmModel()(*[t.to(dev) for t in ins]))
 
 

@@ -11,7 +11,6 @@ import pytest
 import torch
 
 from kernelbench_harbor_amd import MoEModel, MoETop6Model, MoETop8Model, inputs, ops
-from _grader import grader_ok
 from kernelbench_harbor_amd.harness import compare
 from oracle import moe as om
 
@@ -26,7 +25,7 @@ def _f(t):
 @pytest.mark.parametrize("ldt", [torch.float16, torch.bfloat16, torch.float32])
 def test_route_topk(dev, E, k, ldt):
     g = torch.Generator().manual_seed(E + k)
-    lg = inputs._topk_distinct_logits(333, E, k, g, ldt)
+    lg = torch.randn(333, E, generator=g).to(ldt)   # ties included (the oracle orders them as torch)
     topi, topw = ops.moe_route_topk(lg.to(dev), k, torch.float16)
     oi, ow = om.route_topk(_f(lg), k, "f16")
     assert np.array_equal(topi.cpu().numpy(), oi)
@@ -110,5 +109,4 @@ def test_moe_task(dev, name, D, E, H, k, T, dtype):
         gt = om.forward(*args)
         cmp = compare(y[:, c], gt)
         assert cmp.ok, (c, cmp)
-        dt = "f16" if dtype == torch.float16 else "bf16"
-        assert grader_ok(cmp, "moe", gt, lambda: om.forward(*args, dtype=dt)), (c, cmp)
+        assert cmp.task_ok("moe"), (c, cmp)

@@ -6,6 +6,7 @@ import torch
 from kernelbench_harbor_amd import QMoEFFNModel, QMoEModel, inputs, ops
 from kernelbench_harbor_amd.harness import compare
 from oracle import qmoe as oq
+from oracle.numerics import round_to
 
 pytestmark = pytest.mark.gpu
 
@@ -44,51 +45,55 @@ def test_qmoe_parity(dev, T, D, E, N, dtype):
     assert cmp.ok, cmp
 
 
-@pytest.mark.parametrize("group", [32, 64, 256])
+def _one_hot_want(q, s, ks, gi, gw, dt):
+    """One-hot rows of x make expert e's output row q[e][k] * s[e][k / G] exactly (integer B
+    operands, one fp32 product per group), so kbh_qmoe's result is the fp32 combine of those
+    rows with the GPU's fp32 routing weights, rounded once to dt."""
+    W = {e: oq.dequant_expert(q[e].numpy(), s[e].float().numpy(), "f32") for e in np.unique(gi)}
+    T = len(ks)
+    out_k = [np.stack([W[gi[t, k]][ks[t]] for t in range(T)]) for k in range(2)]
+    return round_to(oq.combine(out_k, gw, "f32"), dt)
+
+
+@pytest.mark.parametrize("group", [32, 64, 128, 256])
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
 def test_qmoe_group_sizes(dev, group, dtype):
-    """Scale groups other than the reference's 128 (the producers index scale row k0 / group):
-    tolerance against the ground truth, and one-hot activations bit-exact against the native
-    path."""
+    """Every scale group (the fold scales each group's fp32 sums): tolerance against the ground
+    truth, and one-hot activations bit-exact against the fp32 combine of exact weight rows."""
     print(f"[qmoe group] g{group} {dtype}", flush=True)
     T, D, E, N = 96, 1024, 8, 256
     x, q, s, lg = inputs.qmoe(T, D, E, N, dtype, seed=group, group=group)
     y = ops.qmoe(*[t.to(dev) for t in (x, q, s, lg)])
     cmp = compare(y, oq.qmoe_forward(*_np([x, q, s, lg])))
-    assert cmp.ok, cmp
-    # One-hot rows: each expert output is one dequantised weight row, so the result must equal
-    # the native-dtype combine of those rows bit for bit. The routing weights are the GPU's own
-    # (its exp may put a renormalised weight one ulp away from numpy's on a rounding tie; the
-    # routing is checked separately), the expert ids must match the oracle's.
+    assert cmp.ok and cmp.allclose_ref, cmp
     g = torch.Generator().manual_seed(group + 1)
     ks = torch.randint(0, D, (T,), generator=g)
     xo = torch.zeros(T, D, dtype=dtype)
     xo[torch.arange(T), ks] = 1.0
     yo = ops.qmoe(*[t.to(dev) for t in (xo, q, s, lg)]).float().cpu().numpy()
     dt = "f16" if dtype == torch.float16 else "bf16"
-    gi, gw = ops.moe_route_top2(lg.to(dev), dtype)
-    gi, gw = gi.cpu().numpy(), gw.float().cpu().numpy()
-    assert np.array_equal(gi, oq.route_top2(lg.float().numpy(), dt)[0])
-    W = {e: oq.dequant_expert(q[e].numpy(), s[e].float().numpy(), dt) for e in np.unique(gi)}
-    rows = [[W[e][ks[t]] for e in gi[t]] for t in range(T)]
-    out_k = [np.stack([rows[t][k] for t in range(T)]) for k in range(2)]
-    want = oq.combine(out_k, gw, dt)
+    gi, gw = ops.moe_route_top2(lg.to(dev), torch.float32)
+    gi, gw = gi.cpu().numpy(), gw.cpu().numpy()
+    assert np.array_equal(gi, oq.route_top2(lg.float().numpy())[0])
+    want = _one_hot_want(q, s, ks.numpy(), gi, gw, dt)
     assert np.array_equal(yo, want), np.abs(yo - want).max()
 
 
-def test_qmoe_one_hot_matches_native_rounding(dev):
-    """One-hot activations make each expert output a dequantized weight row (one rounding), so
-    the GPU result must equal the oracle's fp16 path (dequant, products and sum rounded as the
-    reference) bit for bit."""
+def test_qmoe_one_hot_full_range_int8(dev):
+    """Integer weights over the whole int8 range (the producers convert any int8 exactly) with
+    signed, subnormal-free scales: one-hot rows bit-exact in fp16 and bf16."""
     T, D, E, N = 64, 512, 4, 256
-    x, q, s, lg = inputs.qmoe(T, D, E, N, torch.float16, seed=5)
-    g = torch.Generator().manual_seed(6)
-    ks = torch.randint(0, D, (T,), generator=g)
-    x = torch.zeros(T, D, dtype=torch.float16)
-    x[torch.arange(T), ks] = 1.0
-    y = ops.qmoe(x.to(dev), q.to(dev), s.to(dev), lg.to(dev)).float().cpu().numpy()
-    want = oq.qmoe_forward(*_np([x, q, s, lg]), dtype="f16")
-    assert np.array_equal(y, want), np.abs(y - want).max()
+    for dtype, dt in ((torch.float16, "f16"), (torch.bfloat16, "bf16")):
+        x, _, s, lg = inputs.qmoe(T, D, E, N, dtype, seed=5)
+        q = torch.randint(-128, 128, (E, D, N), generator=torch.Generator().manual_seed(6),
+                          dtype=torch.int8)
+        ks = torch.randint(0, D, (T,), generator=torch.Generator().manual_seed(7))
+        xo = torch.zeros(T, D, dtype=dtype)
+        xo[torch.arange(T), ks] = 1.0
+        y = ops.qmoe(xo.to(dev), q.to(dev), s.to(dev), lg.to(dev)).float().cpu().numpy()
+        gi, gw = ops.moe_route_top2(lg.to(dev), torch.float32)
+        want = _one_hot_want(q, s, ks.numpy(), gi.cpu().numpy(), gw.cpu().numpy(), dt)
+        assert np.array_equal(y, want), (dt, np.abs(y - want).max())
 
 
 def test_qmoe_full_size(dev):

@@ -10,8 +10,10 @@ its three configurations in fp16 and bf16 (generate_tasks.py:390-394, 617-626; T
 The GEMMs are checked against the oracle on the first and last 256 output columns (the oracle's
 dense fp32 dequantisation of a 70B-model layer would dominate the suite's time; both slices
 cross every K split and group); W8A8 bit-exactly, the others to the BASELINE tolerances and to
-the reference grader's own allclose(atol = rtol = 2e-2) wherever the reference's native-dtype
-output meets it (tests/_grader.py). The qMoE output is checked whole.
+the reference grader's own allclose(atol = rtol = 2e-2) on every task, bf16 included (the
+reference's own bf16 intermediates fail that allclose on the bf16 W4A16 and qMoE tasks; these
+kernels scale after the MFMA and combine in fp32, so they stay inside it). The qMoE output is
+checked whole.
 """
 import functools
 
@@ -20,7 +22,6 @@ import pytest
 import torch
 
 from kernelbench_harbor_amd import FP8WModel, QMoEModel, W4A16Model, W8A8Model, inputs
-from _grader import grader_ok
 from kernelbench_harbor_amd.harness import compare
 from oracle import fp8w as of
 from oracle import qmoe as oq
@@ -87,7 +88,7 @@ def test_w4a16_task(dev, name, K, N, group, dtype):
         gt = ow.forward(*args)
         cmp = compare(y[:, c], gt)
         assert cmp.ok, (c, cmp)
-        assert grader_ok(cmp, "quant_w4a16_pa", gt, lambda: ow.forward(*args, dtype=_dt(dtype))), (c, cmp)
+        assert cmp.task_ok("quant_w4a16_pa"), (c, cmp)
 
 
 W8_GRID = [(n, K, N, M) for (n, K, N) in LINEAR_SHAPES for M in (16, 64, 256)]
@@ -119,7 +120,7 @@ def test_fp8w_task(dev, name, K, N, block, dtype):
         gt = of.forward(*args)
         cmp = compare(y[:, c], gt)
         assert cmp.ok, (c, cmp)
-        assert grader_ok(cmp, "fp8_microscale", gt, lambda: of.forward(*args, dtype=_dt(dtype))), (c, cmp)
+        assert cmp.task_ok("fp8_microscale"), (c, cmp)
 
 
 QMOE_GRID = [(n, D, E, N, dt) for (n, D, E, N) in FUSED_QMOE_CFG
@@ -137,4 +138,4 @@ def test_qmoe_task(dev, name, D, E, N, dtype):
     gt = oq.qmoe_forward(*args)
     cmp = compare(y, gt)
     assert cmp.ok, cmp
-    assert grader_ok(cmp, "fused_qmoe", gt, lambda: oq.qmoe_forward(*args, dtype=_dt(dtype))), cmp
+    assert cmp.task_ok("fused_qmoe"), cmp
