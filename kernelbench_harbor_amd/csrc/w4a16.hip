@@ -31,9 +31,6 @@
 // global memory straight into MFMA registers. Split-K partial sums use the caller's scratch.
 // Shapes it does not cover fall back to tiled_f16_gemm (256 x 128 LDS-staged tiles) or to the
 // decode kernel.
-#include <atomic>
-#include <mutex>
-
 #include "kbh_common.h"
 #include "splitk.h"
 #include "tiled_f16.h"
@@ -375,6 +372,8 @@ void dispatch_w4_wide(const W4Wide& w, const void* x, const int32_t* qw, const v
     dispatch_w4_wide_spg<BF16, 128, 128>(w, x, qw, s, z, y, scratch, M, N, K, group, st);
 }
 
+}  // namespace
+
 // Bytes of device memory the path a call takes needs beyond its inputs and outputs: the wide
 // kernel's split-K scratch, nothing for the LDS-staged kernel, or the decode kernel's split-K
 // workspace (the dispatch order of kbh_w4a16_gemm).
@@ -387,44 +386,6 @@ size_t w4a16_path_bytes(int M, int N, int K, int group) {
   return splitk_workspace_bytes(M, N, p.splits);
 }
 
-// ---- fixed scratch of the entry point that allocates nothing ---------------------------
-// kbh_w4a16_gemm_noalloc keeps its split-K partial sums in this array instead of a caller
-// buffer. Each GPU the library runs on holds its own copy, at its own address, until the
-// process ends. In host code the name is only a stand-in for the symbol: the device address
-// comes from hipGetSymbolAddress, once per device, with that device current.
-static __device__ __align__(256) uint8_t scratch[KBH_W4A16_NOALLOC_SCRATCH_BYTES];
-
-constexpr int kMaxDevices = 64;
-std::atomic<void*> g_scratch_ptr[kMaxDevices];
-std::mutex g_scratch_mu;
-
-// Device address of `scratch` on the current device (looked up on the first call there).
-int noalloc_scratch(void** out) {
-  int dev = 0;
-  hipError_t e = hipGetDevice(&dev);
-  if (e != hipSuccess) {
-    set_last_hip_error((int)e);
-    return KBH_ERR_LAUNCH;
-  }
-  if (dev < 0 || dev >= kMaxDevices) return KBH_ERR_LAUNCH;
-  void* p = g_scratch_ptr[dev].load(std::memory_order_acquire);
-  if (!p) {
-    std::lock_guard<std::mutex> lock(g_scratch_mu);
-    p = g_scratch_ptr[dev].load(std::memory_order_relaxed);
-    if (!p) {
-      e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
-      if (e != hipSuccess || !p) {
-        set_last_hip_error((int)e);
-        return KBH_ERR_LAUNCH;
-      }
-      g_scratch_ptr[dev].store(p, std::memory_order_release);
-    }
-  }
-  *out = p;
-  return KBH_OK;
-}
-
-}  // namespace
 }  // namespace kbh
 
 extern "C" size_t kbh_w4a16_workspace_bytes(int M, int N, int K, int group) {
@@ -490,26 +451,4 @@ extern "C" int kbh_w4a16_gemm(const void* x, const int32_t* qweight, const void*
   if (bf) dispatch_decode<true>(p, x, qweight, scales, zeros, y, acc, M, N, K, group, st);
   else dispatch_decode<false>(p, x, qweight, scales, zeros, y, acc, M, N, K, group, st);
   return launch_status();
-}
-
-// Same GEMM with its split-K partial sums in the library's fixed per-GPU array (see `scratch`):
-// no workspace, no allocation. Shapes whose path needs more than the array return
-// KBH_ERR_SCRATCH_LIMIT before any HIP call.
-extern "C" int kbh_w4a16_gemm_noalloc(const void* x, const int32_t* qweight, const void* scales,
-                                      const void* zeros, void* y, int M, int N, int K, int group,
-                                      int dtype, void* stream) {
-  using namespace kbh;
-  if (!x || !qweight || !scales || !zeros || !y) return KBH_ERR_NULL;
-  if (dtype != KBH_F16 && dtype != KBH_BF16) return KBH_ERR_DTYPE;
-  if (M < 1 || N < 128 || K < 32 || (N % 128) != 0 || (K % 32) != 0) return KBH_ERR_SHAPE;
-  if (group != 32 && group != 64 && group != 128 && group != 256) return KBH_ERR_SHAPE;
-  if (K % group != 0) return KBH_ERR_SHAPE;
-  const size_t need = w4a16_path_bytes(M, N, K, group);
-  if (need > KBH_W4A16_NOALLOC_SCRATCH_BYTES) return KBH_ERR_SCRATCH_LIMIT;
-  void* p = nullptr;
-  const int st = noalloc_scratch(&p);
-  if (st != KBH_OK) return st;
-  // The path uses one of the two buffers, so both may name the array.
-  return kbh_w4a16_gemm(x, qweight, scales, zeros, y, p, KBH_W4A16_NOALLOC_SCRATCH_BYTES, p,
-                        KBH_W4A16_NOALLOC_SCRATCH_BYTES, M, N, K, group, dtype, stream);
 }
