@@ -73,9 +73,10 @@ constexpr int kMoeMaxTopk = 8;
 constexpr int kTopkWaves = 4;  // tokens per workgroup of the select kernel
 constexpr int kTopkSlots = 32;  // slots of torch's small bitonic sort
 
-template <int LDT>
+template <int LDT, int K>
 __global__ __launch_bounds__(kTopkWaves * 64) void moe_topk_select_kernel(
-    const void* __restrict__ logits, int T, int E, int K, int wmode, MoeBuffers mb) {
+    const void* __restrict__ logits, int T, int E, int wmode, MoeBuffers mb) {
+  static_assert(K >= 1 && K <= kMoeMaxTopk, "top-k");
   constexpr int EPL = kMoeMaxExperts / 64;
   const int lane = threadIdx.x & 63;
   const int t = blockIdx.x * kTopkWaves + (threadIdx.x >> 6);
@@ -99,13 +100,10 @@ __global__ __launch_bounds__(kTopkWaves * 64) void moe_topk_select_kernel(
   for (int o = 32; o >= 1; o >>= 1) sum += __shfl_xor(sum, o, 64);
   // Selection: k rounds of a wave argmax; every lane ends with all picks (lv, li).
   unsigned taken = 0;
-  float lv[kMoeMaxTopk];
-  int li[kMoeMaxTopk];
+  float lv[K];
+  int li[K];
 #pragma unroll
-  for (int j = 0; j < kMoeMaxTopk; ++j) {
-    lv[j] = -INFINITY;
-    li[j] = 0;
-    if (j >= K) continue;
+  for (int j = 0; j < K; ++j) {
     float bv = -INFINITY;
     int be = kMoeMaxExperts;  // sentinel above every index
 #pragma unroll
@@ -131,13 +129,12 @@ __global__ __launch_bounds__(kTopkWaves * 64) void moe_topk_select_kernel(
   float sv = -INFINITY;
   int si = 0, ok = 0;
 #pragma unroll
-  for (int j = 0; j < kMoeMaxTopk; ++j) {
-    if (j >= K) continue;
+  for (int j = 0; j < K; ++j) {
     const int kj = (lv[j] > vk ? 0 : kMoeMaxExperts) + li[j];
     int rank = 0;
 #pragma unroll
-    for (int i = 0; i < kMoeMaxTopk; ++i)
-      if (i < K && (lv[i] > vk ? 0 : kMoeMaxExperts) + li[i] < kj) ++rank;
+    for (int i = 0; i < K; ++i)
+      if ((lv[i] > vk ? 0 : kMoeMaxExperts) + li[i] < kj) ++rank;
     if (rank == slot) { sv = lv[j]; si = li[j]; ok = 1; }
   }
   // torch's small sort: slots a < b = a ^ stride exchange when
@@ -153,7 +150,7 @@ __global__ __launch_bounds__(kTopkWaves * 64) void moe_topk_select_kernel(
     const bool dir = size < kTopkSlots && (((lo ? slot : slot ^ stride) & size) != 0);
     if ((((va > vb) && oka) || !okb) == dir) { sv = ov; si = oi; ok = ook; }
   };
-  if (K > 1) {
+  if constexpr (K > 1) {
 #pragma unroll
     for (int size = 2; size <= kTopkSlots; size *= 2)
 #pragma unroll
@@ -163,8 +160,7 @@ __global__ __launch_bounds__(kTopkWaves * 64) void moe_topk_select_kernel(
   const float pk = keep_f32(expf(sv - mx) / sum);
   float ps = 0.f;
 #pragma unroll
-  for (int j = 0; j < kMoeMaxTopk; ++j)
-    if (j < K) ps = keep_f32(ps + __shfl(pk, j, 64));
+  for (int j = 0; j < K; ++j) ps = keep_f32(ps + __shfl(pk, j, 64));
   if (lane < K) {
     const float w = keep_f32(pk / ps);
     mb.topi[K * t + lane] = si;
@@ -735,12 +731,22 @@ void launch_route_topk(const void* logits, int logits_dtype, int T, int E, int w
                        const MoeBuffers& mb, const MoeLayout& L, hipStream_t st) {
   const dim3 g((T + kTopkWaves - 1) / kTopkWaves), b(kTopkWaves * 64);
   const int K = L.topk;
-  if (logits_dtype == 0)
-    hipLaunchKernelGGL(moe_topk_select_kernel<0>, g, b, 0, st, logits, T, E, K, wmode, mb);
-  else if (logits_dtype == 1)
-    hipLaunchKernelGGL(moe_topk_select_kernel<1>, g, b, 0, st, logits, T, E, K, wmode, mb);
-  else
-    hipLaunchKernelGGL(moe_topk_select_kernel<2>, g, b, 0, st, logits, T, E, K, wmode, mb);
+  auto sel = [&](auto ldt) {
+    constexpr int LDT = decltype(ldt)::value;
+    switch (K) {
+#define KBH_SEL(K_)                                                                          \
+  case K_:                                                                                   \
+    hipLaunchKernelGGL((moe_topk_select_kernel<LDT, K_>), g, b, 0, st, logits, T, E, wmode,  \
+                       mb);                                                                  \
+    return;
+      KBH_SEL(1) KBH_SEL(2) KBH_SEL(3) KBH_SEL(4) KBH_SEL(5) KBH_SEL(6) KBH_SEL(7)
+      default: KBH_SEL(8)
+#undef KBH_SEL
+    }
+  };
+  if (logits_dtype == 0) sel(std::integral_constant<int, 0>{});
+  else if (logits_dtype == 1) sel(std::integral_constant<int, 1>{});
+  else sel(std::integral_constant<int, 2>{});
   hipLaunchKernelGGL(moe_route_build_kernel, dim3(1), dim3(1024), 0, st, T, E, K, mb, L.max_tiles,
                      L.bm);
 }
