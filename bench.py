@@ -60,9 +60,24 @@ PMC_TRAFFIC = {
     "fp8w (reference op) M=16 b128": 70_943_466,
     "qmoe_ffn T=512 D=4096 F=14336 E=8 top2": 1_229_346_633,
     "silu_fp8 (reference op) T=512 H=14336 g128": 61_112_077,
-    "qmoe (reference op) T=256 D=4096 N=14336 E=8": 534_829_326,
+    "qmoe (reference op) T=256 D=4096 N=14336 E=8": 570_156_646,
 }
 
+
+# Kernel time per op call of every record from the rocprofv3 kernel trace of the default bench
+# command (`rocprofv3 --kernel-trace --stats ... -- python3 -u bench.py`): the summed average
+# durations of the call's kbh:: kernels over the run. Dispatch tracing lengthens the small
+# kernels (W4A16 M=1: 13.2 us traced against 11.9 us graph-replayed). Table and commands:
+# profiles/bench_kernel_trace.md.
+KERNEL_TRACE_US = {
+    "w4a16 M=1": 13.20, "w4a16 M=4": 13.33, "w4a16 M=16": 15.21, "w4a16 M=64": 28.88,
+    "w4a16 M=256": 53.92, "w4a16 M=1024": 148.04, "w4a16 M=2048": 272.57,
+    "w8a8 M=16": 18.74, "w8a8 M=512": 59.18, "mxfp8 M=128": 32.44, "mxfp8 M=2048": 150.34,
+    "fp8w (reference op) M=16 b128": 20.43,
+    "qmoe_ffn T=512 D=4096 F=14336 E=8 top2": 955.46,
+    "silu_fp8 (reference op) T=512 H=14336 g128": 13.34,
+    "qmoe (reference op) T=256 D=4096 N=14336 E=8": 198.49,
+}
 
 def gemm_flops(M, N=N_DIM, K=K_DIM):
     return 2 * M * N * K
@@ -198,7 +213,7 @@ def record(name, ts, batched, by, fl, peak, **extra):
     med = ts[len(ts) // 2]
     bound, frac = roofline(batched, by, fl, peak)
     out = {"name": name, **extra, "seed": 0, "us_median": round(med * 1e6, 2),
-           "traffic": PMC_TRAFFIC.get(name),
+           "traffic": PMC_TRAFFIC.get(name), "kernel_trace_us": KERNEL_TRACE_US.get(name),
            "us_batched": round(batched * 1e6, 2), "tflops": round(fl / batched / 1e12, 2),
            "gbps": round(by / batched / 1e9, 1), "bound": bound, "roofline_frac": round(frac, 4),
            "bytes": by, "flops": fl}

@@ -28,6 +28,7 @@
 #include "kbh_common.h"
 #include "tiled_f16.h"
 #include "tiled_wide.h"
+#include "tiled_ws.h"
 #include "w4_dequant.h"
 
 namespace kbh {
@@ -621,6 +622,10 @@ struct W4PairPolicy {
     // dequantisation and LDS layout do not depend on the matrix
     g.template store_part<FAST>(r, gr, Bs, t, p);
   }
+  template <bool FAST>
+  __device__ void store_all(const Raw& r, const Grp& gr, uint8_t* Bs, int t) const {
+    g.template store_all<FAST>(r, gr, Bs, t);
+  }
 };
 
 // h[slot][n] = dtype(silu(gate) * up) from the paired accumulators (fp32 math, one rounding).
@@ -804,9 +809,14 @@ void launch_ffn_wide_spg(const FfnPlan& fp, const MoeLayout& L, const MoeBuffers
     const BP bp{gp, upp};
     const SiluPairOut<BF16> ep{(uint16_t*)h, F};
     const int grid = L.max_tiles * (2 * F / 256);
-    hipLaunchKernelGGL((tiled_wide_gemm<E, TM, 4, SPG, BP, SiluPairOut<BF16>, RM, 1, kFfnPD>),
-                       dim3(grid), dim3(256), 0, st, x, bp, ep, (float*)nullptr, 2 * T, 2 * F, D,
-                       1, D / 32, RM{mb.tiles, mb.perm});
+    if constexpr (TM == 128)
+      hipLaunchKernelGGL((tiled_ws_gemm<E, TM, 4, SPG, BP, SiluPairOut<BF16>, RM, kFfnPD>),
+                         dim3(grid), dim3(512), 0, st, x, bp, ep, (float*)nullptr, 2 * T, 2 * F,
+                         D, 1, D / 32, RM{mb.tiles, mb.perm});
+    else
+      hipLaunchKernelGGL((tiled_wide_gemm<E, TM, 4, SPG, BP, SiluPairOut<BF16>, RM, 1, kFfnPD>),
+                         dim3(grid), dim3(256), 0, st, x, bp, ep, (float*)nullptr, 2 * T, 2 * F,
+                         D, 1, D / 32, RM{mb.tiles, mb.perm});
   }
   // down: h rows in slot order, outputs (or split-K partials) in row 2t + k
   {
@@ -815,9 +825,14 @@ void launch_ffn_wide_spg(const FfnPlan& fp, const MoeLayout& L, const MoeBuffers
     const HalfOut<BF16> ep{(uint16_t*)o, D};
     const int splits = fp.down.splits;
     const int grid = L.max_tiles * (D / 256) * splits;
-    hipLaunchKernelGGL((tiled_wide_gemm<E, TM, 4, SPG, BP, HalfOut<BF16>, RM, 1, kFfnPD>),
-                       dim3(grid), dim3(256), 0, st, h, dp, ep, part, 2 * T, D, F, splits,
-                       fp.down.slabs_per_split, RM{mb.tiles, mb.perm});
+    if constexpr (TM == 128)
+      hipLaunchKernelGGL((tiled_ws_gemm<E, TM, 4, SPG, BP, HalfOut<BF16>, RM, kFfnPD>),
+                         dim3(grid), dim3(512), 0, st, h, dp, ep, part, 2 * T, D, F, splits,
+                         fp.down.slabs_per_split, RM{mb.tiles, mb.perm});
+    else
+      hipLaunchKernelGGL((tiled_wide_gemm<E, TM, 4, SPG, BP, HalfOut<BF16>, RM, 1, kFfnPD>),
+                         dim3(grid), dim3(256), 0, st, h, dp, ep, part, 2 * T, D, F, splits,
+                         fp.down.slabs_per_split, RM{mb.tiles, mb.perm});
     if (splits > 1) {
       const size_t n4 = (size_t)T * D / 4;
       hipLaunchKernelGGL((moe_reduce_combine_kernel<BF16>), dim3((unsigned)((n4 + 255) / 256)),

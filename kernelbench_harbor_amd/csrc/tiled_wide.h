@@ -61,10 +61,6 @@ namespace kbh {
 
 constexpr int WSLAB_BYTES = 64;  // bytes of K per row per slab
 
-#ifndef KBH_WIDE_SPLIT_PRODUCER
-#define KBH_WIDE_SPLIT_PRODUCER 1
-#endif
-
 template <bool B>
 struct WideFlag {
   static constexpr bool value = B;
@@ -150,6 +146,59 @@ struct WideShape {
   // Two workgroups per CU when the accumulators fit in 128 registers per lane.
   static constexpr int kMinBlocks = RB * CB <= 8 ? 2 : 1;
 };
+
+// A wave's accumulators ((TM/WM) x (TN*WM/4) of the tile at row block wm, column block wn)
+// through the output policy (splits == 1, or a paired policy) or into this split's slice of the
+// workspace (plain stores; wide_reduce_kernel sums the slices afterwards, ordered by the launch
+// boundary, so no device-scope fences or atomics are needed and the sum order is fixed).
+// Accumulator element e of tile (i, j): row 8(e/4) + 4(lane/32) + e%4, column lane%32.
+template <class E, int TM, int WM, int TN, class EP, class RM, int RB, int CB>
+__device__ inline void wide_store_tile(const typename E::Acc (&acc)[RB][CB], const EP& ep,
+                                       const RM& rm, const typename RM::Tile& ti,
+                                       typename E::Part* __restrict__ ws, int split, int splits,
+                                       int M, int N, int n0, int wm, int wn, int lane) {
+  constexpr int WN = 4 / WM;
+  const int fr = lane & 31, fg = lane >> 5;
+  const int rbase = wm * (TM / WM) + 4 * fg;
+  const int cbase = n0 + wn * 32 * CB + fr;
+  if constexpr (EP::kPaired) {
+    static_assert(WN == 1 && CB % 4 == 0, "paired output needs whole 128-column chunks per wave");
+#pragma unroll
+    for (int i = 0; i < RB; ++i)
+#pragma unroll
+      for (int j = 0; j < CB; ++j) {
+        if ((j & 3) >= 2) continue;  // second-matrix blocks pair with block j - 2
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+          const int r = rbase + 32 * i + 8 * (e >> 2) + (e & 3);
+          if (r < ti.rows)
+            ep.emit_pair(rm.out_row(ti, r), n0 / 2 + 64 * (j >> 2) + 32 * (j & 1) + fr,
+                         acc[i][j][e], acc[i][j + 2][e]);
+        }
+      }
+  } else if (splits == 1) {
+#pragma unroll
+    for (int i = 0; i < RB; ++i)
+#pragma unroll
+      for (int j = 0; j < CB; ++j)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+          const int r = rbase + 32 * i + 8 * (e >> 2) + (e & 3);
+          if (r < ti.rows) ep.emit(rm.out_row(ti, r), cbase + 32 * j, acc[i][j][e]);
+        }
+  } else {
+    typename E::Part* part = ws + (size_t)split * M * N;
+#pragma unroll
+    for (int i = 0; i < RB; ++i)
+#pragma unroll
+      for (int j = 0; j < CB; ++j)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+          const int r = rbase + 32 * i + 8 * (e >> 2) + (e & 3);
+          if (r < ti.rows) part[(size_t)rm.out_row(ti, r) * N + cbase + 32 * j] = acc[i][j][e];
+        }
+  }
+}
 
 // M: output rows (the size of a split-K slice); N: output columns of the weight producer (TN
 // per tile; paired producers: twice the real output columns).
@@ -293,18 +342,10 @@ tiled_wide_gemm(
   // FAST: the policy's faster producer path, valid when every weight constant of this
   // workgroup's K range and columns allows it (one check before the loop, then a separate copy
   // of the loop, so the loop itself has no branch). The 64- and 128-row tiles take it: there
-  // the producer is on the critical path (W4A16 M=256 57 -> 55 us, M=64 31 -> 30 us, MoE FFN
-  // 993 -> 974 us); with 256-row tiles the second copy of the loop spilled registers and ran
-  // no faster.
+  // the producer is on the critical path (measured on 256-column tiles, which now run on
+  // tiled_ws_gemm: W4A16 M=256 57 -> 55 us, MoE FFN 993 -> 974 us); with 256-row tiles the
+  // second copy of the loop spilled registers and ran no faster.
   constexpr bool kFast = BP::kHasFast && (TM == 64 || TM == 128);
-  // SP (split producer; 64-row tiles): the producer of a slab runs in two halves, the first
-  // beside the step-1 MFMAs of the slab two before it (into the LDS buffer whose step-1
-  // fragments were read before that slab's barrier), the second beside the step-0 MFMAs of the
-  // slab before it, instead of all of it beside the step-0 MFMAs, whose time it doubled. Needs
-  // raw weights two slabs ahead (PD >= 2). Measured: W4A16 M=64 31.1 -> 29.8 us; on 128-row
-  // tiles M=256 55.2 -> 55.9 us and the MoE FFN 982 -> 972 us, so those keep the one-piece
-  // producer.
-  constexpr bool SP = KBH_WIDE_SPLIT_PRODUCER && TM == 64 && PD >= 2 && BP::kParts % 2 == 0;
   bool fast = false;
   if constexpr (kFast) fast = __syncthreads_and(bp.scan_fast(kt0 * SK, (kt0 + KT) * SK, n0, t)) != 0;
   auto run = [&](auto fast_tag) {
@@ -328,18 +369,7 @@ tiled_wide_gemm(
 #pragma unroll
     for (int i = 1; i <= PD; ++i) load_b(R[i % PD], min(i, last));
     load_g(G[1], min(SPG, last));
-    constexpr int NP = BP::kParts, HP = NP / 2;
-    if constexpr (SP) {
-      // First half of slab 1 into buffer 1. With one slab per group, slab 1 starts the second
-      // group (set 1), and set 0 (slab 0's, done) is reloaded with the group of slab 2.
-      if constexpr (SPG == 1) {
-        bp.template prepare_group<FAST>(G[1]);
-        load_g(G[0], min(2, last));
-      }
-#pragma unroll
-      for (int p = 0; p < HP; ++p)
-        bp.template store_part<FAST>(R[1 % PD], G[SPG == 1 ? 1 : 0], Bs[1], t, p);
-    }
+    constexpr int NP = BP::kParts;
     kbh_u32x4 a0[RB], a1[RB];  // A fragments of step 0 (of the slab after next's barrier) / 1
     if constexpr (XS) stage_a(A[0], 0);
     __syncthreads();
@@ -357,47 +387,6 @@ tiled_wide_gemm(
     for (int kt = 0; kt < KT; kt += U) {
 #pragma unroll
       for (int u = 0; u < U; ++u) {
-        if constexpr (SP) {
-          // Slab s: step 0 beside the second half of slab s+1 (buffer 1-cur), barrier, step 1
-          // beside the first half of slab s+2 (buffer cur, whose slab-s fragments are in
-          // registers). Group sets: slab x uses set (x / SPG) & 1 (U is a multiple of 2 SPG);
-          // when slab s+2 starts a group, its set is prepared before its first half and the
-          // other set (slab s+1's group, finished in step 0) is reloaded with the group after.
-          const int s = kt + u;
-          const int cur = u & 1;
-          const int ra = u % PD, rr = (u + 1) % PD, r2 = (u + 2) % PD;
-          const int g1 = ((u + 1) / SPG) & 1, g2 = ((u + 2) / SPG) & 1;
-          const bool new2 = (u + 2) % SPG == 0;
-          read_b(b1, cur, 1);
-          frag_a(a1, A[ra], u & 1, 1);
-          __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-          for (int p = 0; p < HP; ++p) {
-            mma_range(a0, b0, p * NMF / HP, (p + 1) * NMF / HP);
-            __builtin_amdgcn_sched_barrier(0);
-            bp.template store_part<FAST>(R[rr], G[g1], Bs[1 - cur], t, HP + p);
-            __builtin_amdgcn_sched_barrier(0);
-          }
-          __syncthreads();
-          __builtin_amdgcn_sched_barrier(0);
-          read_b(b0, 1 - cur, 0);  // step 0 of slab s+1
-          if constexpr (XS) stage_a(A[(u + 1) % PD], (u + 1) & 1);
-          frag_a(a0, A[(u + 1) % PD], (u + 1) & 1, 0);
-          if (new2) bp.template prepare_group<FAST>(G[g2]);
-          load_a_step(A[ra], min(s + PD, last), 0);
-          load_b(R[rr], min(s + 1 + PD, last));  // slab s+1 is fully produced
-          if (new2) load_g(G[g2 ^ 1], min(s + 2 + SPG, last));
-          load_a_step(A[ra], min(s + PD, last), 1);
-          __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-          for (int p = 0; p < HP; ++p) {
-            mma_range(a1, b1, p * NMF / HP, (p + 1) * NMF / HP);
-            __builtin_amdgcn_sched_barrier(0);
-            bp.template store_part<FAST>(R[r2], G[g2], Bs[cur], t, p);  // slab s+2
-            __builtin_amdgcn_sched_barrier(0);
-          }
-          continue;
-        }
         const int s = kt + u;  // slab in registers / LDS buffer u&1
         const int cur = u & 1;
         const int ra = u % PD, rr = (u + 1) % PD;  // ring slots of slab s (A) and s+1 (raw)
@@ -443,53 +432,7 @@ tiled_wide_gemm(
     run(WideFlag<false>{});
   }
 
-  // Accumulator element e of tile (i, j): row 8(e/4) + 4(lane/32) + e%4, column lane%32.
-  const int rbase = wm * (TM / WM) + 4 * fg;
-  const int cbase = n0 + wn * 32 * CB + fr;
-  if constexpr (EP::kPaired) {
-    static_assert(WN == 1 && CB % 4 == 0, "paired output needs whole 128-column chunks per wave");
-#pragma unroll
-    for (int i = 0; i < RB; ++i)
-#pragma unroll
-      for (int j = 0; j < CB; ++j) {
-        if ((j & 3) >= 2) continue;  // second-matrix blocks pair with block j - 2
-#pragma unroll
-        for (int e = 0; e < 16; ++e) {
-          const int r = rbase + 32 * i + 8 * (e >> 2) + (e & 3);
-          if (r < ti.rows)
-            ep.emit_pair(rm.out_row(ti, r), n0 / 2 + 64 * (j >> 2) + 32 * (j & 1) + fr,
-                         acc[i][j][e], acc[i][j + 2][e]);
-        }
-      }
-    return;
-  } else {
-  if (splits == 1) {
-#pragma unroll
-    for (int i = 0; i < RB; ++i)
-#pragma unroll
-      for (int j = 0; j < CB; ++j)
-#pragma unroll
-        for (int e = 0; e < 16; ++e) {
-          const int r = rbase + 32 * i + 8 * (e >> 2) + (e & 3);
-          if (r < ti.rows) ep.emit(rm.out_row(ti, r), cbase + 32 * j, acc[i][j][e]);
-        }
-    return;
-  }
-  // Split-K: the fp32 partial tile goes to this split's slice of the workspace (plain stores);
-  // wide_reduce_kernel sums the slices afterwards. The launch boundary orders the two, so no
-  // device-scope fences or atomics are needed (both cost far more here than a second small
-  // launch), and the sum order is fixed.
-  typename E::Part* part = ws + (size_t)split * M * N;
-#pragma unroll
-  for (int i = 0; i < RB; ++i)
-#pragma unroll
-    for (int j = 0; j < CB; ++j)
-#pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        const int r = rbase + 32 * i + 8 * (e >> 2) + (e & 3);
-        if (r < ti.rows) part[(size_t)rm.out_row(ti, r) * N + cbase + 32 * j] = acc[i][j][e];
-      }
-  }
+  wide_store_tile<E, TM, WM, TN>(acc, ep, rm, ti, ws, split, splits, M, N, n0, wm, wn, lane);
 }
 
 // Output = sum over splits of ws[split] (in split order), through the output policy. One thread

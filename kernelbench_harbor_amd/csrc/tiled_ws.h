@@ -1,0 +1,248 @@
+// Warp-specialised wide-tile GEMM for 64- and 128-row tiles (tiled_ws_gemm).
+//
+// The same computation, policies (weight producer BP, output EP, row map RM) and launch geometry
+// as tiled_wide_gemm with fp16/bf16 operands, but a workgroup of 8 waves in two roles:
+//  * waves 4..7 (256 threads, the policy's thread ids t = 0..255) only produce: they load the
+//    packed weights PD slabs ahead, dequantize slab s + 2 into LDS buffer (s + 2) % 4 and load
+//    the quantization groups' constants;
+//  * waves 0..3 only consume: x fragments straight from global memory (PD slabs ahead), the B
+//    fragments of slab s from LDS buffer s % 4 (and, before the slab's barrier, the step-0
+//    fragments of slab s + 1, which was completed one barrier earlier), and the MFMAs.
+// One barrier per slab. Buffer (s + 3) % 4 is idle during slab s, so a producer write never
+// meets a consumer read: in slab s the consumers read buffers s % 4 and (s + 1) % 4 and the
+// producers write (s + 2) % 4. Each SIMD holds one wave of each role, so the dequantizing VALU
+// work of one runs beside the MFMAs of the other, where the 4-wave kernel issued both from the
+// same wave in turn. Both roles run their own loop of exactly KT barriers (plus the two of the
+// set-up), so the barrier counts match by construction, and then meet again for the epilogue:
+// split-K partial tiles go through the LDS ring, so that all 8 waves store whole rows.
+// Measured against tiled_wide_gemm (same shapes, graph-replayed, bit-identical outputs): W4A16
+// K=14336 N=4096 M=64 29.1 -> 27.3 us, M=128 38.0 -> 35.3, M=256 55.3 -> 50.4, M=384 84.8 ->
+// 75.5, the Mixtral MoE SiLU FFN T=512 978 -> 864 us. Per-slab timestamps at M=256: the
+// producers take ~1000-1200 cycles per slab against ~780 for the consumers' 16 MFMAs and reads
+// (a dependent VALU instruction issues ~9.5 cycles after the one it waits for; see store_all).
+#pragma once
+
+#include "tiled_wide.h"
+
+namespace kbh {
+
+template <class E, int TM, int WM, int SPG, class BP, class EP, class RM = DenseRows, int PD = 4>
+__global__ __launch_bounds__(512, 1) void tiled_ws_gemm(
+    const void* __restrict__ x, BP bp, EP ep, typename E::Part* __restrict__ ws, int M, int N,
+    int K, int splits, int slabs_per_split, RM rm) {
+  constexpr int TN = BP::kTN;
+  constexpr int SK = E::kSlabK;
+  static_assert(!E::kStageX, "fp16/bf16 operands: x fragments straight from global memory");
+  using Shape = WideShape<TM, TN, WM>;
+  constexpr int RB = Shape::RB, CB = Shape::CB, WN = Shape::WN;
+  constexpr int SLAB = TN * 64;  // LDS bytes per slab buffer
+  constexpr int NBUF = 4;
+  constexpr int U = 2 * SPG > PD ? 2 * SPG : PD;  // slabs per loop iteration
+  static_assert(PD >= 2 && U % PD == 0 && U % (2 * SPG) == 0 && U % NBUF == 0, "unroll");
+  __shared__ __attribute__((aligned(16))) uint8_t Bs[NBUF][SLAB];
+
+  const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+  const int lane = threadIdx.x & 63;
+  const int NB = N / TN;
+  const int id = xcd_remap(blockIdx.x, gridDim.x);
+  const int nb = id % NB;
+  const int rest = id / NB;
+  const int MB = gridDim.x / (NB * splits);  // row blocks (tile-table entries)
+  const int mb = rest % MB;
+  const int split = rest / MB;
+  const int n0 = nb * TN;
+  const int kt0 = split * slabs_per_split;
+  const int KT = slabs_per_split;
+  const int last = KT - 1;
+  const typename RM::Tile ti = rm.tile(mb, TM);
+  if (ti.rows <= 0) return;  // unused tile-table entry (uniform across the workgroup)
+  bp = bp.at_expert(ti.expert);
+
+  // FAST: the policy's faster producer path when every weight constant of this workgroup's K
+  // range and columns allows it (the producers scan, every wave takes part in the barrier).
+  constexpr bool kFast = BP::kHasFast;
+  bool fast = false;
+  if constexpr (kFast)
+    fast = __syncthreads_and(wave >= 4 ? (int)bp.scan_fast(kt0 * SK, (kt0 + KT) * SK, n0,
+                                                           (int)threadIdx.x - 256)
+                                       : 1) != 0;
+
+  typename E::Acc acc[RB][CB];  // the consumers' accumulators
+  if (wave >= 4) {
+    // ---- producers ----
+    const int t = (int)threadIdx.x - 256;
+    auto produce = [&](auto fast_tag) {
+      constexpr bool FAST = decltype(fast_tag)::value;
+      // Ring slot s % PD holds the raw weights of slab s; constants of even / odd groups (index
+      // within the K range) in G[0] / G[1], the next group's loaded one group ahead.
+      typename BP::Raw R[PD];
+      typename BP::Grp G[2];
+      auto load_b = [&](typename BP::Raw& r, int s) { bp.load(r, (kt0 + min(s, last)) * SK, n0, t); };
+      auto load_g = [&](typename BP::Grp& g, int s) {
+        bp.load_group(g, (kt0 + min(s, last)) * SK, n0, t);
+      };
+      auto put = [&](const typename BP::Raw& r, const typename BP::Grp& g, uint8_t* b) {
+        bp.template store_all<FAST>(r, g, b, t);
+      };
+#pragma unroll
+      for (int i = 0; i < PD; ++i) load_b(R[i], i);
+      load_g(G[0], 0);
+      load_g(G[1], SPG);
+      bp.template prepare_group<FAST>(G[0]);
+      put(R[0], G[0], Bs[0]);  // slab 0
+      load_b(R[0], PD);
+      if constexpr (SPG == 1) {  // slab 1 starts group 1; set 0 is reloaded with group 2
+        bp.template prepare_group<FAST>(G[1]);
+        load_g(G[0], 2);
+        put(R[1], G[1], Bs[1]);
+      } else {
+        put(R[1], G[0], Bs[1]);
+      }
+      load_b(R[1 % PD], PD + 1);
+      __syncthreads();  // slabs 0 and 1 are in LDS
+      // Slab kt + u + 2 during consumer slab kt + u. Slabs past the end re-produce the last one
+      // into a buffer nobody reads, so the loop has no branch.
+      for (int kt = 0; kt < KT; kt += U) {
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+          const int pu = u + 2;
+          const int set = (pu / SPG) & 1;
+          if (pu % SPG == 0) {  // slab kt + pu starts a group: its set is ready, reload the other
+            bp.template prepare_group<FAST>(G[set]);
+            load_g(G[set ^ 1], kt + pu + SPG);
+          }
+          put(R[pu % PD], G[set], Bs[pu % NBUF]);
+          load_b(R[pu % PD], kt + pu + PD);
+          __syncthreads();
+        }
+      }
+    };
+    if constexpr (kFast) {
+      if (fast) produce(WideFlag<true>{});
+      else produce(WideFlag<false>{});
+    } else {
+      produce(WideFlag<false>{});
+    }
+  } else {
+    // ---- consumers ----
+    const int wm = wave / WN, wn = wave % WN;
+    const int fr = lane & 31, fg = lane >> 5;
+    // A fragments: lane (r = lane%32, g = lane/32) of row block rb holds tile row
+    // wm*TM/WM + 32rb + r, bytes 32*step + 16g .. +16 of the slab's 64-byte K run.
+    const uint8_t* xrow[RB];
+#pragma unroll
+    for (int q = 0; q < RB; ++q) {
+      const int r = wm * (TM / WM) + q * 32 + fr;
+      xrow[q] = (const uint8_t*)x + (size_t)rm.a_row(ti, r) * K * 2 + fg * 16;
+    }
+    struct AStage {
+      kbh_u32x4 a[RB][2];
+    };
+    auto load_a = [&](AStage& st, int s) {
+      const size_t b0 = (size_t)(kt0 + min(s, last)) * WSLAB_BYTES;
+#pragma unroll
+      for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+          st.a[rb][h] = *reinterpret_cast<const kbh_u32x4*>(xrow[rb] + b0 + 32 * h);
+    };
+    int boff[CB];
+#pragma unroll
+    for (int j = 0; j < CB; ++j) boff[j] = wide_b_offset<TN>(16 * fg, wn * 32 * CB + 32 * j + fr);
+    auto read_b = [&](kbh_u32x4 (&bf)[CB], int buf, int s) {
+#pragma unroll
+      for (int j = 0; j < CB; ++j)
+        bf[j] = *reinterpret_cast<const kbh_u32x4*>(&Bs[buf][boff[j] + s * (TN * 32)]);
+    };
+
+#pragma unroll
+    for (int i = 0; i < RB; ++i)
+#pragma unroll
+      for (int j = 0; j < CB; ++j)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) acc[i][j][e] = 0;
+
+    AStage A[PD];  // slot s % PD: the x fragments of slab s
+#pragma unroll
+    for (int i = 0; i < PD; ++i) load_a(A[i], i);
+    __syncthreads();  // slabs 0 and 1 are in LDS
+    kbh_u32x4 b0[CB], b1[CB];
+    read_b(b0, 0, 0);
+    constexpr int NMF = RB * CB;  // MFMAs per k16 step
+    for (int kt = 0; kt < KT; kt += U) {
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int cur = u % NBUF, nxt = (u + 1) % NBUF, ra = u % PD;
+        read_b(b1, cur, 1);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int i = 0; i < RB; ++i)
+#pragma unroll
+          for (int j = 0; j < CB; ++j) acc[i][j] = E::mma(A[ra].a[i][0], b0[j], acc[i][j]);
+        __builtin_amdgcn_sched_barrier(0);
+        read_b(b0, nxt, 0);  // step 0 of slab kt + u + 1
+#pragma unroll
+        for (int i = 0; i < RB; ++i)
+#pragma unroll
+          for (int j = 0; j < CB; ++j) acc[i][j] = E::mma(A[ra].a[i][1], b1[j], acc[i][j]);
+        load_a(A[ra], kt + u + PD);
+        // Step-1 MFMAs interleaved with the next slab's B reads and this slot's x loads.
+#pragma unroll
+        for (int i = 0; i < NMF; ++i) {
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+          if (i < CB) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+          if (i < 2 * RB) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        __syncthreads();
+      }
+    }
+  }
+
+  if constexpr (!EP::kPaired) {
+    if (splits > 1) {
+      // Split-K partial tile through the LDS ring (free after the loops' last barrier): RP rows
+      // at a time, the consumers write their accumulators, then all 8 waves store 16-byte
+      // chunks of whole rows (row-major, coalesced). The consumers' own 4-byte stores of one
+      // accumulator element at a time (wide_store_tile) took 13.7 us of a 44 us M=128 call.
+      constexpr int RP = NBUF * SLAB / (TN * 4);  // rows per pass
+      constexpr int RW = TM / WM;                 // rows of one consumer wave
+      static_assert(RP % RW == 0, "whole wave stripes per pass");
+      float* Ls = reinterpret_cast<float*>(&Bs[0][0]);
+      typename E::Part* part = ws + (size_t)split * M * N;
+      const int fr = lane & 31, fg = lane >> 5;
+#pragma unroll
+      for (int p = 0; p < (TM + RP - 1) / RP; ++p) {
+        __syncthreads();  // the ring (first pass) or the previous pass's rows have been read
+        if (wave < 4) {
+          const int wm = wave / WN, wn = wave % WN;
+          const int r0 = wm * RW - p * RP;  // this wave's first row within the pass
+          if (r0 >= 0 && r0 < RP) {
+#pragma unroll
+            for (int i = 0; i < RB; ++i)
+#pragma unroll
+              for (int j = 0; j < CB; ++j)
+#pragma unroll
+                for (int e = 0; e < 16; ++e)
+                  Ls[(r0 + 32 * i + 8 * (e >> 2) + 4 * fg + (e & 3)) * TN + wn * 32 * CB + 32 * j +
+                     fr] = acc[i][j][e];
+          }
+        }
+        __syncthreads();
+        for (int q = (int)threadIdx.x; q < RP * TN / 4; q += 512) {
+          const int rl = q / (TN / 4), c = 4 * (q % (TN / 4));
+          const int r = p * RP + rl;
+          if (r < ti.rows)
+            *reinterpret_cast<kbh_f32x4*>(part + (size_t)rm.out_row(ti, r) * N + n0 + c) =
+                *reinterpret_cast<const kbh_f32x4*>(&Ls[rl * TN + c]);
+        }
+      }
+      return;
+    }
+  }
+  if (wave < 4)
+    wide_store_tile<E, TM, WM, TN>(acc, ep, rm, ti, ws, split, splits, M, N, n0, wave / WN,
+                                   wave % WN, lane);
+}
+
+}  // namespace kbh

@@ -211,10 +211,10 @@ struct W4WidePolicy {
     }
   }
 
-  // Rows (2i, 2i+1) of column c of the thread's word, dequantized: one dword (two values).
+  // Rows (2i, 2i+1) of column C of the thread's word, dequantized: one dword (two values), from
+  // P = pair_bytes<C / 2> of the two raw rows.
   template <int C>
-  __device__ uint32_t pair(const Raw& r, const Grp& g, int i) const {
-    const uint32_t P = pair_bytes<(C >> 1)>(r.w[2 * i], r.w[2 * i + 1]);
+  __device__ uint32_t value(uint32_t P, const Grp& g) const {
     const uint32_t m = (C & 1) ? ((P >> 4) & mask) : (P & mask);
     const uint32_t zw = g.z[C >> 1], sw = g.s[C >> 1];
     const uint16_t zb = (uint16_t)((C & 1) ? (zw >> 16) : (zw & 0xffffu));
@@ -233,11 +233,10 @@ struct W4WidePolicy {
       return __builtin_bit_cast(uint32_t, (q - h2{z, z}) * h2{sc, sc});
     }
   }
-  // The same value as pair<C> under FAST (fp16): (q - z) exactly in one step, then * s.
+  // The same value as value<C> under FAST (fp16): (q - z) exactly in one step, then * s.
   template <int C>
-  __device__ uint32_t pair_fast(const Raw& r, const Grp& g, int i) const {
+  __device__ uint32_t value_fast(uint32_t P, const Grp& g) const {
     typedef _Float16 h2 __attribute__((ext_vector_type(2)));
-    const uint32_t P = pair_bytes<(C >> 1)>(r.w[2 * i], r.w[2 * i + 1]);
     const uint32_t sw = g.s[C >> 1];
     const _Float16 sc = __builtin_bit_cast(_Float16, (uint16_t)((C & 1) ? (sw >> 16) : (sw & 0xffffu)));
     const uint32_t zw = g.z[C >> 1];  // 1024 + z (prepare_group<true>)
@@ -256,6 +255,14 @@ struct W4WidePolicy {
                                     __builtin_bit_cast(h2, sixteenth), -h2{zm, zm}) + k960;
     }
     return __builtin_bit_cast(uint32_t, d * h2{sc, sc});
+  }
+  template <int C>
+  __device__ uint32_t pair(const Raw& r, const Grp& g, int i) const {
+    return value<C>(pair_bytes<(C >> 1)>(r.w[2 * i], r.w[2 * i + 1]), g);
+  }
+  template <int C>
+  __device__ uint32_t pair_fast(const Raw& r, const Grp& g, int i) const {
+    return value_fast<C>(pair_bytes<(C >> 1)>(r.w[2 * i], r.w[2 * i + 1]), g);
   }
   template <bool FAST, int C>
   __device__ void put(const Raw& r, const Grp& g, uint8_t* base, int fw) const {
@@ -286,6 +293,87 @@ struct W4WidePolicy {
       case 5: put<FAST, 5>(r, g, base, fw); break;
       case 6: put<FAST, 6>(r, g, base, fw); break;
       default: put<FAST, 7>(r, g, base, fw); break;
+    }
+  }
+  // Every part of the thread's slab share at once, the same LDS bytes as store_part(p) for
+  // p < kParts, computed stage by stage across all columns and row pairs (8 perms, then 16
+  // independent chains side by side) instead of one column's dependent chain after another, whose
+  // latency (~9.5 cycles per dependent VALU instruction against ~5 with 4-8 chains in flight)
+  // bounds a wave that only dequantizes.
+  template <bool FAST>
+  __device__ void store_all(const Raw& r, const Grp& g, uint8_t* Bs, int t) const {
+    constexpr int NI = kRows / 2;  // row pairs
+    const int w = word_of(t), h = rows_of(t);
+    uint8_t* base = Bs + wide_b_offset<TN>(2 * kRows * h, 8 * w) - wide_slot(8 * w) * 16 + w * 128;
+    const int fw = (w ^ (w >> 3)) & 7;
+    uint32_t P[4][NI];
+#pragma unroll
+    for (int i = 0; i < NI; ++i) {
+      P[0][i] = pair_bytes<0>(r.w[2 * i], r.w[2 * i + 1]);
+      P[1][i] = pair_bytes<1>(r.w[2 * i], r.w[2 * i + 1]);
+      P[2][i] = pair_bytes<2>(r.w[2 * i], r.w[2 * i + 1]);
+      P[3][i] = pair_bytes<3>(r.w[2 * i], r.w[2 * i + 1]);
+    }
+    uint32_t v[8][NI];
+    if constexpr (FAST && !BF16) {
+      // The steps of value_fast, one stage at a time over all 8 x NI values (scheduling barriers
+      // keep the stages apart: left alone, the scheduler reuses one temporary register per
+      // value and the chains run back to back).
+      typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+      uint32_t magic = kMagicF16, mask_hi = 0x00F000F0u, sixteenth = 0x2C002C00u;
+      asm("" : "+v"(magic));
+      asm("" : "+s"(mask_hi), "+s"(sixteenth));
+      const h2 k960 = {(_Float16)960.0f, (_Float16)960.0f};
+      h2 zm[8], sc[8];
+#pragma unroll
+      for (int c = 0; c < 8; ++c) {
+        const uint32_t zw = g.z[c >> 1], sw = g.s[c >> 1];
+        const _Float16 z1 = __builtin_bit_cast(_Float16, (uint16_t)((c & 1) ? (zw >> 16) : (zw & 0xffffu)));
+        const _Float16 s1 = __builtin_bit_cast(_Float16, (uint16_t)((c & 1) ? (sw >> 16) : (sw & 0xffffu)));
+        zm[c] = h2{z1, z1};
+        sc[c] = h2{s1, s1};
+      }
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int i = 0; i < NI; ++i)
+#pragma unroll
+        for (int c = 0; c < 8; ++c)
+          v[c][i] = (c & 1) ? ((P[c >> 1][i] & mask_hi) | magic) : ((P[c >> 1][i] & mask) | magic);
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int i = 0; i < NI; ++i)
+#pragma unroll
+        for (int c = 0; c < 8; ++c) {
+          const h2 m = __builtin_bit_cast(h2, v[c][i]);
+          v[c][i] = __builtin_bit_cast(
+              uint32_t, (c & 1) ? __builtin_elementwise_fma(m, __builtin_bit_cast(h2, sixteenth), -zm[c])
+                                : m - zm[c]);
+        }
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int i = 0; i < NI; ++i)
+#pragma unroll
+        for (int c = 1; c < 8; c += 2) v[c][i] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2, v[c][i]) + k960);
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int i = 0; i < NI; ++i)
+#pragma unroll
+        for (int c = 0; c < 8; ++c) v[c][i] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2, v[c][i]) * sc[c]);
+      __builtin_amdgcn_sched_barrier(0);
+    } else {
+#pragma unroll
+      for (int i = 0; i < NI; ++i) {
+        v[0][i] = value<0>(P[0][i], g); v[1][i] = value<1>(P[0][i], g);
+        v[2][i] = value<2>(P[1][i], g); v[3][i] = value<3>(P[1][i], g);
+        v[4][i] = value<4>(P[2][i], g); v[5][i] = value<5>(P[2][i], g);
+        v[6][i] = value<6>(P[3][i], g); v[7][i] = value<7>(P[3][i], g);
+      }
+    }
+#pragma unroll
+    for (int c = 0; c < 8; ++c) {
+      uint8_t* p = base + ((c ^ fw) << 4);
+      if constexpr (NI == 2) *reinterpret_cast<kbh_u32x2*>(p) = kbh_u32x2{v[c][0], v[c][1]};
+      else *reinterpret_cast<uint32_t*>(p) = v[c][0];
     }
   }
 };

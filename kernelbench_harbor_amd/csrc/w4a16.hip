@@ -35,6 +35,7 @@
 #include "splitk.h"
 #include "tiled_f16.h"
 #include "tiled_wide.h"
+#include "tiled_ws.h"
 #include "w4_dequant.h"
 
 namespace kbh {
@@ -290,8 +291,9 @@ void dispatch_decode(const DecodePlan& p, const void* x, const int32_t* qw, cons
 // kernel: up to 64 rows, 64 x 256 tiles; up to 384 rows, 128 x 256 tiles with one workgroup per
 // CU (128 x 128 tiles, two per CU, up to 128 rows when N is not a multiple of 256); 256 x 256
 // tiles above unless the planner's estimate prefers 128-row tiles. The 256-column tiles run
-// with a 4-slab prefetch ring. The older 256 x 128 LDS-staged kernel remains for shapes the wide kernel
-// does not cover.
+// with a 4-slab prefetch ring; those of 64 and 128 rows on the warp-specialised kernel
+// (tiled_ws.h: 4 dequantizing and 4 MFMA waves per workgroup). The older 256 x 128 LDS-staged
+// kernel remains for shapes the wide kernel does not cover.
 constexpr int kWideMinM = 33;
 constexpr int kTiledMinM = 128;
 
@@ -330,15 +332,20 @@ void launch_w4_wide(const W4Wide& w, const void* x, const int32_t* qw, const voi
   using E = WideHalf<BF16>;
   using BP = W4WidePolicy<BF16, TN>;
   using EP = HalfOut<BF16>;
-  constexpr int MINB = (TM == 128 && TN == 256) ? 1 : 0;
   constexpr int WM = TM == 64 ? 2 : 4;  // waves along M
   const BP bp{(const uint32_t*)qw, (const uint16_t*)s, (const uint16_t*)z, N, group, 0, 0,
               0x000F000Fu};
   const EP ep{(uint16_t*)y, N};
-  hipLaunchKernelGGL((tiled_wide_gemm<E, TM, WM, SPG, BP, EP, DenseRows, MINB, w4_wide_pd(TN)>),
-                     dim3(w.plan.grid), dim3(256), 0, st,
-                     x, bp, ep, scratch, M, N, K, w.plan.splits, w.plan.slabs_per_split,
-                     DenseRows{M});
+  if constexpr (TM <= 128 && TN == 256)
+    hipLaunchKernelGGL((tiled_ws_gemm<E, TM, WM, SPG, BP, EP, DenseRows, w4_wide_pd(TN)>),
+                       dim3(w.plan.grid), dim3(512), 0, st,
+                       x, bp, ep, scratch, M, N, K, w.plan.splits, w.plan.slabs_per_split,
+                       DenseRows{M});
+  else
+    hipLaunchKernelGGL((tiled_wide_gemm<E, TM, WM, SPG, BP, EP, DenseRows, 0, w4_wide_pd(TN)>),
+                       dim3(w.plan.grid), dim3(256), 0, st,
+                       x, bp, ep, scratch, M, N, K, w.plan.splits, w.plan.slabs_per_split,
+                       DenseRows{M});
   if (w.plan.splits > 1) {
     const size_t n4 = (size_t)M * N / 4;
     hipLaunchKernelGGL((wide_reduce_kernel<E, EP>), dim3((unsigned)((n4 + 255) / 256)), dim3(256),
