@@ -58,36 +58,36 @@ __global__ __launch_bounds__(512, 1) void tiled_ws_gemm(
   if (ti.rows <= 0) return;  // unused tile-table entry (uniform across the workgroup)
   bp = bp.at_expert(ti.expert);
 
-  // FAST: the policy's faster producer path when every weight constant of this workgroup's K
-  // range and columns allows it (the producers scan, every wave takes part in the barrier).
-  constexpr bool kFast = BP::kHasFast;
-  bool fast = false;
-  if constexpr (kFast)
-    fast = __syncthreads_and(wave >= 4 ? (int)bp.scan_fast(kt0 * SK, (kt0 + KT) * SK, n0,
-                                                           (int)threadIdx.x - 256)
-                                       : 1) != 0;
-
   typename E::Acc acc[RB][CB];  // the consumers' accumulators
-  if (wave >= 4) {
+  const bool producer = wave >= 4;
+  // FAST: the policy's faster producer path when every weight constant of this workgroup's K
+  // range and columns allows it. The producers scan and every wave takes part in the barrier
+  // (one __syncthreads_and in each role's branch); both roles issue their set-up loads before
+  // it, so that the scan's latency and theirs overlap.
+  constexpr bool kFast = BP::kHasFast;
+  const int fr = lane & 31, fg = lane >> 5;
+  if (producer) {
     // ---- producers ----
-    const int t = (int)threadIdx.x - 256;
+    const int t = (int)threadIdx.x - 256;  // the policy's thread id
+    auto load_b = [&](typename BP::Raw& r, int s) { bp.load(r, (kt0 + min(s, last)) * SK, n0, t); };
+    auto load_g = [&](typename BP::Grp& g, int s) {
+      bp.load_group(g, (kt0 + min(s, last)) * SK, n0, t);
+    };
+    // Ring slot s % PD holds the raw weights of slab s; constants of even / odd groups (index
+    // within the K range) in G[0] / G[1], the next group's loaded one group ahead.
+    typename BP::Raw R[PD];
+    typename BP::Grp G[2];
+#pragma unroll
+    for (int i = 0; i < PD; ++i) load_b(R[i], i);
+    load_g(G[0], 0);
+    load_g(G[1], SPG);
+    bool fast = false;
+    if constexpr (kFast) fast = __syncthreads_and((int)bp.scan_fast(kt0 * SK, (kt0 + KT) * SK, n0, t)) != 0;
     auto produce = [&](auto fast_tag) {
       constexpr bool FAST = decltype(fast_tag)::value;
-      // Ring slot s % PD holds the raw weights of slab s; constants of even / odd groups (index
-      // within the K range) in G[0] / G[1], the next group's loaded one group ahead.
-      typename BP::Raw R[PD];
-      typename BP::Grp G[2];
-      auto load_b = [&](typename BP::Raw& r, int s) { bp.load(r, (kt0 + min(s, last)) * SK, n0, t); };
-      auto load_g = [&](typename BP::Grp& g, int s) {
-        bp.load_group(g, (kt0 + min(s, last)) * SK, n0, t);
-      };
       auto put = [&](const typename BP::Raw& r, const typename BP::Grp& g, uint8_t* b) {
         bp.template store_all<FAST>(r, g, b, t);
       };
-#pragma unroll
-      for (int i = 0; i < PD; ++i) load_b(R[i], i);
-      load_g(G[0], 0);
-      load_g(G[1], SPG);
       bp.template prepare_group<FAST>(G[0]);
       put(R[0], G[0], Bs[0]);  // slab 0
       load_b(R[0], PD);
@@ -126,7 +126,6 @@ __global__ __launch_bounds__(512, 1) void tiled_ws_gemm(
   } else {
     // ---- consumers ----
     const int wm = wave / WN, wn = wave % WN;
-    const int fr = lane & 31, fg = lane >> 5;
     // A fragments: lane (r = lane%32, g = lane/32) of row block rb holds tile row
     // wm*TM/WM + 32rb + r, bytes 32*step + 16g .. +16 of the slab's 64-byte K run.
     const uint8_t* xrow[RB];
@@ -146,6 +145,10 @@ __global__ __launch_bounds__(512, 1) void tiled_ws_gemm(
         for (int h = 0; h < 2; ++h)
           st.a[rb][h] = *reinterpret_cast<const kbh_u32x4*>(xrow[rb] + b0 + 32 * h);
     };
+    AStage A[PD];  // slot s % PD holds the x fragments of slab s
+#pragma unroll
+    for (int i = 0; i < PD; ++i) load_a(A[i], i);
+    if constexpr (kFast) (void)__syncthreads_and(1);  // the producers' FAST barrier
     int boff[CB];
 #pragma unroll
     for (int j = 0; j < CB; ++j) boff[j] = wide_b_offset<TN>(16 * fg, wn * 32 * CB + 32 * j + fr);
@@ -162,9 +165,6 @@ __global__ __launch_bounds__(512, 1) void tiled_ws_gemm(
 #pragma unroll
         for (int e = 0; e < 16; ++e) acc[i][j][e] = 0;
 
-    AStage A[PD];  // slot s % PD: the x fragments of slab s
-#pragma unroll
-    for (int i = 0; i < PD; ++i) load_a(A[i], i);
     __syncthreads();  // slabs 0 and 1 are in LDS
     kbh_u32x4 b0[CB], b1[CB];
     read_b(b0, 0, 0);
@@ -200,45 +200,47 @@ __global__ __launch_bounds__(512, 1) void tiled_ws_gemm(
   }
 
   if constexpr (!EP::kPaired) {
-    if (splits > 1) {
-      // Split-K partial tile through the LDS ring (free after the loops' last barrier): RP rows
-      // at a time, the consumers write their accumulators, then all 8 waves store 16-byte
-      // chunks of whole rows (row-major, coalesced). The consumers' own 4-byte stores of one
-      // accumulator element at a time (wide_store_tile) took 13.7 us of a 44 us M=128 call.
-      constexpr int RP = NBUF * SLAB / (TN * 4);  // rows per pass
-      constexpr int RW = TM / WM;                 // rows of one consumer wave
-      static_assert(RP % RW == 0, "whole wave stripes per pass");
-      float* Ls = reinterpret_cast<float*>(&Bs[0][0]);
-      typename E::Part* part = ws + (size_t)split * M * N;
-      const int fr = lane & 31, fg = lane >> 5;
+    // The tile leaves through the LDS ring (free after the loops' last barrier), RP rows at a
+    // time: the consumers write their accumulators, then all 8 waves store 16-byte chunks of
+    // whole rows (row-major, coalesced): fp32 partial sums into this split's slice of the
+    // workspace (split-K) or four outputs at a time through the output policy. The consumers'
+    // own stores of one accumulator element at a time (wide_store_tile) took 13.7 us of a
+    // 44 us W4A16 M=128 call.
+    constexpr int RP = NBUF * SLAB / (TN * 4);  // rows per pass
+    constexpr int RW = TM / WM;                 // rows of one consumer wave
+    static_assert(RP % RW == 0 || RW % RP == 0, "whole wave stripes or row blocks per pass");
+    float* Ls = reinterpret_cast<float*>(&Bs[0][0]);
+    typename E::Part* part = ws + (size_t)split * M * N;
 #pragma unroll
-      for (int p = 0; p < (TM + RP - 1) / RP; ++p) {
-        __syncthreads();  // the ring (first pass) or the previous pass's rows have been read
-        if (wave < 4) {
-          const int wm = wave / WN, wn = wave % WN;
-          const int r0 = wm * RW - p * RP;  // this wave's first row within the pass
-          if (r0 >= 0 && r0 < RP) {
+    for (int p = 0; p < (TM + RP - 1) / RP; ++p) {
+      __syncthreads();  // the ring (first pass) or the previous pass's rows have been read
+      if (wave < 4) {
+        const int wm = wave / WN, wn = wave % WN;
 #pragma unroll
-            for (int i = 0; i < RB; ++i)
+        for (int i = 0; i < RB; ++i) {
+          const int r0 = wm * RW + 32 * i - p * RP;  // row block i's first row within the pass
+          if (r0 < 0 || r0 >= RP) continue;
 #pragma unroll
-              for (int j = 0; j < CB; ++j)
+          for (int j = 0; j < CB; ++j)
 #pragma unroll
-                for (int e = 0; e < 16; ++e)
-                  Ls[(r0 + 32 * i + 8 * (e >> 2) + 4 * fg + (e & 3)) * TN + wn * 32 * CB + 32 * j +
-                     fr] = acc[i][j][e];
-          }
-        }
-        __syncthreads();
-        for (int q = (int)threadIdx.x; q < RP * TN / 4; q += 512) {
-          const int rl = q / (TN / 4), c = 4 * (q % (TN / 4));
-          const int r = p * RP + rl;
-          if (r < ti.rows)
-            *reinterpret_cast<kbh_f32x4*>(part + (size_t)rm.out_row(ti, r) * N + n0 + c) =
-                *reinterpret_cast<const kbh_f32x4*>(&Ls[rl * TN + c]);
+            for (int e = 0; e < 16; ++e)
+              Ls[(r0 + 8 * (e >> 2) + 4 * fg + (e & 3)) * TN + wn * 32 * CB + 32 * j + fr] =
+                  acc[i][j][e];
         }
       }
-      return;
+      __syncthreads();
+      for (int q = (int)threadIdx.x; q < RP * TN / 4; q += 512) {
+        const int rl = q / (TN / 4), c = 4 * (q % (TN / 4));
+        const int r = p * RP + rl;
+        if (r >= ti.rows) continue;
+        const kbh_f32x4 v = *reinterpret_cast<const kbh_f32x4*>(&Ls[rl * TN + c]);
+        if (splits > 1)
+          *reinterpret_cast<kbh_f32x4*>(part + (size_t)rm.out_row(ti, r) * N + n0 + c) = v;
+        else
+          ep.emit4(rm.out_row(ti, r), n0 + c, v);
+      }
     }
+    return;
   }
   if (wave < 4)
     wide_store_tile<E, TM, WM, TN>(acc, ep, rm, ti, ws, split, splits, M, N, n0, wave / WN,

@@ -184,7 +184,10 @@ struct W4WidePolicy {
       typedef _Float16 h8 __attribute__((ext_vector_type(8)));
       const int g0 = k_begin / group, chunks = cols / 8;
       const int total = ((k_end - 1) / group - g0 + 1) * chunks;
+      // Branch-free and unrolled, so that the loads of several chunks are in flight together
+      // (with short-circuit tests each load waited for the previous chunk's verdict).
       bool ok = true;
+#pragma unroll 4
       for (int i = t; i < total; i += 256) {
         const h8 z = __builtin_bit_cast(
             h8, *reinterpret_cast<const kbh_u32x4*>(zeros + (size_t)(g0 + i / chunks) * N + n0 +
@@ -194,7 +197,7 @@ struct W4WidePolicy {
         const h8 bm = (z + (_Float16)1024.0f) - (_Float16)1024.0f;
 #pragma unroll
         for (int e = 0; e < 8; ++e)
-          ok = ok && bm[e] == z[e] && (float)z[e] < 960.0f && (float)z[e] > -960.0f;
+          ok &= (bm[e] == z[e]) & ((float)z[e] < 960.0f) & ((float)z[e] > -960.0f);
       }
       return ok;
     }
