@@ -54,11 +54,11 @@ def w4a16_bytes(M, K=K_DIM, N=N_DIM, G=GROUP):
 # every kbh:: kernel of the call. Table and commands: profiles/hbm_traffic_all_records.md.
 PMC_TRAFFIC = {
     "w4a16 M=1": 32_167_648, "w4a16 M=4": 34_454_252, "w4a16 M=16": 42_545_554,
-    "w4a16 M=64": 65_934_336, "w4a16 M=256": 108_180_696, "w4a16 M=1024": 240_722_352,
+    "w4a16 M=64": 64_027_853, "w4a16 M=256": 108_150_784, "w4a16 M=1024": 240_722_352,
     "w4a16 M=2048": 340_853_600, "w8a8 M=16": 68_182_320, "w8a8 M=512": 210_735_483,
     "mxfp8 M=128": 94_936_720, "mxfp8 M=2048": 483_042_099,
     "fp8w (reference op) M=16 b128": 70_943_466,
-    "qmoe_ffn T=512 D=4096 F=14336 E=8 top2": 1_229_346_633,
+    "qmoe_ffn T=512 D=4096 F=14336 E=8 top2": 1_224_380_211,
     "silu_fp8 (reference op) T=512 H=14336 g128": 61_112_077,
     "qmoe (reference op) T=256 D=4096 N=14336 E=8": 570_156_646,
 }
@@ -67,16 +67,16 @@ PMC_TRAFFIC = {
 # Kernel time per op call of every record from the rocprofv3 kernel trace of the default bench
 # command (`rocprofv3 --kernel-trace --stats ... -- python3 -u bench.py`): the summed average
 # durations of the call's kbh:: kernels over the run. Dispatch tracing lengthens the small
-# kernels (W4A16 M=1: 13.2 us traced against 11.9 us graph-replayed). Table and commands:
+# kernels (W4A16 M=1: 13.4 us traced against 12.1 us graph-replayed). Table and commands:
 # profiles/bench_kernel_trace.md.
 KERNEL_TRACE_US = {
-    "w4a16 M=1": 13.20, "w4a16 M=4": 13.33, "w4a16 M=16": 15.21, "w4a16 M=64": 28.88,
-    "w4a16 M=256": 53.92, "w4a16 M=1024": 148.04, "w4a16 M=2048": 272.57,
-    "w8a8 M=16": 18.74, "w8a8 M=512": 59.18, "mxfp8 M=128": 32.44, "mxfp8 M=2048": 150.34,
-    "fp8w (reference op) M=16 b128": 20.43,
-    "qmoe_ffn T=512 D=4096 F=14336 E=8 top2": 955.46,
-    "silu_fp8 (reference op) T=512 H=14336 g128": 13.34,
-    "qmoe (reference op) T=256 D=4096 N=14336 E=8": 198.49,
+    "w4a16 M=1": 13.39, "w4a16 M=4": 13.45, "w4a16 M=16": 15.15, "w4a16 M=64": 26.75,
+    "w4a16 M=256": 51.52, "w4a16 M=1024": 155.95, "w4a16 M=2048": 285.96,
+    "w8a8 M=16": 19.19, "w8a8 M=512": 59.32, "mxfp8 M=128": 32.44, "mxfp8 M=2048": 151.71,
+    "fp8w (reference op) M=16 b128": 20.74,
+    "qmoe_ffn T=512 D=4096 F=14336 E=8 top2": 860.33,
+    "silu_fp8 (reference op) T=512 H=14336 g128": 13.23,
+    "qmoe (reference op) T=256 D=4096 N=14336 E=8": 202.27,
 }
 
 def gemm_flops(M, N=N_DIM, K=K_DIM):
