@@ -128,6 +128,20 @@ def test_qmoe_ffn_parity(dev, T, D, F, E, dtype):
     assert cmp.ok, cmp
 
 
+@pytest.mark.parametrize("group", [32, 64, 256])
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_qmoe_ffn_group_sizes(dev, group, dtype):
+    """128-row expert tiles (64-191 routed rows per expert) on the warp-specialised kernel with
+    every other quantization group (32, 64 and 256 rows: 1, 2 and 8 slabs per group) for both
+    GEMMs; the down projection splits K."""
+    T, D, F, E = 192, 512, 1024, 4
+    print(f"[qmoe ffn group] g{group} {dtype}", flush=True)
+    ins = inputs.qmoe_ffn(T, D, F, E, group=group, dtype=dtype, seed=group)
+    y = ops.qmoe_ffn(*[t.to(dev) for t in ins])
+    cmp = compare(y, oq.ffn_forward(*_np(ins)))
+    assert cmp.ok, cmp
+
+
 @pytest.mark.parametrize("T,D,F,E,dtype", [(64, 256, 512, 4, torch.float16),
                                             (300, 256, 512, 4, torch.float16)])
 def test_qmoe_ffn_native_rounding(dev, T, D, F, E, dtype):

@@ -51,6 +51,11 @@ CASES = [
     (64, 1024, 768, 256, torch.bfloat16, "reference"),
     # N % 256 != 0 above 128 rows: the 256 x 128 LDS-staged kernel
     (160, 2048, 384, 128, torch.float16, "baseline"),
+    # warp-specialised 128-row tiles (64 < M <= 384, N % 256 == 0) with 256- and 32-row groups
+    # (the producers' group schedules SPG = 8 and SPG = 1), fp16 and bf16, ragged M
+    (160, 4096, 512, 256, torch.float16, "reference"),
+    (72, 2048, 512, 32, torch.bfloat16, "baseline"),
+    (350, 2048, 256, 256, torch.bfloat16, "reference"),
 ]
 
 
