@@ -15,6 +15,8 @@
 // same wave in turn. Both roles run their own loop of exactly KT barriers (plus the two of the
 // set-up), so the barrier counts match by construction, and then meet again for the epilogue:
 // split-K partial tiles go through the LDS ring, so that all 8 waves store whole rows.
+// 64-row tiles run two producer sets (waves 4..7 and 8..11, PS below), each dequantizing one
+// row pair of every thread's four rows.
 // Measured against tiled_wide_gemm (same shapes, graph-replayed, bit-identical outputs): W4A16
 // K=14336 N=4096 M=64 29.1 -> 27.3 us, M=128 38.0 -> 35.3, M=256 55.3 -> 50.4, M=384 84.8 ->
 // 75.5, the Mixtral MoE SiLU FFN T=512 978 -> 864 us. Per-slab timestamps at M=256: the
@@ -26,8 +28,24 @@
 
 namespace kbh {
 
-template <class E, int TM, int WM, int SPG, class BP, class EP, class RM = DenseRows, int PD = 4>
-__global__ __launch_bounds__(512, 1) void tiled_ws_gemm(
+// Raw weights one producer thread holds per slab: the policy's whole share (one producer set) or
+// its half (BP::RawHalf, two sets).
+template <class BP, int PS>
+struct WsRaw {
+  using type = typename BP::Raw;
+};
+template <class BP>
+struct WsRaw<BP, 2> {
+  using type = typename BP::RawHalf;
+};
+
+// PS: producer sets. 1: waves 4..7 dequantize whole slabs. 2: waves 4..7 and 8..11 run the same
+//   loop on the same thread ids and barriers, set p loading and dequantizing row pair p of each
+//   thread's rows (BP::load_half / store_half), so two producer waves share each SIMD's VALU
+//   with the MFMA wave (768 threads, at most 168 VGPRs per wave: 64-row tiles).
+template <class E, int TM, int WM, int SPG, class BP, class EP, class RM = DenseRows, int PD = 4,
+          int PS = 1>
+__global__ __launch_bounds__(256 * (1 + PS), 1) void tiled_ws_gemm(
     const void* __restrict__ x, BP bp, EP ep, typename E::Part* __restrict__ ws, int M, int N,
     int K, int splits, int slabs_per_split, RM rm) {
   constexpr int TN = BP::kTN;
@@ -39,6 +57,8 @@ __global__ __launch_bounds__(512, 1) void tiled_ws_gemm(
   constexpr int NBUF = 4;
   constexpr int U = 2 * SPG > PD ? 2 * SPG : PD;  // slabs per loop iteration
   static_assert(PD >= 2 && U % PD == 0 && U % (2 * SPG) == 0 && U % NBUF == 0, "unroll");
+  static_assert(PS == 1 || PS == 2, "one or two producer sets");
+  constexpr int NT = 256 * (1 + PS);  // threads
   __shared__ __attribute__((aligned(16))) uint8_t Bs[NBUF][SLAB];
 
   const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
@@ -68,25 +88,32 @@ __global__ __launch_bounds__(512, 1) void tiled_ws_gemm(
   const int fr = lane & 31, fg = lane >> 5;
   if (producer) {
     // ---- producers ----
-    const int t = (int)threadIdx.x - 256;  // the policy's thread id
-    auto load_b = [&](typename BP::Raw& r, int s) { bp.load(r, (kt0 + min(s, last)) * SK, n0, t); };
+    const int pset = PS == 1 ? 0 : (wave - 4) >> 2;            // producer set
+    const int t = (int)threadIdx.x - 256 - 256 * pset;  // the policy's thread id
+    using Raw = typename WsRaw<BP, PS>::type;
+    auto load_b = [&](Raw& r, int s) {
+      if constexpr (PS == 1) bp.load(r, (kt0 + min(s, last)) * SK, n0, t);
+      else bp.load_half(r, (kt0 + min(s, last)) * SK, n0, t, pset);
+    };
     auto load_g = [&](typename BP::Grp& g, int s) {
       bp.load_group(g, (kt0 + min(s, last)) * SK, n0, t);
     };
     // Ring slot s % PD holds the raw weights of slab s; constants of even / odd groups (index
     // within the K range) in G[0] / G[1], the next group's loaded one group ahead.
-    typename BP::Raw R[PD];
+    Raw R[PD];
     typename BP::Grp G[2];
 #pragma unroll
     for (int i = 0; i < PD; ++i) load_b(R[i], i);
     load_g(G[0], 0);
     load_g(G[1], SPG);
     bool fast = false;
-    if constexpr (kFast) fast = __syncthreads_and((int)bp.scan_fast(kt0 * SK, (kt0 + KT) * SK, n0, t)) != 0;
+    if constexpr (kFast)
+      fast = __syncthreads_and(pset == 0 ? (int)bp.scan_fast(kt0 * SK, (kt0 + KT) * SK, n0, t) : 1) != 0;
     auto produce = [&](auto fast_tag) {
       constexpr bool FAST = decltype(fast_tag)::value;
-      auto put = [&](const typename BP::Raw& r, const typename BP::Grp& g, uint8_t* b) {
-        bp.template store_all<FAST>(r, g, b, t);
+      auto put = [&](const Raw& r, const typename BP::Grp& g, uint8_t* b) {
+        if constexpr (PS == 1) bp.template store_all<FAST>(r, g, b, t);
+        else bp.template store_half<FAST>(r, g, b, t, pset);
       };
       bp.template prepare_group<FAST>(G[0]);
       put(R[0], G[0], Bs[0]);  // slab 0
@@ -229,7 +256,7 @@ __global__ __launch_bounds__(512, 1) void tiled_ws_gemm(
         }
       }
       __syncthreads();
-      for (int q = (int)threadIdx.x; q < RP * TN / 4; q += 512) {
+      for (int q = (int)threadIdx.x; q < RP * TN / 4; q += NT) {
         const int rl = q / (TN / 4), c = 4 * (q % (TN / 4));
         const int r = p * RP + rl;
         if (r >= ti.rows) continue;

@@ -305,23 +305,50 @@ struct W4WidePolicy {
   // bounds a wave that only dequantizes.
   template <bool FAST>
   __device__ void store_all(const Raw& r, const Grp& g, uint8_t* Bs, int t) const {
-    constexpr int NI = kRows / 2;  // row pairs
+    store_cols<FAST, 0, 8>(r, g, Bs, t);
+  }
+  // Two producer sets (TN = 256): set `half` of thread t loads and dequantizes rows
+  // 4h + 2 half, +1 of the thread's 4 (one row pair) and writes their dword of each column.
+  struct RawHalf {
+    uint32_t w[2];
+  };
+  __device__ void load_half(RawHalf& r, int k0, int n0, int t, int half) const {
+    static_assert(kRows == 4, "row pairs of 4-row threads");
+    const int w = word_of(t), h = rows_of(t);
+    const int NP = N >> 3;
+    const uint32_t* q = qw + (size_t)(k0 + kRows * h + 2 * half) * NP + (n0 >> 3) + w;
+    r.w[0] = q[0];
+    r.w[1] = q[NP];
+  }
+  template <bool FAST>
+  __device__ void store_half(const RawHalf& r, const Grp& g, uint8_t* Bs, int t, int half) const {
+    const Raw full{{r.w[0], r.w[1], 0u, 0u}};
+    store_cols<FAST, 0, 8, 1>(full, g, Bs + 4 * half, t);
+  }
+  // Columns C0..C0+NC-1 (C0, NC even) of the thread's word, as store_part(p) for those p, for
+  // the first NIP row pairs of r (a single pair is stored as one dword per column at Bs + the
+  // pair-0 offset).
+  template <bool FAST, int C0, int NC, int NIP = kRows / 2>
+  __device__ void store_cols(const Raw& r, const Grp& g, uint8_t* Bs, int t) const {
+    static_assert(C0 % 2 == 0 && NC % 2 == 0 && C0 + NC <= 8, "whole byte pairs");
+    static_assert(NIP >= 1 && NIP <= kRows / 2, "row pairs");
+    constexpr int NI = NIP;  // row pairs
     const int w = word_of(t), h = rows_of(t);
     uint8_t* base = Bs + wide_b_offset<TN>(2 * kRows * h, 8 * w) - wide_slot(8 * w) * 16 + w * 128;
     const int fw = (w ^ (w >> 3)) & 7;
     uint32_t P[4][NI];
 #pragma unroll
     for (int i = 0; i < NI; ++i) {
-      P[0][i] = pair_bytes<0>(r.w[2 * i], r.w[2 * i + 1]);
-      P[1][i] = pair_bytes<1>(r.w[2 * i], r.w[2 * i + 1]);
-      P[2][i] = pair_bytes<2>(r.w[2 * i], r.w[2 * i + 1]);
-      P[3][i] = pair_bytes<3>(r.w[2 * i], r.w[2 * i + 1]);
+      if constexpr (C0 <= 0 && 0 < C0 + NC) P[0][i] = pair_bytes<0>(r.w[2 * i], r.w[2 * i + 1]);
+      if constexpr (C0 <= 2 && 2 < C0 + NC) P[1][i] = pair_bytes<1>(r.w[2 * i], r.w[2 * i + 1]);
+      if constexpr (C0 <= 4 && 4 < C0 + NC) P[2][i] = pair_bytes<2>(r.w[2 * i], r.w[2 * i + 1]);
+      if constexpr (C0 <= 6 && 6 < C0 + NC) P[3][i] = pair_bytes<3>(r.w[2 * i], r.w[2 * i + 1]);
     }
     uint32_t v[8][NI];
     if constexpr (FAST && !BF16) {
-      // The steps of value_fast, one stage at a time over all 8 x NI values (scheduling barriers
-      // keep the stages apart: left alone, the scheduler reuses one temporary register per
-      // value and the chains run back to back).
+      // The steps of value_fast, one stage at a time over all NC x NI values (scheduling
+      // barriers keep the stages apart: left alone, the scheduler reuses one temporary register
+      // per value and the chains run back to back).
       typedef _Float16 h2 __attribute__((ext_vector_type(2)));
       uint32_t magic = kMagicF16, mask_hi = 0x00F000F0u, sixteenth = 0x2C002C00u;
       asm("" : "+v"(magic));
@@ -329,7 +356,7 @@ struct W4WidePolicy {
       const h2 k960 = {(_Float16)960.0f, (_Float16)960.0f};
       h2 zm[8], sc[8];
 #pragma unroll
-      for (int c = 0; c < 8; ++c) {
+      for (int c = C0; c < C0 + NC; ++c) {
         const uint32_t zw = g.z[c >> 1], sw = g.s[c >> 1];
         const _Float16 z1 = __builtin_bit_cast(_Float16, (uint16_t)((c & 1) ? (zw >> 16) : (zw & 0xffffu)));
         const _Float16 s1 = __builtin_bit_cast(_Float16, (uint16_t)((c & 1) ? (sw >> 16) : (sw & 0xffffu)));
@@ -340,13 +367,13 @@ struct W4WidePolicy {
 #pragma unroll
       for (int i = 0; i < NI; ++i)
 #pragma unroll
-        for (int c = 0; c < 8; ++c)
+        for (int c = C0; c < C0 + NC; ++c)
           v[c][i] = (c & 1) ? ((P[c >> 1][i] & mask_hi) | magic) : ((P[c >> 1][i] & mask) | magic);
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int i = 0; i < NI; ++i)
 #pragma unroll
-        for (int c = 0; c < 8; ++c) {
+        for (int c = C0; c < C0 + NC; ++c) {
           const h2 m = __builtin_bit_cast(h2, v[c][i]);
           v[c][i] = __builtin_bit_cast(
               uint32_t, (c & 1) ? __builtin_elementwise_fma(m, __builtin_bit_cast(h2, sixteenth), -zm[c])
@@ -356,24 +383,24 @@ struct W4WidePolicy {
 #pragma unroll
       for (int i = 0; i < NI; ++i)
 #pragma unroll
-        for (int c = 1; c < 8; c += 2) v[c][i] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2, v[c][i]) + k960);
+        for (int c = C0 + 1; c < C0 + NC; c += 2) v[c][i] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2, v[c][i]) + k960);
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int i = 0; i < NI; ++i)
 #pragma unroll
-        for (int c = 0; c < 8; ++c) v[c][i] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2, v[c][i]) * sc[c]);
+        for (int c = C0; c < C0 + NC; ++c) v[c][i] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2, v[c][i]) * sc[c]);
       __builtin_amdgcn_sched_barrier(0);
     } else {
 #pragma unroll
       for (int i = 0; i < NI; ++i) {
-        v[0][i] = value<0>(P[0][i], g); v[1][i] = value<1>(P[0][i], g);
-        v[2][i] = value<2>(P[1][i], g); v[3][i] = value<3>(P[1][i], g);
-        v[4][i] = value<4>(P[2][i], g); v[5][i] = value<5>(P[2][i], g);
-        v[6][i] = value<6>(P[3][i], g); v[7][i] = value<7>(P[3][i], g);
+        if constexpr (C0 <= 0 && 0 < C0 + NC) { v[0][i] = value<0>(P[0][i], g); v[1][i] = value<1>(P[0][i], g); }
+        if constexpr (C0 <= 2 && 2 < C0 + NC) { v[2][i] = value<2>(P[1][i], g); v[3][i] = value<3>(P[1][i], g); }
+        if constexpr (C0 <= 4 && 4 < C0 + NC) { v[4][i] = value<4>(P[2][i], g); v[5][i] = value<5>(P[2][i], g); }
+        if constexpr (C0 <= 6 && 6 < C0 + NC) { v[6][i] = value<6>(P[3][i], g); v[7][i] = value<7>(P[3][i], g); }
       }
     }
 #pragma unroll
-    for (int c = 0; c < 8; ++c) {
+    for (int c = C0; c < C0 + NC; ++c) {
       uint8_t* p = base + ((c ^ fw) << 4);
       if constexpr (NI == 2) *reinterpret_cast<kbh_u32x2*>(p) = kbh_u32x2{v[c][0], v[c][1]};
       else *reinterpret_cast<uint32_t*>(p) = v[c][0];

@@ -337,9 +337,13 @@ void launch_w4_wide(const W4Wide& w, const void* x, const int32_t* qw, const voi
   const BP bp{(const uint32_t*)qw, (const uint16_t*)s, (const uint16_t*)z, N, group, 0, 0,
               0x000F000Fu};
   const EP ep{(uint16_t*)y, N};
+  // Producer sets of the warp-specialised kernel: two for 64-row tiles, whose MFMA waves need
+  // only 64 accumulator registers, so that 12 waves fit (K=14336 N=4096: M=33 24.2 -> 23.5 us,
+  // M=48 25.4 -> 24.7, M=64 26.7 -> 26.4; an 8-slab raw ring on top measured no faster).
+  constexpr int PS = TM == 64 ? 2 : 1;
   if constexpr (TM <= 128 && TN == 256)
-    hipLaunchKernelGGL((tiled_ws_gemm<E, TM, WM, SPG, BP, EP, DenseRows, w4_wide_pd(TN)>),
-                       dim3(w.plan.grid), dim3(512), 0, st,
+    hipLaunchKernelGGL((tiled_ws_gemm<E, TM, WM, SPG, BP, EP, DenseRows, w4_wide_pd(TN), PS>),
+                       dim3(w.plan.grid), dim3(256 * (1 + PS)), 0, st,
                        x, bp, ep, scratch, M, N, K, w.plan.splits, w.plan.slabs_per_split,
                        DenseRows{M});
   else

@@ -46,9 +46,11 @@ CASES = [
     (200, 1024, 768, 128, torch.bfloat16, "baseline"),
     (384, 4096, 512, 64, torch.float16, "baseline"),
     (257, 8192, 256, 128, torch.float16, "baseline"),
-    # 64 x 256 tiles (M <= 64, N % 256 == 0): 32- and 256-row groups, split-K and not
+    # 64 x 256 tiles (M <= 64, N % 256 == 0; two producer sets): every group size, split-K and not
     (48, 2048, 512, 32, torch.float16, "baseline"),
     (64, 1024, 768, 256, torch.bfloat16, "reference"),
+    (56, 2048, 512, 128, torch.float16, "baseline"),
+    (40, 4096, 256, 128, torch.bfloat16, "reference"),
     # N % 256 != 0 above 128 rows: the 256 x 128 LDS-staged kernel
     (160, 2048, 384, 128, torch.float16, "baseline"),
     # warp-specialised 128-row tiles (64 < M <= 512, N % 256 == 0) with 256- and 32-row groups
