@@ -178,32 +178,76 @@ struct W4WidePolicy {
   // values with fewer instructions. scan_cols reports whether this thread's share of the
   // zero points [k_begin, k_end) x [n0, n0 + cols) allows it; the kernel ANDs the workgroup.
   __device__ bool scan_cols(int k_begin, int k_end, int n0, int cols, int t) const {
+    return scan_from(k_begin, k_end, n0, cols, t, 0);
+  }
+  __device__ bool scan_fast(int k_begin, int k_end, int n0, int t) const {
+    return scan_cols(k_begin, k_end, n0, TN, t);
+  }
+  // The same test in two steps: scan_load issues this thread's first kScanPre chunk loads (the
+  // warp-specialised kernel calls it before the weights' first slabs, so that the zero points
+  // are the first data to come back instead of the last), scan_check tests them and any further
+  // chunks.
+  static constexpr int kScanPre = 4;
+  struct ScanPre {
+    kbh_u32x4 z[kScanPre];
+  };
+  __device__ void scan_load_cols(ScanPre& sp, int k_begin, int k_end, int n0, int cols, int t) const {
+    const int g0 = k_begin / group, chunks = cols / 8;
+    const int total = ((k_end - 1) / group - g0 + 1) * chunks;
+#pragma unroll
+    for (int j = 0; j < kScanPre; ++j) {
+      const int i = t + 256 * j;
+      sp.z[j] = i < total ? *reinterpret_cast<const kbh_u32x4*>(zeros + (size_t)(g0 + i / chunks) * N +
+                                                               n0 + 8 * (i % chunks))
+                          : kbh_u32x4{0u, 0u, 0u, 0u};  // zero points 0: allowed
+    }
+  }
+  __device__ bool scan_check_cols(const ScanPre& sp, int k_begin, int k_end, int n0, int cols,
+                                  int t) const {
+    bool ok = true;
+#pragma unroll
+    for (int j = 0; j < kScanPre; ++j) ok &= zeros_fast(sp.z[j]);
+    return ok & scan_from(k_begin, k_end, n0, cols, t, kScanPre);
+  }
+  __device__ void scan_load(ScanPre& sp, int k_begin, int k_end, int n0, int t) const {
+    scan_load_cols(sp, k_begin, k_end, n0, TN, t);
+  }
+  __device__ bool scan_check(const ScanPre& sp, int k_begin, int k_end, int n0, int t) const {
+    return scan_check_cols(sp, k_begin, k_end, n0, TN, t);
+  }
+  // Whether the 8 fp16 zero points of one chunk allow FAST (always false for bf16).
+  __device__ static bool zeros_fast(kbh_u32x4 zv) {
     if constexpr (BF16) {
       return false;
     } else {
       typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+      const h8 z = __builtin_bit_cast(h8, zv);
+      // z + 1024 rounds to an integer below 2048: the round trip is exact iff z is an integer
+      // in (-1024, 1024); |z| < 960 keeps (64 + q) - (1024 + z) + 960 in range too
+      const h8 bm = (z + (_Float16)1024.0f) - (_Float16)1024.0f;
+      bool ok = true;
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+        ok &= (bm[e] == z[e]) & ((float)z[e] < 960.0f) & ((float)z[e] > -960.0f);
+      return ok;
+    }
+  }
+  // Chunks t + 256 (first + j), j >= 0, of the zero points [k_begin, k_end) x [n0, n0 + cols).
+  __device__ bool scan_from(int k_begin, int k_end, int n0, int cols, int t, int first) const {
+    if constexpr (BF16) {
+      return false;
+    } else {
       const int g0 = k_begin / group, chunks = cols / 8;
       const int total = ((k_end - 1) / group - g0 + 1) * chunks;
       // Branch-free and unrolled, so that the loads of several chunks are in flight together
       // (with short-circuit tests each load waited for the previous chunk's verdict).
       bool ok = true;
 #pragma unroll 4
-      for (int i = t; i < total; i += 256) {
-        const h8 z = __builtin_bit_cast(
-            h8, *reinterpret_cast<const kbh_u32x4*>(zeros + (size_t)(g0 + i / chunks) * N + n0 +
-                                                    8 * (i % chunks)));
-        // z + 1024 rounds to an integer below 2048: the round trip is exact iff z is an integer
-        // in (-1024, 1024); |z| < 960 keeps (64 + q) - (1024 + z) + 960 in range too
-        const h8 bm = (z + (_Float16)1024.0f) - (_Float16)1024.0f;
-#pragma unroll
-        for (int e = 0; e < 8; ++e)
-          ok &= (bm[e] == z[e]) & ((float)z[e] < 960.0f) & ((float)z[e] > -960.0f);
-      }
+      for (int i = t + 256 * first; i < total; i += 256)
+        ok &= zeros_fast(*reinterpret_cast<const kbh_u32x4*>(zeros + (size_t)(g0 + i / chunks) * N +
+                                                             n0 + 8 * (i % chunks)));
       return ok;
     }
-  }
-  __device__ bool scan_fast(int k_begin, int k_end, int n0, int t) const {
-    return scan_cols(k_begin, k_end, n0, TN, t);
   }
   // Derived constants of a loaded group, once before its first slab (the loads have landed).
   template <bool FAST>
