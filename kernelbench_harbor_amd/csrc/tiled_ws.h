@@ -276,9 +276,49 @@ __global__ __launch_bounds__(256 * (1 + PS), 1) void tiled_ws_gemm(
     }
     return;
   }
-  if (wave < 4)
-    wide_store_tile<E, TM, WM, TN>(acc, ep, rm, ti, ws, split, splits, M, N, n0, wave / WN,
-                                   wave % WN, lane);
+  if constexpr (EP::kPaired) {
+    // Paired output (gate/up accumulator blocks j and j + 2 give one output block of TN / 2
+    // columns): also through the ring. The consumers write each output's 16-bit result as one
+    // 32-bit word (RQ rows per pass), then all waves store 16-byte chunks of 8 outputs. Measured
+    // on the Mixtral SiLU FFN's gate/up launch: 16.3k -> 10.3k cycles per workgroup against the
+    // consumers' own 2-byte stores (wide_store_tile); FFN 854 -> 826 us.
+    static_assert(WN == 1 && CB % 4 == 0, "paired output needs whole 128-column chunks per wave");
+    constexpr int NO = TN / 2;                     // output columns of the tile
+    constexpr int RQ = NBUF * SLAB / (NO * 4);     // rows per pass
+    constexpr int RW = TM / WM;                    // rows of one consumer wave
+    static_assert(RQ % RW == 0 || RW % RQ == 0, "whole wave stripes or row blocks per pass");
+    uint32_t* Lw = reinterpret_cast<uint32_t*>(&Bs[0][0]);
+#pragma unroll
+    for (int p = 0; p < (TM + RQ - 1) / RQ; ++p) {
+      __syncthreads();  // the ring (first pass) or the previous pass's rows have been read
+      if (wave < 4) {
+#pragma unroll
+        for (int i = 0; i < RB; ++i) {
+          const int r0 = wave * RW + 32 * i - p * RQ;
+          if (r0 < 0 || r0 >= RQ) continue;
+#pragma unroll
+          for (int j = 0; j < CB; ++j) {
+            if ((j & 3) >= 2) continue;  // second-matrix blocks pair with block j - 2
+#pragma unroll
+            for (int e = 0; e < 16; ++e)
+              Lw[(r0 + 8 * (e >> 2) + 4 * fg + (e & 3)) * NO + 64 * (j >> 2) + 32 * (j & 1) + fr] =
+                  ep.pair_bits(acc[i][j][e], acc[i][j + 2][e]);
+          }
+        }
+      }
+      __syncthreads();
+      for (int q = (int)threadIdx.x; q < RQ * NO / 8; q += NT) {
+        const int rl = q / (NO / 8), c = 8 * (q % (NO / 8));
+        const int r = p * RQ + rl;
+        if (r >= ti.rows) continue;
+        const kbh_u32x4 a = *reinterpret_cast<const kbh_u32x4*>(&Lw[rl * NO + c]);
+        const kbh_u32x4 b = *reinterpret_cast<const kbh_u32x4*>(&Lw[rl * NO + c + 4]);
+        ep.store8(rm.out_row(ti, r), n0 / 2 + c,
+                  kbh_u32x4{a[0] | (a[1] << 16), a[2] | (a[3] << 16), b[0] | (b[1] << 16),
+                            b[2] | (b[3] << 16)});
+      }
+    }
+  }
 }
 
 }  // namespace kbh
