@@ -36,6 +36,7 @@
 #include "tiled_f16.h"
 #include "tiled_wide.h"
 #include "tiled_ws.h"
+#include "tiled_ws256.h"
 #include "w4_dequant.h"
 
 namespace kbh {
@@ -292,8 +293,10 @@ void dispatch_decode(const DecodePlan& p, const void* x, const int32_t* qw, cons
 // CU (128 x 128 tiles, two per CU, up to 128 rows when N is not a multiple of 256); 256 x 256
 // tiles above unless the planner's estimate prefers 128-row tiles. The 256-column tiles run
 // with a 4-slab prefetch ring; those of 64 and 128 rows on the warp-specialised kernel
-// (tiled_ws.h: 4 dequantizing and 4 MFMA waves per workgroup). The older 256 x 128 LDS-staged
-// kernel remains for shapes the wide kernel does not cover.
+// (tiled_ws.h: 4 dequantizing and 4 MFMA waves per workgroup), those of 256 rows on its 12-wave
+// form (tiled_ws256.h: 4 waves stage weights and x, 8 MFMA waves; K=14336 N=4096 M=1024
+// 153.0 -> 137.0 us, M=2048 282.7 -> 250.4 us against the 4-wave kernel). The older 256 x 128
+// LDS-staged kernel remains for shapes the wide kernel does not cover.
 constexpr int kWideMinM = 33;
 constexpr int kTiledMinM = 128;
 
@@ -346,6 +349,10 @@ void launch_w4_wide(const W4Wide& w, const void* x, const int32_t* qw, const voi
                        dim3(w.plan.grid), dim3(256 * (1 + PS)), 0, st,
                        x, bp, ep, scratch, M, N, K, w.plan.splits, w.plan.slabs_per_split,
                        DenseRows{M});
+  else if constexpr (TM == 256 && TN == 256)
+    hipLaunchKernelGGL((tiled_ws256_gemm<E, SPG, BP, EP, w4_wide_pd(TN)>), dim3(w.plan.grid),
+                       dim3(768), 0, st, x, bp, ep, scratch, M, N, K, w.plan.splits,
+                       w.plan.slabs_per_split);
   else
     hipLaunchKernelGGL((tiled_wide_gemm<E, TM, WM, SPG, BP, EP, DenseRows, 0, w4_wide_pd(TN)>),
                        dim3(w.plan.grid), dim3(256), 0, st,
