@@ -2,16 +2,22 @@
 //
 // The computation, weight policy BP, output policy EP and launch geometry of tiled_wide_gemm with
 // 256 x 256 tiles and fp16/bf16 operands, on 12 waves in two roles:
-//  * waves 8..11 (the policy's thread ids t = 0..255) produce both operands of every 32-deep
-//    slab into a 4-buffer LDS ring: the dequantized weights (BP::store_all) and the slab's x
-//    rows (256 rows x 64 bytes), each loaded PD slabs ahead;
+//  * waves 8..11 (the policy's thread ids t = 0..255) dequantize the weights of every 32-deep
+//    slab into a 4-buffer LDS ring (BP::store_all), the packed words loaded PD slabs ahead, and
+//    stage the slab's x rows (256 rows x 64 bytes) into the same ring with LDS-mode buffer
+//    loads, two slabs ahead;
 //  * waves 0..7 only read fragments and issue MFMAs, 64 rows x 128 columns each (4 x 2 waves),
 //    with the accumulators of a whole 256 x 256 tile between them.
 // One barrier per slab, as in tiled_ws_gemm: in slab s the MFMA waves read buffer s % 4, the
 // producers fill (s + 2) % 4, and buffers (s + 1) % 4 (filled a barrier earlier) and (s + 3) % 4
-// are idle, so a write never meets a read. x goes through LDS because an MFMA wave holding 128
-// accumulator registers has no room for a register ring of x fragments (12 waves: at most 168
-// registers per wave).
+// are idle, so a write never meets a read (x for slab s + 2 goes into buffer (s + 2) % 4 as
+// well). x goes through LDS because an MFMA wave holding 128 accumulator registers has no room
+// for a register ring of x fragments (12 waves: at most 168 registers per wave); the LDS-mode
+// loads need no registers at all. The x loads are inline assembly (M0 = the LDS block, then
+// buffer_load_dwordx4 ... lds) and the producers wait for them with explicit vmcnt counts: as
+// compiler builtins, every barrier waited for all of them (vmcnt(0)), including the ones just
+// issued for two slabs later (M=2048 250 -> 296 us). The offsets are 32-bit: the caller keeps
+// (M + 256) x K x 2 bytes under 2 GiB. Rows past M read as zero (the buffer's size bound).
 #pragma once
 
 #include "tiled_ws.h"
@@ -27,18 +33,18 @@ __global__ __launch_bounds__(768, 1) void tiled_ws256_gemm(
   static_assert(!E::kStageX, "fp16/bf16 operands");
   constexpr int SK = E::kSlabK;        // 32 K elements per slab
   constexpr int SLAB = TN * 64;        // B bytes per buffer
-  constexpr int ACH = TM * 16 + 64;    // A bytes per 16-byte chunk column (+64: bank skew)
-  constexpr int ASLAB = 4 * ACH;       // A bytes per buffer: 4 chunks of every row
+  constexpr int ASLAB = TM * 64;       // A bytes per buffer: 256 rows x 64 bytes
   constexpr int NBUF = 4;
-  constexpr int RING = NBUF * (SLAB + ASLAB);
+  constexpr int RING = NBUF * SLAB;    // the weight buffers (the epilogue's staging area)
   constexpr int U = 2 * SPG > PD ? 2 * SPG : PD;  // slabs per loop iteration
   static_assert(PD >= 2 && U % PD == 0 && U % (2 * SPG) == 0 && U % NBUF == 0, "unroll");
   constexpr int RB = 2, CB = 4;  // 32 x 32 blocks of one MFMA wave
   constexpr int NT = 768;
-  constexpr int PDX = 2;  // x prefetch depth (x rows are shared by the column tiles, mostly L2 hits)
+  // The weight buffers (also the epilogue's staging area) and the x buffers.
   __shared__ __attribute__((aligned(16))) uint8_t L[RING];
+  __shared__ __attribute__((aligned(16))) uint8_t A0[ASLAB], A1[ASLAB], A2[ASLAB], A3[ASLAB];
   auto bbuf = [&](int b) { return L + b * SLAB; };
-  auto abuf = [&](int b) { return L + NBUF * SLAB + b * ASLAB; };
+  auto abuf = [&](int b) { return b == 0 ? A0 : b == 1 ? A1 : b == 2 ? A2 : A3; };
 
   const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
   const int lane = threadIdx.x & 63;
@@ -65,39 +71,40 @@ __global__ __launch_bounds__(768, 1) void tiled_ws256_gemm(
     auto load_g = [&](typename BP::Grp& g, int s) {
       bp.load_group(g, (kt0 + min(s, last)) * SK, n0, t);
     };
-    // x: producer wave pw stages rows 64 pw .. 64 pw + 63; lane l loads chunk l % 4 (16 bytes)
-    // of rows 64 pw + 16 i + l / 4, i < 4, so one load covers 16 rows x 64 bytes.
-    const int xc = lane & 3;
-    int xr[4];
-    const uint8_t* xp[4];
+    // x, straight from global memory into the ring with the buffer loads' LDS mode (lane i of a
+    // 16-byte load lands at M0 + 16 i): a load fills one 1 KB block of 16 rows; lane l takes row
+    // l / 4 of the block and the chunk the swizzle puts at position l % 4. Producer wave p
+    // loads blocks 4p .. 4p + 3 of every slab.
+    typedef __attribute__((address_space(3))) void* lds_t;
+    const uint32_t vx =
+        (uint32_t)((m0 + (lane >> 2)) * K * 2 + 16 * ((lane & 3) ^ ((lane >> 4) & 3)));
+    typedef unsigned int u32x4v __attribute__((ext_vector_type(4)));
+    const size_t xb = (size_t)M * K * 2;
+    const uint64_t xa = (uint64_t)(uintptr_t)x;
+    const u32x4v rxs = {(uint32_t)xa, (uint32_t)(xa >> 32) & 0xffffu,
+                        xb >= 0xffffffffu ? 0xffffffffu : (uint32_t)xb, 0x00020000u};
+    auto stage_x = [&](int s, int buf) {
+      const int k0b = (kt0 + min(s, last)) * WSLAB_BYTES;
+      uint8_t* a = abuf(buf);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      xr[i] = 64 * (wave - 8) + 16 * i + (lane >> 2);
-      xp[i] = (const uint8_t*)x + (size_t)(m0 + min(xr[i], rows - 1)) * K * 2 + 16 * xc;
-    }
-    struct XStage {
-      kbh_u32x4 c[4];
-    };
-    auto load_x = [&](XStage& st, int s) {
-      const size_t b0 = (size_t)(kt0 + min(s, last)) * WSLAB_BYTES;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) st.c[i] = *reinterpret_cast<const kbh_u32x4*>(xp[i] + b0);
-    };
-    auto put_x = [&](const XStage& st, uint8_t* a) {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) *reinterpret_cast<kbh_u32x4*>(a + xc * ACH + xr[i] * 16) = st.c[i];
+      for (int h = 0; h < 4; ++h) {
+        const int blk = 4 * (wave - 8) + h;
+        const uint32_t la = (uint32_t)(uintptr_t)(lds_t)(a + 1024 * blk);
+        const uint32_t so = (uint32_t)(16 * blk * K * 2 + k0b);
+        asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
+                     :: "s"(la), "v"(vx), "s"(rxs), "s"(so) : "memory", "m0");
+      }
     };
     typename BP::ScanPre sp;
     if constexpr (kFast) bp.scan_load(sp, kt0 * SK, (kt0 + KT) * SK, n0, t);
     typename BP::Raw R[PD];
-    XStage X[PDX];
     typename BP::Grp G[2];
 #pragma unroll
     for (int i = 0; i < PD; ++i) load_b(R[i], i);
-#pragma unroll
-    for (int i = 0; i < PDX; ++i) load_x(X[i], i);
     load_g(G[0], 0);
     load_g(G[1], SPG);
+    stage_x(0, 0);
+    stage_x(1, 1);
     bool fast = false;
     if constexpr (kFast)
       fast = __syncthreads_and((int)bp.scan_check(sp, kt0 * SK, (kt0 + KT) * SK, n0, t)) != 0;
@@ -108,9 +115,7 @@ __global__ __launch_bounds__(768, 1) void tiled_ws256_gemm(
       };
       bp.template prepare_group<FAST>(G[0]);
       put(R[0], G[0], 0);  // slab 0
-      put_x(X[0], abuf(0));
       load_b(R[0], PD);
-      load_x(X[0], PDX);
       if constexpr (SPG == 1) {  // slab 1 starts group 1; set 0 is reloaded with group 2
         bp.template prepare_group<FAST>(G[1]);
         load_g(G[0], 2);
@@ -118,9 +123,8 @@ __global__ __launch_bounds__(768, 1) void tiled_ws256_gemm(
       } else {
         put(R[1], G[0], 1);
       }
-      put_x(X[1], abuf(1));
       load_b(R[1 % PD], PD + 1);
-      load_x(X[1 % PDX], PDX + 1);
+      asm volatile("s_waitcnt vmcnt(8)" ::: "memory");  // x of slabs 0 and 1 has landed
       __syncthreads();  // slabs 0 and 1 are in LDS
       for (int kt = 0; kt < KT; kt += U) {
 #pragma unroll
@@ -132,9 +136,11 @@ __global__ __launch_bounds__(768, 1) void tiled_ws256_gemm(
             load_g(G[set ^ 1], kt + pu + SPG);
           }
           put(R[pu % PD], G[set], pu % NBUF);
-          put_x(X[pu % PDX], abuf(pu % NBUF));
+          stage_x(kt + pu, pu % NBUF);  // x of slab kt + pu, read two barriers later
           load_b(R[pu % PD], kt + pu + PD);
-          load_x(X[pu % PDX], kt + pu + PDX);
+          // The x loads of the previous slab have landed (at most this slab's 4 x loads, 4 raw
+          // weight loads and 2 group loads are younger).
+          asm volatile("s_waitcnt vmcnt(10)" ::: "memory");
           __syncthreads();
         }
       }
@@ -145,16 +151,25 @@ __global__ __launch_bounds__(768, 1) void tiled_ws256_gemm(
     } else {
       produce(WideFlag<false>{});
     }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // no x load in flight past the loops
   } else {
     // ---- MFMA waves: rows 64 wm .., columns 128 wn .. of the tile ----
+    // x of a slab: row r keeps its 16-byte chunk c at r * 64 + 16 (c ^ ((r >> 2) & 3)) of the
+    // buffer (staged by the producers), so the 16 rows a fragment read covers hit 16 different
+    // bank groups.
     const int wm = wave >> 1, wn = wave & 1;
     if constexpr (kFast) (void)__syncthreads_and(1);  // the producers' FAST barrier
-    int boff[CB];
+    // B fragment j: column 128 wn + 32 j + fr at wide_b_offset = bbase + 512 j + (bsw ^ 16 c_j):
+    // the column slot's low 3 bits are s_0 ^ c_j with c_j = 4 (j & 1) ^ (j >> 1) (two registers
+    // instead of four offsets)
+    const int bsw = 16 * (wide_slot(128 * wn + fr) & 7);
+    const int bbase = wide_b_offset<TN>(16 * fg, 128 * wn + fr) - bsw;
+    // [k16 step]: chunk 2 step + fg of row 64 wm + fr (row block i adds 32 rows: the swizzle
+    // term (r >> 2) & 3 = (fr >> 2) & 3 is the same for both)
+    int aoff[2];
 #pragma unroll
-    for (int j = 0; j < CB; ++j) boff[j] = wide_b_offset<TN>(16 * fg, 128 * wn + 32 * j + fr);
-    int aoff[RB];
-#pragma unroll
-    for (int i = 0; i < RB; ++i) aoff[i] = fg * ACH + (64 * wm + 32 * i + fr) * 16;
+    for (int st = 0; st < 2; ++st)
+      aoff[st] = (64 * wm + fr) * 64 + 16 * ((2 * st + fg) ^ ((fr >> 2) & 3));
 #pragma unroll
     for (int i = 0; i < RB; ++i)
 #pragma unroll
@@ -172,10 +187,11 @@ __global__ __launch_bounds__(768, 1) void tiled_ws256_gemm(
           kbh_u32x4 af[RB], bf[CB];
 #pragma unroll
           for (int i = 0; i < RB; ++i)
-            af[i] = *reinterpret_cast<const kbh_u32x4*>(ab + aoff[i] + 2 * s * ACH);
+            af[i] = *reinterpret_cast<const kbh_u32x4*>(ab + aoff[s] + 32 * 64 * i);
 #pragma unroll
           for (int j = 0; j < CB; ++j)
-            bf[j] = *reinterpret_cast<const kbh_u32x4*>(bb + boff[j] + s * (TN * 32));
+            bf[j] = *reinterpret_cast<const kbh_u32x4*>(
+                bb + bbase + (bsw ^ (16 * ((4 * (j & 1)) ^ (j >> 1)))) + 512 * j + s * (TN * 32));
 #pragma unroll
           for (int i = 0; i < RB; ++i)
 #pragma unroll
@@ -189,7 +205,7 @@ __global__ __launch_bounds__(768, 1) void tiled_ws256_gemm(
   // The tile leaves through the ring, RP rows at a time: the MFMA waves write their
   // accumulators, then all 12 waves store 16-byte chunks of whole rows (fp32 split-K slices, or
   // four outputs at a time through the output policy).
-  constexpr int RP = 128;  // rows per pass: 128 x 256 x 4 bytes of the ring
+  constexpr int RP = 64;  // rows per pass: 64 x 256 x 4 bytes, the weight buffers
   static_assert(RP * TN * 4 <= RING, "pass fits the ring");
   float* Ls = reinterpret_cast<float*>(L);
   typename E::Part* part = ws + (size_t)split * M * N;

@@ -295,7 +295,7 @@ void dispatch_decode(const DecodePlan& p, const void* x, const int32_t* qw, cons
 // with a 4-slab prefetch ring; those of 64 and 128 rows on the warp-specialised kernel
 // (tiled_ws.h: 4 dequantizing and 4 MFMA waves per workgroup), those of 256 rows on its 12-wave
 // form (tiled_ws256.h: 4 waves stage weights and x, 8 MFMA waves; K=14336 N=4096 M=1024
-// 153.0 -> 137.0 us, M=2048 282.7 -> 250.4 us against the 4-wave kernel). The older 256 x 128
+// 153.0 -> 131.7 us, M=2048 282.7 -> 245.9 us against the 4-wave kernel). The older 256 x 128
 // LDS-staged kernel remains for shapes the wide kernel does not cover.
 constexpr int kWideMinM = 33;
 constexpr int kTiledMinM = 128;
@@ -349,15 +349,24 @@ void launch_w4_wide(const W4Wide& w, const void* x, const int32_t* qw, const voi
                        dim3(w.plan.grid), dim3(256 * (1 + PS)), 0, st,
                        x, bp, ep, scratch, M, N, K, w.plan.splits, w.plan.slabs_per_split,
                        DenseRows{M});
-  else if constexpr (TM == 256 && TN == 256)
-    hipLaunchKernelGGL((tiled_ws256_gemm<E, SPG, BP, EP, w4_wide_pd(TN)>), dim3(w.plan.grid),
-                       dim3(768), 0, st, x, bp, ep, scratch, M, N, K, w.plan.splits,
-                       w.plan.slabs_per_split);
-  else
-    hipLaunchKernelGGL((tiled_wide_gemm<E, TM, WM, SPG, BP, EP, DenseRows, 0, w4_wide_pd(TN)>),
-                       dim3(w.plan.grid), dim3(256), 0, st,
-                       x, bp, ep, scratch, M, N, K, w.plan.splits, w.plan.slabs_per_split,
-                       DenseRows{M});
+  else {
+    // 256 x 256 tiles: the 12-wave kernel while x is under 2 GiB (its buffer offsets are
+    // 32-bit), else the 4-wave one.
+    bool done = false;
+    if constexpr (TM == 256 && TN == 256) {
+      if ((size_t)(M + TM) * K * 2 < ((size_t)1 << 31)) {
+        hipLaunchKernelGGL((tiled_ws256_gemm<E, SPG, BP, EP, w4_wide_pd(TN)>), dim3(w.plan.grid),
+                           dim3(768), 0, st, x, bp, ep, scratch, M, N, K, w.plan.splits,
+                           w.plan.slabs_per_split);
+        done = true;
+      }
+    }
+    if (!done)
+      hipLaunchKernelGGL((tiled_wide_gemm<E, TM, WM, SPG, BP, EP, DenseRows, 0, w4_wide_pd(TN)>),
+                         dim3(w.plan.grid), dim3(256), 0, st,
+                         x, bp, ep, scratch, M, N, K, w.plan.splits, w.plan.slabs_per_split,
+                         DenseRows{M});
+  }
   if (w.plan.splits > 1) {
     const size_t n4 = (size_t)M * N / 4;
     hipLaunchKernelGGL((wide_reduce_kernel<E, EP>), dim3((unsigned)((n4 + 255) / 256)), dim3(256),
