@@ -289,7 +289,7 @@ void dispatch_decode(const DecodePlan& p, const void* x, const int32_t* qw, cons
 // Large-M kernels
 // ======================================================================================
 // Above kWideMinM rows the wide-tile kernel (tiled_wide.h) takes over from the split-K decode
-// kernel: up to 64 rows, 64 x 256 tiles; up to 512 rows, 128 x 256 tiles with one workgroup per
+// kernel: up to 64 rows, 64 x 256 tiles; up to 256 rows, 128 x 256 tiles with one workgroup per
 // CU (128 x 128 tiles, two per CU, up to 128 rows when N is not a multiple of 256); 256 x 256
 // tiles above unless the planner's estimate prefers 128-row tiles. The 256-column tiles run
 // with a 4-slab prefetch ring; those of 64 and 128 rows on the warp-specialised kernel
@@ -321,13 +321,13 @@ bool plan_w4_wide(int M, int N, int K, int group, W4Wide* w) {
   // tile would spend half its MFMAs and A loads on padding. The split count is planned for one
   // workgroup per CU: more splits (two per CU) measured slower, their fp32 slices outweighing
   // the extra parallelism (K=14336 N=4096 M=64: 14 splits 31.2 us, 28 splits 34.4 us).
-  // 128-row tiles (one warp-specialised workgroup per CU) up to 512 rows: fewer K splits, so
-  // fewer fp32 slices to write and sum, than 256-row tiles (K=14336 N=4096, M=512: 83.8 against
-  // 91.3 us); 256-row tiles above, where the two measure alike (M=768: 138.2 / 137.6 us,
-  // M=1024: 157.1 / 154.8 us, M=2048: 286.7 / 284-292 us).
+  // 128-row tiles (one warp-specialised workgroup per CU) up to 256 rows: fewer K splits, so
+  // fewer fp32 slices to write and sum, than 256-row tiles (K=14336 N=4096, M=256: 50.5 against
+  // 53.7 us); above, 256-row tiles on the 12-wave kernel unless the estimate prefers 128 rows
+  // (M=320 68.9 against 75.2 us, M=384 71.4 / 77.3, M=512 80.5 / 84.7).
   const bool rows64 = M <= 64 && w->tn == 256;
   return plan_wide(M, N, K, w->tn, 32, unroll, w->tn == 128 ? 512 : 256, &w->plan,
-                   rows64 ? 64 : 128, w->tn == 256, w->tn == 256 ? 512 : 128);
+                   rows64 ? 64 : 128, w->tn == 256, w->tn == 256 ? 256 : 128);
 }
 
 template <bool BF16, int TM, int TN, int SPG>

@@ -39,7 +39,7 @@ CASES = [
     # K not a multiple of 64 -> split-K path even for large M
     (96, 1056, 256, 32, torch.float16, "baseline"),
     # wide-tile kernel: 128x128 tiles (33 <= M <= 128, N % 256 != 0), 128x256 tiles
-    # (64 < M <= 512), 256x256 tiles (M > 512), every group size, split-K and not, ragged M
+    # (64 < M <= 256), 256x256 tiles (M > 256), every group size, split-K and not, ragged M
     (33, 2048, 256, 64, torch.float16, "baseline"),
     (128, 4096, 384, 256, torch.bfloat16, "reference"),
     (129, 2048, 512, 32, torch.float16, "reference"),
@@ -53,12 +53,15 @@ CASES = [
     (40, 4096, 256, 128, torch.bfloat16, "reference"),
     # N % 256 != 0 above 128 rows: the 256 x 128 LDS-staged kernel
     (160, 2048, 384, 128, torch.float16, "baseline"),
-    # warp-specialised 128-row tiles (64 < M <= 512, N % 256 == 0) with 256- and 32-row groups
+    # warp-specialised 128-row tiles (64 < M <= 256, N % 256 == 0) and 256-row tiles above, with
+    # 256- and 32-row groups
     # (the producers' group schedules SPG = 8 and SPG = 1), fp16 and bf16, ragged M
     (160, 4096, 512, 256, torch.float16, "reference"),
     (72, 2048, 512, 32, torch.bfloat16, "baseline"),
     (350, 2048, 256, 256, torch.bfloat16, "reference"),
     (480, 4096, 512, 128, torch.float16, "baseline"),
+    (600, 2048, 512, 32, torch.bfloat16, "baseline"),
+    (777, 2048, 256, 256, torch.float16, "reference"),
 ]
 
 
