@@ -1,23 +1,25 @@
-// Warp-specialised 256 x 256 tiles (tiled_ws256_gemm) for dense W4A16 rows.
+// Warp-specialised 256 x 256 tiles (tiled_ws256_gemm) for dense rows: W4A16 (fp16/bf16) and
+// W8A8 (int8) operands.
 //
 // The computation, weight policy BP, output policy EP and launch geometry of tiled_wide_gemm with
-// 256 x 256 tiles and fp16/bf16 operands, on 12 waves in two roles:
-//  * waves 8..11 (the policy's thread ids t = 0..255) dequantize the weights of every 32-deep
-//    slab into a 4-buffer LDS ring (BP::store_all), the packed words loaded PD slabs ahead, and
-//    stage the slab's x rows (256 rows x 64 bytes) into the same ring with LDS-mode buffer
-//    loads, two slabs ahead;
+// 256 x 256 tiles, on 12 waves in two roles:
+//  * waves 8..11 (the policy's thread ids t = 0..255) write the weights of every slab (64 bytes
+//    of K: 32 fp16/bf16 or 64 int8 values) into a 4-buffer LDS ring in MFMA operand order
+//    (BP::store_all: dequantized W4, or transposed int8), the raw words loaded PD slabs ahead,
+//    and stage the slab's x rows (256 rows x 64 bytes) into the same ring with LDS-mode buffer
+//    loads, three slabs ahead (into the buffer that is idle during the current slab);
 //  * waves 0..7 only read fragments and issue MFMAs, 64 rows x 128 columns each (4 x 2 waves),
 //    with the accumulators of a whole 256 x 256 tile between them.
 // One barrier per slab, as in tiled_ws_gemm: in slab s the MFMA waves read buffer s % 4, the
 // producers fill (s + 2) % 4, and buffers (s + 1) % 4 (filled a barrier earlier) and (s + 3) % 4
-// are idle, so a write never meets a read (x for slab s + 2 goes into buffer (s + 2) % 4 as
-// well). x goes through LDS because an MFMA wave holding 128 accumulator registers has no room
+// are idle, so a write never meets a read (x for slab s + 3 goes into x buffer (s + 3) % 4).
+// x goes through LDS because an MFMA wave holding 128 accumulator registers has no room
 // for a register ring of x fragments (12 waves: at most 168 registers per wave); the LDS-mode
 // loads need no registers at all. The x loads are inline assembly (M0 = the LDS block, then
 // buffer_load_dwordx4 ... lds) and the producers wait for them with explicit vmcnt counts: as
 // compiler builtins, every barrier waited for all of them (vmcnt(0)), including the ones just
 // issued for two slabs later (M=2048 250 -> 296 us). The offsets are 32-bit: the caller keeps
-// (M + 256) x K x 2 bytes under 2 GiB. Rows past M read as zero (the buffer's size bound).
+// (M + 256) rows of x under 2 GiB. Rows past M read as zero (the buffer's size bound).
 #pragma once
 
 #include "tiled_ws.h"
@@ -30,8 +32,8 @@ __global__ __launch_bounds__(768, 1) void tiled_ws256_gemm(
     int K, int splits, int slabs_per_split) {
   constexpr int TM = 256, TN = 256;
   static_assert(BP::kTN == TN, "256-column weight policy");
-  static_assert(!E::kStageX, "fp16/bf16 operands");
-  constexpr int SK = E::kSlabK;        // 32 K elements per slab
+  constexpr int SK = E::kSlabK;        // K elements per slab (64 bytes of every row)
+  constexpr int EB = WSLAB_BYTES / SK;  // bytes per element
   constexpr int SLAB = TN * 64;        // B bytes per buffer
   constexpr int ASLAB = TM * 64;       // A bytes per buffer: 256 rows x 64 bytes
   constexpr int NBUF = 4;
@@ -77,9 +79,9 @@ __global__ __launch_bounds__(768, 1) void tiled_ws256_gemm(
     // loads blocks 4p .. 4p + 3 of every slab.
     typedef __attribute__((address_space(3))) void* lds_t;
     const uint32_t vx =
-        (uint32_t)((m0 + (lane >> 2)) * K * 2 + 16 * ((lane & 3) ^ ((lane >> 4) & 3)));
+        (uint32_t)((m0 + (lane >> 2)) * K * EB + 16 * ((lane & 3) ^ ((lane >> 4) & 3)));
     typedef unsigned int u32x4v __attribute__((ext_vector_type(4)));
-    const size_t xb = (size_t)M * K * 2;
+    const size_t xb = (size_t)M * K * EB;
     const uint64_t xa = (uint64_t)(uintptr_t)x;
     const u32x4v rxs = {(uint32_t)xa, (uint32_t)(xa >> 32) & 0xffffu,
                         xb >= 0xffffffffu ? 0xffffffffu : (uint32_t)xb, 0x00020000u};
@@ -90,7 +92,7 @@ __global__ __launch_bounds__(768, 1) void tiled_ws256_gemm(
       for (int h = 0; h < 4; ++h) {
         const int blk = 4 * (wave - 8) + h;
         const uint32_t la = (uint32_t)(uintptr_t)(lds_t)(a + 1024 * blk);
-        const uint32_t so = (uint32_t)(16 * blk * K * 2 + k0b);
+        const uint32_t so = (uint32_t)(16 * blk * K * EB + k0b);
         asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
                      :: "s"(la), "v"(vx), "s"(rxs), "s"(so) : "memory", "m0");
       }
@@ -105,6 +107,7 @@ __global__ __launch_bounds__(768, 1) void tiled_ws256_gemm(
     load_g(G[1], SPG);
     stage_x(0, 0);
     stage_x(1, 1);
+    stage_x(2, 2);
     bool fast = false;
     if constexpr (kFast)
       fast = __syncthreads_and((int)bp.scan_check(sp, kt0 * SK, (kt0 + KT) * SK, n0, t)) != 0;
@@ -124,7 +127,9 @@ __global__ __launch_bounds__(768, 1) void tiled_ws256_gemm(
         put(R[1], G[0], 1);
       }
       load_b(R[1 % PD], PD + 1);
-      asm volatile("s_waitcnt vmcnt(8)" ::: "memory");  // x of slabs 0 and 1 has landed
+      // x of slabs 0 and 1 has landed (younger: slab 2's 4 x loads, the two 4-word raw loads and
+      // at most one group load pair)
+      asm volatile("s_waitcnt vmcnt(12)" ::: "memory");
       __syncthreads();  // slabs 0 and 1 are in LDS
       for (int kt = 0; kt < KT; kt += U) {
 #pragma unroll
@@ -136,11 +141,13 @@ __global__ __launch_bounds__(768, 1) void tiled_ws256_gemm(
             load_g(G[set ^ 1], kt + pu + SPG);
           }
           put(R[pu % PD], G[set], pu % NBUF);
-          stage_x(kt + pu, pu % NBUF);  // x of slab kt + pu, read two barriers later
+          // x of slab kt + u + 3 into the buffer that is idle during slab kt + u (read three
+          // barriers later)
+          stage_x(kt + u + 3, (u + 3) % NBUF);
           load_b(R[pu % PD], kt + pu + PD);
-          // The x loads of the previous slab have landed (at most this slab's 4 x loads, 4 raw
-          // weight loads and 2 group loads are younger).
-          asm volatile("s_waitcnt vmcnt(10)" ::: "memory");
+          // x of the next slab (issued two iterations ago) has landed: at least 20 loads are
+          // younger (4 raw words of that iteration, 8-10 loads of each of the last two).
+          asm volatile("s_waitcnt vmcnt(20)" ::: "memory");
           __syncthreads();
         }
       }
@@ -207,7 +214,9 @@ __global__ __launch_bounds__(768, 1) void tiled_ws256_gemm(
   // four outputs at a time through the output policy).
   constexpr int RP = 64;  // rows per pass: 64 x 256 x 4 bytes, the weight buffers
   static_assert(RP * TN * 4 <= RING, "pass fits the ring");
-  float* Ls = reinterpret_cast<float*>(L);
+  using Part = typename E::Part;
+  using Part4 = typename E::Part4;
+  Part* Ls = reinterpret_cast<Part*>(L);
   typename E::Part* part = ws + (size_t)split * M * N;
 #pragma unroll
   for (int p = 0; p < TM / RP; ++p) {
@@ -230,9 +239,9 @@ __global__ __launch_bounds__(768, 1) void tiled_ws256_gemm(
       const int rl = q / (TN / 4), c = 4 * (q % (TN / 4));
       const int r = p * RP + rl;
       if (r >= rows) continue;
-      const kbh_f32x4 v = *reinterpret_cast<const kbh_f32x4*>(&Ls[rl * TN + c]);
+      const Part4 v = *reinterpret_cast<const Part4*>(&Ls[rl * TN + c]);
       if (splits > 1)
-        *reinterpret_cast<kbh_f32x4*>(part + (size_t)(m0 + r) * N + n0 + c) = v;
+        *reinterpret_cast<Part4*>(part + (size_t)(m0 + r) * N + n0 + c) = v;
       else
         ep.emit4(m0 + r, n0 + c, v);
     }

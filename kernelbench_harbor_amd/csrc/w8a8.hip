@@ -18,6 +18,7 @@
 #include "kbh_common.h"
 #include "splitk.h"
 #include "tiled_wide.h"
+#include "tiled_ws256.h"
 
 namespace kbh {
 namespace {
@@ -293,6 +294,12 @@ struct W8WidePolicy {
   __device__ bool scan_fast(int, int, int, int) const { return false; }
   template <bool FAST>
   __device__ void prepare_group(Grp&) const {}
+  struct ScanPre {};  // no zero points, no FAST path
+  template <bool FAST>
+  __device__ void store_all(const Raw& r, const Grp& g, uint8_t* Bs, int t) const {
+    store_part<FAST>(r, g, Bs, t, 0);
+    store_part<FAST>(r, g, Bs, t, 1);
+  }
   template <bool FAST>
   __device__ void store_part(const Raw& r, const Grp&, uint8_t* Bs, int t, int p) const {
     const int cb = cb_of(t), rb = rb_of(t);
@@ -364,10 +371,20 @@ void launch_w8_wide(const WidePlan& p, const void* x, const void* w, const void*
   const W8WidePolicy bp{(const int8_t*)w, N};
   const EP ep{out, (const uint16_t*)xs, (const uint16_t*)wsc, N};
   constexpr int MINB = TM == 128 ? 1 : 0;
-  hipLaunchKernelGGL((tiled_wide_gemm<WideI8, TM, 4, 1, W8WidePolicy, EP, DenseRows, MINB, PD>),
-                     dim3(p.grid),
-                     dim3(256), 0, st, x, bp, ep, scratch, M, N, K, p.splits, p.slabs_per_split,
-                     DenseRows{M});
+  // 256-row tiles with a 4-slab ring: the 12-wave kernel (tiled_ws256.h) while x is under 2 GiB.
+  bool done = false;
+  if constexpr (TM == 256 && PD == 4) {
+    if ((size_t)(M + TM) * K < ((size_t)1 << 31)) {
+      hipLaunchKernelGGL((tiled_ws256_gemm<WideI8, 1, W8WidePolicy, EP, PD>), dim3(p.grid),
+                         dim3(768), 0, st, x, bp, ep, scratch, M, N, K, p.splits,
+                         p.slabs_per_split);
+      done = true;
+    }
+  }
+  if (!done)
+    hipLaunchKernelGGL((tiled_wide_gemm<WideI8, TM, 4, 1, W8WidePolicy, EP, DenseRows, MINB, PD>),
+                       dim3(p.grid), dim3(256), 0, st, x, bp, ep, scratch, M, N, K, p.splits,
+                       p.slabs_per_split, DenseRows{M});
   if (p.splits > 1) {
     const size_t n4 = (size_t)M * N / 4;
     hipLaunchKernelGGL((wide_reduce_kernel<WideI8, EP>), dim3((unsigned)((n4 + 255) / 256)),
