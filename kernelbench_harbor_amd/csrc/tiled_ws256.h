@@ -37,16 +37,15 @@ __global__ __launch_bounds__(768, 1) void tiled_ws256_gemm(
   constexpr int SLAB = TN * 64;        // B bytes per buffer
   constexpr int ASLAB = TM * 64;       // A bytes per buffer: 256 rows x 64 bytes
   constexpr int NBUF = 4;
-  constexpr int RING = NBUF * SLAB;    // the weight buffers (the epilogue's staging area)
+  constexpr int RING = NBUF * (SLAB + ASLAB);  // weight and x buffers (the epilogue's staging)
   constexpr int U = 2 * SPG > PD ? 2 * SPG : PD;  // slabs per loop iteration
   static_assert(PD >= 2 && U % PD == 0 && U % (2 * SPG) == 0 && U % NBUF == 0, "unroll");
   constexpr int RB = 2, CB = 4;  // 32 x 32 blocks of one MFMA wave
   constexpr int NT = 768;
-  // The weight buffers (also the epilogue's staging area) and the x buffers.
+  // The weight buffers, then the x buffers; the epilogue stages rows through all of it.
   __shared__ __attribute__((aligned(16))) uint8_t L[RING];
-  __shared__ __attribute__((aligned(16))) uint8_t A0[ASLAB], A1[ASLAB], A2[ASLAB], A3[ASLAB];
   auto bbuf = [&](int b) { return L + b * SLAB; };
-  auto abuf = [&](int b) { return b == 0 ? A0 : b == 1 ? A1 : b == 2 ? A2 : A3; };
+  auto abuf = [&](int b) { return L + NBUF * SLAB + b * ASLAB; };
 
   const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
   const int lane = threadIdx.x & 63;
@@ -212,7 +211,7 @@ __global__ __launch_bounds__(768, 1) void tiled_ws256_gemm(
   // The tile leaves through the ring, RP rows at a time: the MFMA waves write their
   // accumulators, then all 12 waves store 16-byte chunks of whole rows (fp32 split-K slices, or
   // four outputs at a time through the output policy).
-  constexpr int RP = 64;  // rows per pass: 64 x 256 x 4 bytes, the weight buffers
+  constexpr int RP = 128;  // rows per pass: 128 x 256 x 4 bytes, the whole ring
   static_assert(RP * TN * 4 <= RING, "pass fits the ring");
   using Part = typename E::Part;
   using Part4 = typename E::Part4;
