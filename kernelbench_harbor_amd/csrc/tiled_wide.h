@@ -449,6 +449,26 @@ __global__ __launch_bounds__(256) void wide_reduce_kernel(const typename E::Part
   ep.emit4(r, (int)(e - (size_t)r * N), v);
 }
 
+// LDS-mode buffer loads issued as inline assembly (M0 = the LDS address), for kernels that wait
+// for them with explicit vmcnt counts: the compiler does not track such loads, so it adds no
+// waits for them (as a compiler builtin, every barrier after one became a wait for all of them).
+// Lane i's 16 bytes land at LDS byte address lds + 16 i; the global offset is voff + soff within
+// the buffer r (offsets are 32-bit; loads past the buffer's size read as zero).
+typedef unsigned int kbh_rsrc4 __attribute__((ext_vector_type(4)));
+__device__ inline kbh_rsrc4 raw_rsrc(const void* p, size_t bytes) {
+  const uint64_t a = (uint64_t)(uintptr_t)p;
+  return kbh_rsrc4{(uint32_t)a, (uint32_t)(a >> 32) & 0xffffu,
+                   bytes >= 0xffffffffu ? 0xffffffffu : (uint32_t)bytes, 0x00020000u};
+}
+__device__ inline uint32_t lds_addr(const void* p) {
+  typedef __attribute__((address_space(3))) const void* lds_cptr;
+  return (uint32_t)(uintptr_t)(lds_cptr)p;
+}
+__device__ inline void lds_load16(uint32_t lds, uint32_t voff, kbh_rsrc4 r, uint32_t soff) {
+  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
+               :: "s"(lds), "v"(voff), "s"(r), "s"(soff) : "memory", "m0");
+}
+
 // Split-K plans keep their partial-sum slices within this many bytes (the writes and reads of
 // more cost more than the extra splits gain, and it bounds the scratch a call needs).
 constexpr size_t kWideMaxSliceBytes = (size_t)64 << 20;

@@ -43,8 +43,12 @@ struct WsRaw<BP, 2> {
 //   loop on the same thread ids and barriers, set p loading and dequantizing row pair p of each
 //   thread's rows (BP::load_half / store_half), so two producer waves share each SIMD's VALU
 //   with the MFMA wave (768 threads, at most 168 VGPRs per wave: 64-row tiles).
+// XD: x through the LDS ring too (128-row tiles, one producer set): the producers stage each
+//   slab's x rows with LDS-mode buffer loads three slabs ahead (as tiled_ws256_gemm does) and the
+//   MFMA waves read their A fragments from LDS instead of holding a register ring of them. The
+//   x offsets are 32-bit: the caller keeps M x K x 2 bytes under 2 GiB.
 template <class E, int TM, int WM, int SPG, class BP, class EP, class RM = DenseRows, int PD = 4,
-          int PS = 1>
+          int PS = 1, bool XD = false>
 __global__ __launch_bounds__(256 * (1 + PS), 1) void tiled_ws_gemm(
     const void* __restrict__ x, BP bp, EP ep, typename E::Part* __restrict__ ws, int M, int N,
     int K, int splits, int slabs_per_split, RM rm) {
@@ -58,8 +62,11 @@ __global__ __launch_bounds__(256 * (1 + PS), 1) void tiled_ws_gemm(
   constexpr int U = 2 * SPG > PD ? 2 * SPG : PD;  // slabs per loop iteration
   static_assert(PD >= 2 && U % PD == 0 && U % (2 * SPG) == 0 && U % NBUF == 0, "unroll");
   static_assert(PS == 1 || PS == 2, "one or two producer sets");
+  static_assert(!XD || (TM == 128 && WM == 4 && PS == 1 && !E::kStageX), "LDS x: 128-row fp16 tiles");
   constexpr int NT = 256 * (1 + PS);  // threads
   __shared__ __attribute__((aligned(16))) uint8_t Bs[NBUF][SLAB];
+  // XD: x of a slab, row r keeping its 16-byte chunk c at r * 64 + 16 (c ^ ((r >> 2) & 3)).
+  __shared__ __attribute__((aligned(16))) uint8_t Xs[XD ? NBUF : 1][XD ? TM * 64 : 16];
 
   const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
   const int lane = threadIdx.x & 63;
@@ -113,6 +120,30 @@ __global__ __launch_bounds__(256 * (1 + PS), 1) void tiled_ws_gemm(
     for (int i = 0; i < PD; ++i) load_b(R[i], i);
     load_g(G[0], 0);
     load_g(G[1], SPG);
+    // XD: producer wave p stages x blocks 2p and 2p + 1 (16 rows each) of every slab; lane l
+    // takes row l / 4 of a block and the chunk the swizzle puts at position l % 4.
+    uint32_t vxh[2] = {0u, 0u};
+    kbh_rsrc4 rx = {0u, 0u, 0u, 0u};
+    auto stage_x = [&](int s, int buf) {
+      if constexpr (XD) {
+        const uint32_t k0b = (uint32_t)((kt0 + min(s, last)) * WSLAB_BYTES);
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+          lds_load16(lds_addr(&Xs[buf][1024 * (2 * (wave - 4) + h)]), vxh[h], rx, k0b);
+      }
+    };
+    if constexpr (XD) {
+      rx = raw_rsrc(x, (size_t)M * K * 2);
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const int r = 16 * (2 * (wave - 4) + h) + (lane >> 2);
+        vxh[h] = (uint32_t)((size_t)rm.a_row(ti, r) * K * 2) +
+                 (uint32_t)(16 * ((lane & 3) ^ ((lane >> 4) & 3)));
+      }
+      stage_x(0, 0);
+      stage_x(1, 1);
+      stage_x(2, 2);
+    }
     bool fast = false;
     if constexpr (kFast)
       fast = __syncthreads_and(pset == 0 ? (int)bp.scan_check(sp, kt0 * SK, (kt0 + KT) * SK, n0, t) : 1) != 0;
@@ -133,6 +164,9 @@ __global__ __launch_bounds__(256 * (1 + PS), 1) void tiled_ws_gemm(
         put(R[1], G[0], Bs[1]);
       }
       load_b(R[1 % PD], PD + 1);
+      // XD: x of slabs 0 and 1 has landed (younger: slab 2's two x loads, the two raw-word
+      // loads and at most one group load pair)
+      if constexpr (XD) asm volatile("s_waitcnt vmcnt(10)" ::: "memory");
       __syncthreads();  // slabs 0 and 1 are in LDS
       // Slab kt + u + 2 during consumer slab kt + u. Slabs past the end re-produce the last one
       // into a buffer nobody reads, so the loop has no branch.
@@ -146,7 +180,10 @@ __global__ __launch_bounds__(256 * (1 + PS), 1) void tiled_ws_gemm(
             load_g(G[set ^ 1], kt + pu + SPG);
           }
           put(R[pu % PD], G[set], Bs[pu % NBUF]);
+          stage_x(kt + u + 3, (u + 3) % NBUF);  // into the x buffer idle during slab kt + u
           load_b(R[pu % PD], kt + pu + PD);
+          // XD: x of the next slab has landed (at least 16 loads are younger)
+          if constexpr (XD) asm volatile("s_waitcnt vmcnt(16)" ::: "memory");
           __syncthreads();
         }
       }
@@ -157,6 +194,7 @@ __global__ __launch_bounds__(256 * (1 + PS), 1) void tiled_ws_gemm(
     } else {
       produce(WideFlag<false>{});
     }
+    if constexpr (XD) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // none past the loops
   } else {
     // ---- consumers ----
     const int wm = wave / WN, wn = wave % WN;
@@ -172,16 +210,30 @@ __global__ __launch_bounds__(256 * (1 + PS), 1) void tiled_ws_gemm(
       kbh_u32x4 a[RB][2];
     };
     auto load_a = [&](AStage& st, int s) {
-      const size_t b0 = (size_t)(kt0 + min(s, last)) * WSLAB_BYTES;
+      if constexpr (!XD) {
+        const size_t b0 = (size_t)(kt0 + min(s, last)) * WSLAB_BYTES;
 #pragma unroll
-      for (int rb = 0; rb < RB; ++rb)
+        for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+          for (int h = 0; h < 2; ++h)
+            st.a[rb][h] = *reinterpret_cast<const kbh_u32x4*>(xrow[rb] + b0 + 32 * h);
+      }
+    };
+    // XD: the fragment of k16 step h, chunk 2h + fg of row 32 wm + fr (RB = 1), from LDS
+    int xoff[2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) xoff[h] = (32 * wm + fr) * 64 + 16 * ((2 * h + fg) ^ ((fr >> 2) & 3));
+    auto read_a = [&](AStage& st, int buf) {
+      if constexpr (XD) {
 #pragma unroll
         for (int h = 0; h < 2; ++h)
-          st.a[rb][h] = *reinterpret_cast<const kbh_u32x4*>(xrow[rb] + b0 + 32 * h);
+          st.a[0][h] = *reinterpret_cast<const kbh_u32x4*>(&Xs[buf][xoff[h]]);
+      }
     };
-    AStage A[PD];  // slot s % PD holds the x fragments of slab s
+    constexpr int PDA = XD ? 1 : PD;  // register ring of x fragments
+    AStage A[PDA];  // slot s % PD holds the x fragments of slab s (XD: the current slab's)
 #pragma unroll
-    for (int i = 0; i < PD; ++i) load_a(A[i], i);
+    for (int i = 0; i < PDA; ++i) load_a(A[i], i);
     if constexpr (kFast) (void)__syncthreads_and(1);  // the producers' FAST barrier
     int boff[CB];
 #pragma unroll
@@ -206,7 +258,8 @@ __global__ __launch_bounds__(256 * (1 + PS), 1) void tiled_ws_gemm(
     for (int kt = 0; kt < KT; kt += U) {
 #pragma unroll
       for (int u = 0; u < U; ++u) {
-        const int cur = u % NBUF, nxt = (u + 1) % NBUF, ra = u % PD;
+        const int cur = u % NBUF, nxt = (u + 1) % NBUF, ra = u % PDA;
+        read_a(A[ra], cur);
         read_b(b1, cur, 1);
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll

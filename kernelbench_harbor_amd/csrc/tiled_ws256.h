@@ -76,24 +76,16 @@ __global__ __launch_bounds__(768, 1) void tiled_ws256_gemm(
     // 16-byte load lands at M0 + 16 i): a load fills one 1 KB block of 16 rows; lane l takes row
     // l / 4 of the block and the chunk the swizzle puts at position l % 4. Producer wave p
     // loads blocks 4p .. 4p + 3 of every slab.
-    typedef __attribute__((address_space(3))) void* lds_t;
     const uint32_t vx =
         (uint32_t)((m0 + (lane >> 2)) * K * EB + 16 * ((lane & 3) ^ ((lane >> 4) & 3)));
-    typedef unsigned int u32x4v __attribute__((ext_vector_type(4)));
-    const size_t xb = (size_t)M * K * EB;
-    const uint64_t xa = (uint64_t)(uintptr_t)x;
-    const u32x4v rxs = {(uint32_t)xa, (uint32_t)(xa >> 32) & 0xffffu,
-                        xb >= 0xffffffffu ? 0xffffffffu : (uint32_t)xb, 0x00020000u};
+    const kbh_rsrc4 rxs = raw_rsrc(x, (size_t)M * K * EB);
     auto stage_x = [&](int s, int buf) {
       const int k0b = (kt0 + min(s, last)) * WSLAB_BYTES;
-      uint8_t* a = abuf(buf);
+      const uint8_t* a = abuf(buf);
 #pragma unroll
       for (int h = 0; h < 4; ++h) {
         const int blk = 4 * (wave - 8) + h;
-        const uint32_t la = (uint32_t)(uintptr_t)(lds_t)(a + 1024 * blk);
-        const uint32_t so = (uint32_t)(16 * blk * K * EB + k0b);
-        asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
-                     :: "s"(la), "v"(vx), "s"(rxs), "s"(so) : "memory", "m0");
+        lds_load16(lds_addr(a + 1024 * blk), vx, rxs, (uint32_t)(16 * blk * K * EB + k0b));
       }
     };
     typename BP::ScanPre sp;

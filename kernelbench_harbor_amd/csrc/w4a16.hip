@@ -344,12 +344,20 @@ void launch_w4_wide(const W4Wide& w, const void* x, const int32_t* qw, const voi
   // only 64 accumulator registers, so that 12 waves fit (K=14336 N=4096: M=33 24.2 -> 23.5 us,
   // M=48 25.4 -> 24.7, M=64 26.7 -> 26.4; an 8-slab raw ring on top measured no faster).
   constexpr int PS = TM == 64 ? 2 : 1;
-  if constexpr (TM <= 128 && TN == 256)
-    hipLaunchKernelGGL((tiled_ws_gemm<E, TM, WM, SPG, BP, EP, DenseRows, w4_wide_pd(TN), PS>),
-                       dim3(w.plan.grid), dim3(256 * (1 + PS)), 0, st,
-                       x, bp, ep, scratch, M, N, K, w.plan.splits, w.plan.slabs_per_split,
-                       DenseRows{M});
-  else {
+  if constexpr (TM <= 128 && TN == 256) {
+    // 128-row tiles stage x through LDS too (XD) while x is under 2 GiB.
+    if (TM == 128 && (size_t)M * K * 2 < ((size_t)1 << 31))
+      hipLaunchKernelGGL((tiled_ws_gemm<E, TM, WM, SPG, BP, EP, DenseRows, w4_wide_pd(TN), PS,
+                                        TM == 128>),
+                         dim3(w.plan.grid), dim3(256 * (1 + PS)), 0, st,
+                         x, bp, ep, scratch, M, N, K, w.plan.splits, w.plan.slabs_per_split,
+                         DenseRows{M});
+    else
+      hipLaunchKernelGGL((tiled_ws_gemm<E, TM, WM, SPG, BP, EP, DenseRows, w4_wide_pd(TN), PS>),
+                         dim3(w.plan.grid), dim3(256 * (1 + PS)), 0, st,
+                         x, bp, ep, scratch, M, N, K, w.plan.splits, w.plan.slabs_per_split,
+                         DenseRows{M});
+  } else {
     // 256 x 256 tiles: the 12-wave kernel while x is under 2 GiB (its buffer offsets are
     // 32-bit), else the 4-wave one.
     bool done = false;
