@@ -834,9 +834,10 @@ void launch_ffn_wide_spg(const FfnPlan& fp, const MoeLayout& L, const MoeBuffers
     const BP bp{gp, upp};
     const SiluPairOut<BF16> ep{(uint16_t*)h, F};
     const int grid = L.max_tiles * (2 * F / 256);
-    // 128-row tiles stage x through LDS (XD; x of T x D fp16 values, under 2 GiB).
+    // 128-row tiles: 2 x 2 MFMA waves of 64 x 128 (each wave one gate/up column pair chunk), x
+    // staged through LDS (XD; x of T x D fp16 values, under 2 GiB).
     if constexpr (TM == 128)
-      hipLaunchKernelGGL((tiled_ws_gemm<E, TM, 4, SPG, BP, SiluPairOut<BF16>, RM, kFfnPD, 1, true>),
+      hipLaunchKernelGGL((tiled_ws_gemm<E, TM, 2, SPG, BP, SiluPairOut<BF16>, RM, kFfnPD, 1, true>),
                          dim3(grid), dim3(512), 0, st, x, bp, ep, (float*)nullptr, 2 * T, 2 * F,
                          D, 1, D / 32, RM{mb.tiles, mb.perm});
     else
@@ -852,7 +853,7 @@ void launch_ffn_wide_spg(const FfnPlan& fp, const MoeLayout& L, const MoeBuffers
     const int splits = fp.down.splits;
     const int grid = L.max_tiles * (D / 256) * splits;
     if constexpr (TM == 128)
-      hipLaunchKernelGGL((tiled_ws_gemm<E, TM, 4, SPG, BP, HalfOut<BF16>, RM, kFfnPD, 1, true>),
+      hipLaunchKernelGGL((tiled_ws_gemm<E, TM, 2, SPG, BP, HalfOut<BF16>, RM, kFfnPD, 1, true>),
                          dim3(grid), dim3(512), 0, st, h, dp, ep, part, 2 * T, D, F, splits,
                          fp.down.slabs_per_split, RM{mb.tiles, mb.perm});
     else

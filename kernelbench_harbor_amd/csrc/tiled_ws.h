@@ -62,7 +62,7 @@ __global__ __launch_bounds__(256 * (1 + PS), 1) void tiled_ws_gemm(
   constexpr int U = 2 * SPG > PD ? 2 * SPG : PD;  // slabs per loop iteration
   static_assert(PD >= 2 && U % PD == 0 && U % (2 * SPG) == 0 && U % NBUF == 0, "unroll");
   static_assert(PS == 1 || PS == 2, "one or two producer sets");
-  static_assert(!XD || (TM == 128 && WM == 4 && PS == 1 && !E::kStageX), "LDS x: 128-row fp16 tiles");
+  static_assert(!XD || (TM == 128 && PS == 1 && !E::kStageX), "LDS x: 128-row fp16 tiles");
   constexpr int NT = 256 * (1 + PS);  // threads
   __shared__ __attribute__((aligned(16))) uint8_t Bs[NBUF][SLAB];
   // XD: x of a slab, row r keeping its 16-byte chunk c at r * 64 + 16 (c ^ ((r >> 2) & 3)).
@@ -222,12 +222,15 @@ __global__ __launch_bounds__(256 * (1 + PS), 1) void tiled_ws_gemm(
     // XD: the fragment of k16 step h, chunk 2h + fg of row 32 wm + fr (RB = 1), from LDS
     int xoff[2];
 #pragma unroll
-    for (int h = 0; h < 2; ++h) xoff[h] = (32 * wm + fr) * 64 + 16 * ((2 * h + fg) ^ ((fr >> 2) & 3));
+    for (int h = 0; h < 2; ++h)
+      xoff[h] = (wm * (TM / WM) + fr) * 64 + 16 * ((2 * h + fg) ^ ((fr >> 2) & 3));
     auto read_a = [&](AStage& st, int buf) {
       if constexpr (XD) {
 #pragma unroll
-        for (int h = 0; h < 2; ++h)
-          st.a[0][h] = *reinterpret_cast<const kbh_u32x4*>(&Xs[buf][xoff[h]]);
+        for (int i = 0; i < RB; ++i)
+#pragma unroll
+          for (int h = 0; h < 2; ++h)
+            st.a[i][h] = *reinterpret_cast<const kbh_u32x4*>(&Xs[buf][xoff[h] + 2048 * i]);
       }
     };
     constexpr int PDA = XD ? 1 : PD;  // register ring of x fragments
@@ -335,7 +338,7 @@ __global__ __launch_bounds__(256 * (1 + PS), 1) void tiled_ws_gemm(
     // 32-bit word (RQ rows per pass), then all waves store 16-byte chunks of 8 outputs. Measured
     // on the Mixtral SiLU FFN's gate/up launch: 16.3k -> 10.3k cycles per workgroup against the
     // consumers' own 2-byte stores (wide_store_tile); FFN 854 -> 826 us.
-    static_assert(WN == 1 && CB % 4 == 0, "paired output needs whole 128-column chunks per wave");
+    static_assert(CB % 4 == 0, "paired output needs whole 128-column chunks per wave");
     constexpr int NO = TN / 2;                     // output columns of the tile
     constexpr int RQ = NBUF * SLAB / (NO * 4);     // rows per pass
     constexpr int RW = TM / WM;                    // rows of one consumer wave
@@ -347,14 +350,15 @@ __global__ __launch_bounds__(256 * (1 + PS), 1) void tiled_ws_gemm(
       if (wave < 4) {
 #pragma unroll
         for (int i = 0; i < RB; ++i) {
-          const int r0 = wave * RW + 32 * i - p * RQ;
+          const int r0 = (wave / WN) * RW + 32 * i - p * RQ;
           if (r0 < 0 || r0 >= RQ) continue;
 #pragma unroll
           for (int j = 0; j < CB; ++j) {
             if ((j & 3) >= 2) continue;  // second-matrix blocks pair with block j - 2
+            const int jg = (wave % WN) * CB + j;  // block index within the tile
 #pragma unroll
             for (int e = 0; e < 16; ++e)
-              Lw[(r0 + 8 * (e >> 2) + 4 * fg + (e & 3)) * NO + 64 * (j >> 2) + 32 * (j & 1) + fr] =
+              Lw[(r0 + 8 * (e >> 2) + 4 * fg + (e & 3)) * NO + 64 * (jg >> 2) + 32 * (jg & 1) + fr] =
                   ep.pair_bits(acc[i][j][e], acc[i][j + 2][e]);
           }
         }

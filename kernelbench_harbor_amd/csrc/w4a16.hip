@@ -336,7 +336,10 @@ void launch_w4_wide(const W4Wide& w, const void* x, const int32_t* qw, const voi
   using E = WideHalf<BF16>;
   using BP = W4WidePolicy<BF16, TN>;
   using EP = HalfOut<BF16>;
-  constexpr int WM = TM == 64 ? 2 : 4;  // waves along M
+  // MFMA waves along M: 2 x 2 waves for 64- and 128-row tiles (128-row tiles: 64 x 128 per wave,
+  // each B fragment read by 2 waves instead of 4; K=14336 N=4096 M=128 35.6 -> 34.9 us, M=256
+  // 50.9 -> 49.8 against 4 x 1 waves of 32 x 256), 4 x 1 for the 4-wave kernel's 256-row tiles.
+  constexpr int WM = TM == 256 ? 4 : 2;
   const BP bp{(const uint32_t*)qw, (const uint16_t*)s, (const uint16_t*)z, N, group, 0, 0,
               0x000F000Fu};
   const EP ep{(uint16_t*)y, N};
