@@ -54,11 +54,11 @@ def w4a16_bytes(M, K=K_DIM, N=N_DIM, G=GROUP):
 # every kbh:: kernel of the call. Table and commands: profiles/hbm_traffic_all_records.md.
 PMC_TRAFFIC = {
     "w4a16 M=1": 32_167_648, "w4a16 M=4": 34_454_252, "w4a16 M=16": 42_545_554,
-    "w4a16 M=64": 64_036_864, "w4a16 M=256": 108_212_224, "w4a16 M=1024": 238_119_731,
+    "w4a16 M=64": 64_036_864, "w4a16 M=256": 108_226_970, "w4a16 M=1024": 238_119_731,
     "w4a16 M=2048": 340_120_166, "w8a8 M=16": 68_182_320, "w8a8 M=512": 206_879_744,
     "mxfp8 M=128": 94_936_720, "mxfp8 M=2048": 483_042_099,
     "fp8w (reference op) M=16 b128": 70_943_466,
-    "qmoe_ffn T=512 D=4096 F=14336 E=8 top2": 1_225_718_170,
+    "qmoe_ffn T=512 D=4096 F=14336 E=8 top2": 1_219_607_347,
     "silu_fp8 (reference op) T=512 H=14336 g128": 61_112_077,
     "qmoe (reference op) T=256 D=4096 N=14336 E=8": 570_156_646,
 }
@@ -70,13 +70,13 @@ PMC_TRAFFIC = {
 # kernels (W4A16 M=1: 13.4 us traced against 12.1 us graph-replayed). Table and commands:
 # profiles/bench_kernel_trace.md.
 KERNEL_TRACE_US = {
-    "w4a16 M=1": 13.03, "w4a16 M=4": 13.18, "w4a16 M=16": 15.46, "w4a16 M=64": 26.10,
-    "w4a16 M=256": 49.97, "w4a16 M=1024": 133.03, "w4a16 M=2048": 246.94,
-    "w8a8 M=16": 19.43, "w8a8 M=512": 54.84, "mxfp8 M=128": 32.31, "mxfp8 M=2048": 151.97,
-    "fp8w (reference op) M=16 b128": 20.87,
-    "qmoe_ffn T=512 D=4096 F=14336 E=8 top2": 815.26,
-    "silu_fp8 (reference op) T=512 H=14336 g128": 13.29,
-    "qmoe (reference op) T=256 D=4096 N=14336 E=8": 197.59,
+    "w4a16 M=1": 12.98, "w4a16 M=4": 13.32, "w4a16 M=16": 15.53, "w4a16 M=64": 27.22,
+    "w4a16 M=256": 49.73, "w4a16 M=1024": 130.89, "w4a16 M=2048": 242.07,
+    "w8a8 M=16": 18.80, "w8a8 M=512": 56.04, "mxfp8 M=128": 32.59, "mxfp8 M=2048": 152.87,
+    "fp8w (reference op) M=16 b128": 20.75,
+    "qmoe_ffn T=512 D=4096 F=14336 E=8 top2": 770.31,
+    "silu_fp8 (reference op) T=512 H=14336 g128": 13.38,
+    "qmoe (reference op) T=256 D=4096 N=14336 E=8": 196.17,
 }
 
 def gemm_flops(M, N=N_DIM, K=K_DIM):
