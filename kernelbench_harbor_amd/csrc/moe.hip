@@ -835,7 +835,8 @@ void launch_ffn_wide_spg(const FfnPlan& fp, const MoeLayout& L, const MoeBuffers
     const SiluPairOut<BF16> ep{(uint16_t*)h, F};
     const int grid = L.max_tiles * (2 * F / 256);
     // 128-row tiles: 2 x 2 MFMA waves of 64 x 128 (each wave one gate/up column pair chunk), x
-    // staged through LDS (XD; x of T x D fp16 values, under 2 GiB).
+    // staged through LDS (XD: 32-bit offsets; ffn_layout takes this path only while 2T rows of
+    // x and of h stay under 2 GiB).
     if constexpr (TM == 128)
       hipLaunchKernelGGL((tiled_ws_gemm<E, TM, 2, SPG, BP, SiluPairOut<BF16>, RM, kFfnPD, 1, true>),
                          dim3(grid), dim3(512), 0, st, x, bp, ep, (float*)nullptr, 2 * T, 2 * F,
@@ -904,8 +905,11 @@ void launch_ffn_wide(const FfnPlan& fp, const MoeLayout& L, const MoeBuffers& mb
 // FFN layout: TM-row tiles (the plan's) and room for the down projection's split-K partials when the wide
 // path applies (plan_ffn); otherwise the 256 x 128 grouped kernels run.
 MoeLayout ffn_layout(int T, int E, int D, int F, int group, bool* wide, FfnPlan* fp) {
+  // The wide path stages x (T x D) and h (2T x F) through LDS with 32-bit buffer offsets, so it
+  // needs 2T rows of either under 2 GiB; beyond that the grouped kernels (64-bit addresses) run.
+  const size_t act_bytes = (size_t)2 * T * (size_t)(D > F ? D : F) * 2;
   *wide = (group == 32 || group == 64 || group == 128 || group == 256) &&
-          plan_ffn(T, E, D, F, group, fp);
+          act_bytes < ((size_t)1 << 31) && plan_ffn(T, E, D, F, group, fp);
   if (!*wide) return moe_layout(T, E, F, D);
   const size_t part = fp->down.splits > 1 ? (size_t)fp->down.splits * 2 * T * D * 4 : 0;
   return moe_layout(T, E, F, D, fp->tm, part);
