@@ -5,9 +5,10 @@
 //  * waves 4..7 (256 threads, the policy's thread ids t = 0..255) only produce: they load the
 //    packed weights PD slabs ahead, dequantize slab s + 2 into LDS buffer (s + 2) % 4 and load
 //    the quantization groups' constants;
-//  * waves 0..3 only consume: x fragments straight from global memory (PD slabs ahead), the B
-//    fragments of slab s from LDS buffer s % 4 (and, before the slab's barrier, the step-0
-//    fragments of slab s + 1, which was completed one barrier earlier), and the MFMAs.
+//  * waves 0..3 only consume: x fragments straight from global memory (PD slabs ahead; with XD,
+//    128-row tiles, from an LDS x buffer the producers fill three slabs ahead), the B fragments
+//    of slab s from LDS buffer s % 4 (and, before the slab's barrier, the step-0 fragments of
+//    slab s + 1, which was completed one barrier earlier), and the MFMAs.
 // One barrier per slab. Buffer (s + 3) % 4 is idle during slab s, so a producer write never
 // meets a consumer read: in slab s the consumers read buffers s % 4 and (s + 1) % 4 and the
 // producers write (s + 2) % 4. Each SIMD holds one wave of each role, so the dequantizing VALU
