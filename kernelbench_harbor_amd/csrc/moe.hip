@@ -629,8 +629,9 @@ struct W4PairPolicy {
     u.scan_load_cols(sp.u, k_begin, k_end, n0 / 2, TN / 2, t);
   }
   __device__ bool scan_check(const ScanPre& sp, int k_begin, int k_end, int n0, int t) const {
-    return g.scan_check_cols(sp.g, k_begin, k_end, n0 / 2, TN / 2, t) &
-           u.scan_check_cols(sp.u, k_begin, k_end, n0 / 2, TN / 2, t);
+    // both checks run (no short circuit), so both matrices' scan loads are consumed together
+    return (int)g.scan_check_cols(sp.g, k_begin, k_end, n0 / 2, TN / 2, t) &
+           (int)u.scan_check_cols(sp.u, k_begin, k_end, n0 / 2, TN / 2, t);
   }
   template <bool FAST>
   __device__ void prepare_group(Grp& gr) const { g.template prepare_group<FAST>(gr); }

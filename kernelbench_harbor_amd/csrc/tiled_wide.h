@@ -464,10 +464,16 @@ __device__ inline uint32_t lds_addr(const void* p) {
   typedef __attribute__((address_space(3))) const void* lds_cptr;
   return (uint32_t)(uintptr_t)(lds_cptr)p;
 }
+// The m0 clobber is declared although clang reports m0 as reserved (-Winline-asm): the compiler
+// sets m0 itself before each of its own m0 uses, and no kernel here keeps a value in m0 across
+// these loads (every one of them sets m0 first).
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
 __device__ inline void lds_load16(uint32_t lds, uint32_t voff, kbh_rsrc4 r, uint32_t soff) {
   asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
                :: "s"(lds), "v"(voff), "s"(r), "s"(soff) : "memory", "m0");
 }
+#pragma clang diagnostic pop
 
 // Split-K plans keep their partial-sum slices within this many bytes (the writes and reads of
 // more cost more than the extra splits gain, and it bounds the scratch a call needs).
