@@ -1,7 +1,7 @@
 #!/usr/bin/env python3
 """Benchmark of the quantized-GEMM operator path on one MI355X.
 
-Headline (BASELINE metric, configs[1]): the W4A16 g128 GEMM sweep. One step = one W4A16 call
+Headline (the benchmark metric, the W4A16 configuration): the W4A16 g128 GEMM sweep. One step = one W4A16 call
 at every M in {1, 4, 16, 64, 256, 1024, 2048} with K=14336, N=4096, fp16. `value` = total
 FLOPs of a step / wall time of a step (TFLOP/s).
 
@@ -10,7 +10,7 @@ M in {128, 2048}, the top-2 W4A16 MoE SiLU FFN (T=512, Mixtral layer), the refer
 (T=256), the reference FP8 weight-only op (M=16) and the reference fused SiLU + FP8 quantisation
 (T=512, H=14336).
 
-Inputs are synthetic (seeded, BASELINE distributions) and resident in HBM before timing. Each
+Inputs are synthetic (seeded, the benchmark's distributions) and resident in HBM before timing. Each
 configuration rotates over enough input copies (> 2x the 256 MB Infinity Cache) that every call
 streams its weights from HBM. Per configuration two timings are reported: the median of 100
 event-bracketed single calls after 25 warm-up calls (`us_median`, the reference grader's
@@ -324,14 +324,14 @@ def cpu_time(fn, ins, max_calls=5, budget_s=9.0, warmups=2):
 
 
 # Records whose native-dtype CPU path is always timed, whatever the host's fp16 GEMM rate:
-# BASELINE configuration 0 (the reference W4A16 module on CPU, M=16) is the named CPU baseline.
+# The benchmark's CPU configuration (the reference W4A16 module on CPU, M=16) is the named CPU baseline.
 NATIVE_ALWAYS = {"w4a16 M=16": 20.0}   # record -> time budget (s) of its timed native calls
 
 
 def check_record(name, chk, ins, gt):
     """Correctness of the GPU output `chk["y"]` of a record, computed on the same seeded inputs
     `ins` the CPU leg times, against the fp32 ground truth `gt` (the reference op sequence on
-    fp32-upcast inputs, kb_verifier.py:195-196): the BASELINE gate and the grader's allclose, and
+    fp32-upcast inputs, kb_verifier.py:195-196): the benchmark's accuracy gate and the grader's allclose, and
     the bit-exact integer stages where the record has them (the oracle is the checker here)."""
     from kernelbench_harbor_amd import harness
     from oracle import numerics, w4a16 as ow4, w8a8 as ow8
@@ -417,7 +417,7 @@ def cpu_reference(jobs, native_budget_s=1.0, checks=None):
 
 
 def cpu_jobs(ms, with_configs):
-    """The CPU workloads: one per sweep M and one per BASELINE configuration, on the same seeded
+    """The CPU workloads: one per sweep M and one per benchmark configuration, on the same seeded
     inputs the GPU records use (CPU tensors)."""
     import torch
 
@@ -448,7 +448,7 @@ def cpu_jobs(ms, with_configs):
 
 # ---- workloads -------------------------------------------------------------------------------
 def config_table(torch, dev, inputs, ops):
-    """The BASELINE configurations besides the headline sweep: name -> (make the rotated device
+    """The benchmark configurations besides the headline sweep: name -> (make the rotated device
     input sets, the op, algorithmic bytes, flops, MFMA peak, record fields). The qMoE FFN and the
     reference qMoE op hold 757 / 470 MB of weights per set, already larger than the Infinity
     Cache, so they use one set."""
@@ -584,7 +584,7 @@ def vs_torch(torch, dev, inputs, ops, iters=100, warmup=25):
 
 
 def provenance(torch, dev):
-    """Seed, software versions and device of the run (BASELINE.md record fields)."""
+    """Seed, software versions and device of the run (the fields every bench record carries)."""
     p = torch.cuda.get_device_properties(dev)
     return {"seed": 0, "torch": torch.__version__, "hip": torch.version.hip,
             "device": p.name, "arch": getattr(p, "gcnArchName", None),
@@ -757,7 +757,7 @@ def main():
                  "timing": "mean of the HIP-event-bracketed calls of the timed steps, on the "
                            "stream the kernels run on"})
 
-    # ---- the other BASELINE configurations ----
+    # ---- the other benchmark configurations ----
     configs = []
     if not args.no_configs:
         for name, (make, fn, by, fl, peak, extra) in config_table(torch, dev, inputs, ops).items():
@@ -778,7 +778,7 @@ def main():
         "ms_per_step": round(wall / args.steps * 1e3, 4),
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
         "dtype": "f16",
-        "data": "synthetic (seeded; BASELINE distributions; weights rotated to stay HBM-cold)",
+        "data": "synthetic (seeded; the benchmark's distributions; weights rotated to stay HBM-cold)",
         "config": {"workload": "W4A16 g128 GEMM sweep, one call per M per step",
                    "M": ms, "K": K_DIM, "N": N_DIM, "group": GROUP,
                    "qweight_layout": "int32 [K, N/8], 8 nibbles along N",

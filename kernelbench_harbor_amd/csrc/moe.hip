@@ -4,7 +4,7 @@
 //   probs = softmax(fp32(router_logits)); topv, topi = top2(probs); w = dtype(topv / sum(topv))
 //   W_e   = dtype(dtype(qweight[e]) * dtype(scales[e, d/G]))          (int4 values stored int8)
 //   y[t]  = sum_k dtype(dtype(x[t] @ W_{topi[t,k]}) * w[t,k])          (the gather of all_out)
-// SiLU FFN (no reference module, same routing and combine):
+// SiLU FFN (the benchmark's SiLU FFN configuration; no reference module, same routing and combine):
 //   h = dtype(silu(x @ Wg_e) * (x @ Wu_e)),  o = dtype(h @ Wd_e),  y[t] = sum_k dtype(o_k w_k)
 // with W4A16 g128 gate/up/down weights (packed along their output dimension).
 //

@@ -1,4 +1,4 @@
-// MXFP8 block-scaled GEMM on gfx950 scaled MFMA (no reference module:
+// MXFP8 block-scaled GEMM on gfx950 scaled MFMA (the benchmark's MXFP8 configuration; no reference module:
 // the nearest reference math is generate_tasks.py:337-342 (absmax / 448, cast to e4m3fn) and
 // tasks/fp8_microscale/*/environment/reference.py:11 (fp8 decode times scale)).
 //

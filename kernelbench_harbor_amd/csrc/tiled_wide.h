@@ -501,7 +501,7 @@ inline bool plan_wide(int M, int N, int K, int tn, int slab_k, int unroll, int s
   if (N % tn != 0 || K % (unroll * slab_k) != 0 || M < 1) return false;
   const int KT = K / slab_k;
   // Plan for tile height tm; returns the estimated time in units of a third of a 128-row slab
-  // (a 256-row slab measures about 4/3 of a 128-row one, ~1 us at the BASELINE shapes), plus
+  // (a 256-row slab measures about 4/3 of a 128-row one, ~1 us at the benchmark shapes), plus
   // the split-K slices: s slices of M x N 4-byte partial sums are written and read back, about
   // one unit per 2^18 of them (2 MiB of traffic at ~5 TB/s). Without that term the plan chose
   // 56 splits at M=384 (336 MiB of slices).

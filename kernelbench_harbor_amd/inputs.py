@@ -102,7 +102,7 @@ def mx_quantize(src: torch.Tensor):
 
 
 def mxfp8(M: int, K: int = 14336, N: int = 4096, seed: int = 0):
-    """[a, a_scale, b, b_scale] for BASELINE configuration 3: fp32 sources ~ N(0,1), [M, K] and
+    """[a, a_scale, b, b_scale] for the benchmark's MXFP8 configuration: fp32 sources ~ N(0,1), [M, K] and
     [N, K], MX-quantised along K."""
     g = _gen(seed)
     a_src = torch.randn(M, K, generator=g)
@@ -138,7 +138,7 @@ def qmoe(T: int = 256, D: int = 4096, E: int = 8, N: int = 14336,
 def qmoe_ffn(T: int = 512, D: int = 4096, F: int = 14336, E: int = 8, group: int = 128,
              dtype: torch.dtype = torch.float16, seed: int = 0):
     """[x, router_logits, gate_q, gate_s, gate_z, up_q, up_s, up_z, down_q, down_s, down_z] for
-    fp32 logits N(0,1) without top-2 ties, x N(0,1), W4A16 experts
+    the benchmark's SiLU FFN configuration: fp32 logits N(0,1) without top-2 ties, x N(0,1), W4A16 experts
     with scales U[0.002, 0.02] and zero points U{0..15}."""
     g = _gen(seed)
     x = torch.randn(T, D, generator=g).to(dtype)

@@ -48,7 +48,7 @@ class FP8WModel(nn.Module):
 class MXFP8Model(nn.Module):
     """MXFP8 block-scaled GEMM (both operands e4m3, e8m0 1x32 scales), fp16 output.
 
-    No reference module: written in the reference's Model idiom for the BASELINE MXFP8
+    No reference module: written in the reference's Model idiom for the benchmark's MXFP8
     configuration. forward(a [M,K], a_scale [M,K/32], b [N,K], b_scale [N,K/32]) -> [M,N] fp16.
     """
 
@@ -68,7 +68,7 @@ class QMoEModel(nn.Module):
 
 
 class QMoEFFNModel(nn.Module):
-    """Top-2 MoE SiLU FFN with W4A16 g128 experts.
+    """Top-2 MoE SiLU FFN with W4A16 g128 experts (the benchmark's SiLU FFN configuration).
 
     No reference module; written in the reference's Model idiom with its routing and combine:
     forward(x, router_logits, gate_qweight, gate_scales, gate_zeros, up_qweight, up_scales,

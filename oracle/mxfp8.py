@@ -1,7 +1,7 @@
 """Oracle for the MXFP8 block-scaled GEMM (test infrastructure only).
 
 No reference module exists for this configuration; the math follows the OCP MX definition used
-by BASELINE configuration 3 and the reference's FP8 pieces: absmax / 448 and the e4m3fn cast
+by the benchmark's MXFP8 configuration and the reference's FP8 pieces: absmax / 448 and the e4m3fn cast
 (generate_tasks.py:337-342), fp8 decode times scale (tasks/fp8_microscale/*/environment/
 reference.py:11).
 """

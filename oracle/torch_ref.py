@@ -7,7 +7,7 @@ Each function repeats the torch op sequence of one reference ``Model.forward`` (
 function) on tensors of any device, in the dtype of its inputs: called on the task's fp16/bf16 inputs it
 is the reference's native path, called on fp32-upcast floating inputs (integer tensors left
 alone, common/kb_verifier.py:195-196) it is the grader's fp32 ground truth. The two
-BASELINE-only configurations without a reference module (MXFP8, the SiLU FFN) are written in
+Benchmark-only configurations without a reference module (MXFP8, the SiLU FFN) are written in
 the same style from the math their sources define.
 """
 from __future__ import annotations

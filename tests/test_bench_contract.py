@@ -1,5 +1,5 @@
 """bench.py's contract checked on the CPU: the algorithmic byte and FLOP counts it divides by
-(pinned to the figures of the BASELINE configurations) and the single-GPU exit."""
+(pinned to the figures of the benchmark configurations) and the single-GPU exit."""
 import os
 import subprocess
 import sys

@@ -2,7 +2,7 @@
 132-143): for one task of every family at its real layer shape, the drop-in module is graded by
 harness.grade over five fresh input draws against the fp32 ground truth, computed as the grader
 does (the reference op sequence on fp32-upcast inputs; for moe and multi_lora_qgemm the numpy
-oracle), with the BASELINE gate and the family's own metric on every draw; harness.bench then
+oracle), with the benchmark's accuracy gate and the family's own metric on every draw; harness.bench then
 times a module with the grader's 25 warm-up and 100 event-bracketed calls."""
 import math
 
@@ -82,7 +82,7 @@ FUSED_QMOE = [(n, D, E, N, dt) for (n, D, E, N) in (("deepseek_moe", 2048, 64, 1
 @pytest.mark.parametrize("name,D,E,N,dtype", FUSED_QMOE)
 def test_grade_fused_qmoe_tasks(dev, name, D, E, N, dtype):
     """The reference grader's verdict on every fused_qmoe task: five fresh draws, each within the
-    BASELINE gate and the task's allclose(2e-2, 2e-2) against the ground truth the grader
+    benchmark accuracy gate and the task's allclose(2e-2, 2e-2) against the ground truth the grader
     computes (the reference forward on fp32-upcast inputs on the device). The reference's own
     bf16 path fails that allclose on these shapes; the drop-in's fp32 evaluation does not."""
     print(f"[grade qmoe] {name} {dtype}", flush=True)

@@ -1,6 +1,6 @@
 """GPU parity of the multi-LoRA quantized linear (kbh_lora_qgemm) against the CPU oracle
 (oracle/lora.py): the reference's six tasks at their real shapes (generate_tasks.py:427-431,
-632-638: T=64, three adapter configurations x fp16/bf16) and ragged cases to the BASELINE
+632-638: T=64, three adapter configurations x fp16/bf16) and ragged cases to the benchmark's
 tolerance against the fp32 ground truth, and one-hot activations with dyadic adapters (every
 sum exact in fp32) bit-exactly against the oracle's native-dtype path, which checks each
 rounding: dequantised weight, base, shrink, expand and the final add."""

@@ -1,5 +1,5 @@
 """GPU parity of the top-k fp16/bf16 MoE (kbh_moe, kbh_moe_route_topk) against the CPU oracle
-(oracle/moe.py): routing ids exactly, weights within one ulp; outputs to the BASELINE tolerance
+(oracle/moe.py): routing ids exactly, weights within one ulp; outputs to the benchmark's tolerance
 against the fp32 ground truth; one-hot activations bit-exact against the oracle's native-dtype
 path; and every task of the reference generator's moe family at its real shape
 (generate_tasks.py:189-195, 552-553: five layers x T in {16, 128, 512} fp16 plus T=512 bf16),

@@ -51,7 +51,7 @@ def test_mxfp8_e8m0_decode_bit_exact(dev, M, N):
 
 @pytest.mark.parametrize("M", [128, 2048])
 def test_mxfp8_full_size(dev, M):
-    """M in {128, 2048}, K=14336, N=4096."""
+    """The benchmark's MXFP8 configuration: M in {128, 2048}, K=14336, N=4096."""
     print(f"[mxfp8 full] M={M}", flush=True)
     a, sa, b, sb = inputs.mxfp8(M, 14336, 4096, seed=M)
     y = MXFP8Model()(a.to(dev), sa.to(dev), b.to(dev), sb.to(dev))

@@ -189,7 +189,7 @@ def test_qmoe_ffn_tile_overflow_rows(dev, F, dtype):
 
 
 def test_qmoe_ffn_full_size_all_experts(dev):
-    """BASELINE configuration 4 (T=512, D=4096, F=14336, E=8): the whole layer runs on the GPU;
+    """The benchmark's SiLU FFN configuration (T=512, D=4096, F=14336, E=8): the whole layer runs on the GPU;
     the oracle checks every token (so all eight experts' gate, up and down matrices) on two
     256-column slices of the output, the first and the last."""
     print("[qmoe ffn full]", flush=True)

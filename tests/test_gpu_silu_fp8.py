@@ -5,7 +5,7 @@ the CPU oracle (oracle/silu_fp8.py).
   gate * up is exact and every later step is exactly rounded: codes, scales and outputs must be
   bit-identical, including crafted values on and between e4m3 grid points (ties to even).
 * The reference's task grid (generate_tasks.py:351-355, 610-614; N(0,1) inputs): the SiLU's
-  exp differs from numpy's by a few ulp, so outputs are compared to the BASELINE tolerance and
+  exp differs from numpy's by a few ulp, so outputs are compared to the benchmark's tolerance and
   the reference's own cosine / relative-L1 gate (common/kb_verifier.py:172-176), and at least
   99.9% of the e4m3 codes must be identical.
 """

@@ -10,7 +10,7 @@ last 256 columns):
 * "plain": grid % 8 != 0, the sum falls back to linear indexing.
 
 W8A8's raw int32 accumulators are compared bit for bit with an int64 matmul; the fp16/bf16
-GEMMs within the BASELINE tolerance of the oracle, and repeated calls must agree bit for bit."""
+GEMMs within the benchmark's tolerance of the oracle, and repeated calls must agree bit for bit."""
 import numpy as np
 import pytest
 import torch

@@ -9,7 +9,7 @@ its three configurations in fp16 and bf16 (generate_tasks.py:390-394, 617-626; T
 
 The GEMMs are checked against the oracle on the first and last 256 output columns (the oracle's
 dense fp32 dequantisation of a 70B-model layer would dominate the suite's time; both slices
-cross every K split and group); W8A8 bit-exactly, the others to the BASELINE tolerances and to
+cross every K split and group); W8A8 bit-exactly, the others to the benchmark's tolerances and to
 the reference grader's own allclose(atol = rtol = 2e-2) on every task, bf16 included (the
 reference's own bf16 intermediates fail that allclose on the bf16 W4A16 and qMoE tasks; these
 kernels scale after the MFMA and combine in fp32, so they stay inside it). The qMoE output is

@@ -77,7 +77,7 @@ def test_w4a16_parity(dev, M, K, N, group, dtype, dist):
 
 @pytest.mark.parametrize("M", [1, 4, 16])
 def test_w4a16_full_size_decode(dev, M):
-    """BASELINE configs 0/1 shape: K=14336, N=4096, g128, fp16."""
+    """The benchmark's W4A16 shape: K=14336, N=4096, g128, fp16."""
     print(f"[w4a16 full] M={M}", flush=True)
     x, qw, s, z = inputs.w4a16(M, 14336, 4096, 128, torch.float16, seed=M)
     y = W4A16Model()(x.to(dev), qw.to(dev), s.to(dev), z.to(dev))
@@ -128,7 +128,7 @@ def test_w4a16_dequant_bit_exact(dev, dtype, M, N, zeros):
 
 @pytest.mark.parametrize("M", [64, 256, 1024])
 def test_w4a16_full_size_sweep_points(dev, M):
-    """The remaining BASELINE config 1 sweep points at K=14336, N=4096, g128 (64-row tiles with
+    """The remaining points of the benchmark's W4A16 sweep at K=14336, N=4096, g128 (64-row tiles with
     many K splits, 256-row tiles, split-K 256-row tiles), checked against the oracle on the first
     and last 256 output columns (every K split and group crosses both)."""
     print(f"[w4a16 full] M={M}", flush=True)
@@ -141,7 +141,7 @@ def test_w4a16_full_size_sweep_points(dev, M):
 
 
 def test_w4a16_full_size_prefill(dev):
-    """BASELINE config 1 largest point: M=2048, K=14336, N=4096."""
+    """The largest point of the benchmark's W4A16 sweep: M=2048, K=14336, N=4096."""
     print("[w4a16 full] M=2048", flush=True)
     x, qw, s, z = inputs.w4a16(2048, 14336, 4096, 128, torch.float16, seed=5)
     y = W4A16Model()(x.to(dev), qw.to(dev), s.to(dev), z.to(dev))

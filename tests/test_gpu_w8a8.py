@@ -46,7 +46,7 @@ def test_w8a8_bit_exact(dev, M, K, N, dist):
 
 @pytest.mark.parametrize("M", [16, 512])
 def test_w8a8_full_size(dev, M):
-    """SmoothQuant inputs at M in {16, 512}, K=14336, N=4096."""
+    """The benchmark's W8A8 configuration: SmoothQuant inputs at M in {16, 512}, K=14336, N=4096."""
     print(f"[w8a8 full] M={M}", flush=True)
     x, w, xs, ws = inputs.w8a8(M, 14336, 4096, seed=M)
     y = W8A8Model()(x.to(dev), w.to(dev), xs.to(dev), ws.to(dev))
