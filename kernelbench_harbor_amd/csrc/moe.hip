@@ -241,6 +241,53 @@ struct F16SlabPolicy {
 };
 static_assert(32 * kBnPitch == 128 * TLD, "an N-major slab uses the buffer of a k-major one");
 
+// Weight producer of the warp-specialised kernel (tiled_ws.h) for fp16/bf16 weights [E][K][N]
+// (N contiguous): thread t loads 4 rows (K) x 8 columns (16 bytes per row) of a 32 x 256 slab
+// and writes each column's 4 values as one 8-byte piece of the K-contiguous operand layout
+// (wide_b_offset), pairing the 16-bit halves of two rows with one v_perm_b32 per dword; the
+// thread map (column block cb, row block rb) is the int8 producer's.
+struct F16WidePolicy {
+  static constexpr int kTN = 256;
+  static constexpr bool kHasFast = false;
+  const uint16_t* w;
+  int N;
+  size_t w_stride;
+  struct Raw {
+    kbh_u32x4 r[4];
+  };
+  struct Grp {};
+  struct ScanPre {};
+  __device__ F16WidePolicy at_expert(int e) const {
+    F16WidePolicy p = *this;
+    p.w += (size_t)e * w_stride;
+    return p;
+  }
+  __device__ static int cb_of(int t) { return (t & 7) | (((t >> 4) & 3) << 3); }
+  __device__ static int rb_of(int t) { return ((t >> 3) & 1) | ((t >> 6) << 1); }
+  __device__ void load(Raw& r, int k0, int n0, int t) const {
+    const uint16_t* p = w + (size_t)(k0 + 4 * rb_of(t)) * N + n0 + 8 * cb_of(t);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) r.r[i] = *reinterpret_cast<const kbh_u32x4*>(p + (size_t)i * N);
+  }
+  __device__ void load_group(Grp&, int, int, int) const {}
+  template <bool FAST>
+  __device__ void prepare_group(Grp&) const {}
+  template <bool FAST>
+  __device__ void store_all(const Raw& r, const Grp&, uint8_t* Bs, int t) const {
+    const int cb = cb_of(t), rb = rb_of(t);
+    // wide_b_offset<256>(8 rb, 8 cb + c) = base + 16 (c ^ fw)
+    uint8_t* base = Bs + wide_b_offset<256>(8 * rb, 8 * cb) - wide_slot(8 * cb) * 16 + cb * 128;
+    const int fw = (cb ^ (cb >> 3)) & 7;
+#pragma unroll
+    for (int c = 0; c < 8; ++c) {
+      const uint32_t sel = (c & 1) ? 0x07060302u : 0x05040100u;  // high or low halves
+      const uint32_t d0 = __builtin_amdgcn_perm(r.r[1][c >> 1], r.r[0][c >> 1], sel);
+      const uint32_t d1 = __builtin_amdgcn_perm(r.r[3][c >> 1], r.r[2][c >> 1], sel);
+      *reinterpret_cast<kbh_u32x2*>(base + ((c ^ fw) << 4)) = kbh_u32x2{d0, d1};
+    }
+  }
+};
+
 // Policies without kNMajor store k-major slabs (Bs[tld_row(n) * TLD + k]).
 template <class BP, class = void>
 struct NMajor {
@@ -1100,6 +1147,35 @@ extern "C" int kbh_moe(const void* x, const void* w, const void* router_logits, 
   const F16SlabPolicy bp{(const uint16_t*)w, H, (size_t)D * H};
   const size_t n4 = (size_t)T * H / 4;
   const dim3 cgrid((unsigned)((n4 + 255) / 256));
+  const size_t S = (size_t)T * topk;
+  // Experts averaging 96 or more routed rows: 128-row expert tiles of 256 columns on the
+  // warp-specialised kernel (x staged through LDS, 32-bit offsets; bit-identical to the grouped
+  // kernel). Measured at T=512 (graph-replayed): grok1 295 -> 275 us, mixtral 411 -> 409; at 64
+  // rows per expert (qwen2_57b top-8) 313 -> 324, so those stay on the grouped kernel.
+  if (L.bm == 128 && S >= (size_t)96 * E && H % 256 == 0 && D % 128 == 0 &&
+      S * D * 2 < ((size_t)1 << 31)) {
+    const F16WidePolicy wp{(const uint16_t*)w, H, (size_t)D * H};
+    using RM = GroupedRows<true, true>;
+    const RM rm{mb.tiles, mb.perm, topk};
+    const dim3 grid((unsigned)(L.max_tiles * (H / 256)));
+    if (bf)
+      hipLaunchKernelGGL((tiled_ws_gemm<WideHalf<true>, 128, 2, 1, F16WidePolicy, HalfOut<true>, RM,
+                                        4, 1, true>),
+                         grid, dim3(512), 0, st, x, wp, HalfOut<true>{(uint16_t*)o, H},
+                         (float*)nullptr, (int)S, H, D, 1, D / 32, rm);
+    else
+      hipLaunchKernelGGL((tiled_ws_gemm<WideHalf<false>, 128, 2, 1, F16WidePolicy, HalfOut<false>,
+                                        RM, 4, 1, true>),
+                         grid, dim3(512), 0, st, x, wp, HalfOut<false>{(uint16_t*)o, H},
+                         (float*)nullptr, (int)S, H, D, 1, D / 32, rm);
+    if (bf)
+      hipLaunchKernelGGL(moe_combine_k_kernel<true>, cgrid, dim3(256), 0, st, (const uint16_t*)o,
+                         mb.topw, (uint16_t*)y, T, H, topk);
+    else
+      hipLaunchKernelGGL(moe_combine_k_kernel<false>, cgrid, dim3(256), 0, st, (const uint16_t*)o,
+                         mb.topw, (uint16_t*)y, T, H, topk);
+    return launch_status();
+  }
   if (bf) {
     launch_moe_gemm<true, F16SlabPolicy, true, false, true>(L, x, D, mb, bp, bp, o, H, H, D, st);
     hipLaunchKernelGGL(moe_combine_k_kernel<true>, cgrid, dim3(256), 0, st, (const uint16_t*)o,

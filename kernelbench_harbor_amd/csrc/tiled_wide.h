@@ -114,12 +114,13 @@ struct DenseRows {
   __device__ int out_row(const Tile& ti, int r) const { return ti.m0 + r; }
 };
 
-// Tile mb of the table {expert, first slot, rows}; slot s reads x row perm[s] >> 1 (GATHER) or
-// row s, and writes output row perm[s] (PERM_OUT) or row s.
+// Tile mb of the table {expert, first slot, rows}; slot s reads x row perm[s] / topk (GATHER;
+// perm[s] = topk * token + k) or row s, and writes output row perm[s] (PERM_OUT) or row s.
 template <bool GATHER, bool PERM_OUT>
 struct GroupedRows {
   const int* tiles;
   const int* perm;
+  int topk = 2;
   struct Tile {
     int s0, rows, expert;
   };
@@ -129,7 +130,7 @@ struct GroupedRows {
   }
   __device__ int a_row(const Tile& ti, int r) const {
     const int s = ti.s0 + min(r, ti.rows - 1);
-    return GATHER ? (perm[s] >> 1) : s;
+    return GATHER ? (topk == 2 ? (perm[s] >> 1) : perm[s] / topk) : s;
   }
   __device__ int out_row(const Tile& ti, int r) const {
     const int s = ti.s0 + r;

@@ -40,6 +40,10 @@ CASES = [
     (300, 512, 8, 256, 2, torch.bfloat16),
     (1, 128, 4, 128, 1, torch.float16),
     (250, 384, 16, 640, 8, torch.float16),   # > 48 rows per expert: 128-row tiles
+    # >= 96 rows per expert, N a multiple of 256: the warp-specialised kernel
+    (420, 512, 8, 512, 2, torch.float16),
+    (400, 256, 4, 256, 2, torch.bfloat16),
+    (120, 256, 4, 512, 4, torch.float16),    # top-4: x rows gathered as perm / 4
     (5, 128, 256, 128, 8, torch.float16),    # the largest expert count
     (1, 256, 64, 256, 8, torch.bfloat16),    # one token, eight experts
 ]
