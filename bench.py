@@ -704,17 +704,12 @@ def main():
     # Calls from the largest M down: the host issues the small calls while the large ones run,
     # so no kernel waits for the host's per-call work (the same calls in any order).
     order = sorted(ms, reverse=True)
-    # The timed steps bracket only the dominant launch (the largest M: the most FLOPs and time
-    # of a step) with HIP events, for the roofline; an event pair around every call added ~5 us
-    # per call to a step (0.560 against 0.527-0.531 ms), so every M's calls are event-timed in
-    # untimed steps after them (us_step_mean).
-    Md = max(ms)
 
-    def step(rec, only=None):
+    def step(rec):
         for M in order:
             i = calls[M] % len(sets[M])
             calls[M] += 1
-            if rec and (only is None or M == only):
+            if rec:
                 a = torch.cuda.Event(enable_timing=True)
                 b = torch.cuda.Event(enable_timing=True)
                 a.record()
@@ -731,18 +726,13 @@ def main():
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for _ in range(args.steps):
-        step(True, Md)
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
-    dom = [a.elapsed_time(b) * 1e-3 for a, b in ev[Md]]
-    ev = {M: [] for M in ms}
-    for _ in range(args.steps):
         step(True)
     torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
 
     sweep, step_flops, mean_s, checks = [], 0, {}, {}
     for M in ms:
-        ts = dom if M == Md else [a.elapsed_time(b) * 1e-3 for a, b in ev[M]]
+        ts = sorted(a.elapsed_time(b) * 1e-3 for a, b in ev[M])
         mean_s[M] = sum(ts) / len(ts)
         grader, batched = time_config(torch, ops.w4a16_gemm, sets[M])
         sweep.append(record(f"w4a16 M={M}", grader, batched, w4a16_bytes(M), gemm_flops(M),
@@ -754,6 +744,8 @@ def main():
     del sets
     torch.cuda.empty_cache()
 
+    # Dominant launch of a step: the M whose calls take the most time.
+    Md = max(ms, key=lambda m: mean_s[m])
     d = next(r for r in sweep if r["M"] == Md)
     if d["bound"] == "hbm":
         ach = d["bytes"] / mean_s[Md] / 1e9
